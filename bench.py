@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Benchmark: fused paged-attention decode on one MI355X.
+
+One "step" = one decode-attention call over the whole batch (one layer) of the
+Qwen3-8B-shaped GQA workload (B=32, Hq=32, Hkv=8, D=128, BS=128, context
+lengths U[1024, 8192], seeded), inputs resident in HBM. Prints ONE JSON line:
+value = algorithmic KV-read GB/s (K+V of valid tokens + Q + out + tables,
+divided by the kernel time), plus µs/step, the roofline of the kernel and the
+CPU baseline (the C restatement of the reference kernels, timed on the host).
+
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline]
+
+Only one GPU is used; --gpus N with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+DEFAULT_CONFIG = "cfg2_qwen3_8b"
+METRIC = "decode-attn KV-read GB/s (Qwen3-8B GQA decode, bs=32)"
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default=DEFAULT_CONFIG)
+    p.add_argument("--blocks-per-split", type=int, default=0, help="0 = automatic split plan")
+    p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample duration")
+    p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
+    p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
+                   help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
+    return p.parse_args()
+
+
+def cpu_baseline(case, args) -> dict | None:
+    """Time the C restatement of the reference kernels on this host (kind "port")."""
+    try:
+        import numpy as np
+
+        from oracle import pa_oracle_c
+        from simpler_amd.workloads import algorithmic_bytes
+    except Exception as e:  # pragma: no cover - reported, never fatal
+        return {"value": None, "error": f"oracle unavailable: {e}"}
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    c = case.config
+
+    def bits(t):
+        return t.contiguous().view(__import__("torch").int16).numpy().view(np.uint16)
+
+    q, k = bits(case.query), bits(case.key_cache)
+    v = None if c.mla else bits(case.value_cache)
+    bt, cl = case.block_table.numpy(), case.context_lens.numpy()
+    out = np.zeros((c.batch, c.q_len, c.num_heads, c.head_dim_v), dtype=np.float32)
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        pa_oracle_c.decode(q, k, v, bt, cl, case.scale, causal=c.causal, v_dim=c.head_dim_v if c.mla else None,
+                           n_threads=threads, out=out)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or runs >= 1000:
+            break
+    per_step = el / runs
+    nbytes = algorithmic_bytes(case, out_bytes=2 if args.out_dtype == "bf16" else 4)
+    return {
+        "value": round(nbytes / per_step / 1e9, 3),
+        "unit": "GB/s",
+        "us_per_step": round(per_step * 1e6, 1),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full {c.name} decode step (all {c.batch}x{c.kv_heads} sequence/kv-head items), "
+                  f"{runs} repetitions in {el:.1f} s, C restatement of the reference QK/SF/PV/UP kernels "
+                  f"(oracle/pa_oracle.c), {threads} pthreads",
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by batch / kv head with no exchange, see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from simpler_amd import paged_attention as pa
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, algorithmic_flops, kv_bytes, make_case
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    print(f"[bench] generating {cfg.name}: {cfg.description}", file=sys.stderr, flush=True)
+    case_cpu = make_case(cfg)
+    case = case_cpu.to(dev)
+    out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
+    out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
+    pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
+                         case.scale, causal=cfg.causal, blocks_per_split=args.blocks_per_split)
+    bps, max_splits = pa.plan(pargs)
+    stream = torch.cuda.current_stream(dev)
+
+    print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    pa.check_errors(dev)
+
+    # timed region: K back-to-back launches on the stream the kernel runs on
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    kernel_ms = start.elapsed_time(end) / args.steps
+    print(f"[bench] timed {args.steps} steps: {kernel_ms * 1e3:.1f} us/step (events), wall {wall:.3f} s",
+          file=sys.stderr, flush=True)
+
+    out_bytes = 2 if out_dtype == torch.bfloat16 else 4
+    nbytes = algorithmic_bytes(case_cpu, out_bytes=out_bytes)
+    gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+    flops = algorithmic_flops(case_cpu)
+    traffic = None
+    tf = Path(args.traffic_file)
+    if tf.exists():
+        try:
+            t = json.loads(tf.read_text()).get(cfg.name)
+            traffic = t.get("hbm_bytes_per_launch") if isinstance(t, dict) else None
+        except Exception:
+            traffic = None
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(kernel_ms, 5),
+        "us_per_step": round(kernel_ms * 1e3, 2),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name}: {cfg.description}",
+            "seed": case_cpu.seed,
+            "batch": cfg.batch,
+            "q_len": cfg.q_len,
+            "num_heads": cfg.num_heads,
+            "kv_heads": cfg.kv_heads,
+            "head_dim": [cfg.head_dim_k, cfg.head_dim_v],
+            "block_size": cfg.block_size,
+            "context_tokens": int(case_cpu.context_lens.sum()),
+            "out_dtype": args.out_dtype,
+            "blocks_per_split": bps,
+            "max_splits": max_splits,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": nbytes,
+            "kv_bytes": kv_bytes(case_cpu),
+            "kernel": "pa_decode_splitk_kernel",
+            "tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,118 @@
+/*
+ * simpler_hip — paged-attention decode entry points of libsimpler_hip.so.
+ *
+ * These replace the work that simpler's orchestration function
+ * `aicpu_orchestration_entry` submits as four AICore tasks (QK, SF, PV, UP)
+ * per KV block (reference: examples/a2a3/tensormap_and_ringbuffer/
+ * paged_attention/kernels/orchestration/paged_attention_orch.cpp:77-291).
+ * The argument meaning follows that function's 7-argument contract
+ * (:94-102): query, key_cache, value_cache, block_table, context_lens, out,
+ * scale. Here the whole chain is one fused split-K gfx950 kernel.
+ *
+ * Plain C ABI: device pointers, sizes and an opaque HIP stream (hipStream_t
+ * passed as void*; NULL = the null stream). No torch types.
+ */
+#ifndef SIMPLER_HIP_PA_DECODE_H
+#define SIMPLER_HIP_PA_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#pragma GCC visibility push(default)
+
+/* Error codes (0 = success, negative = error; same convention as the reference
+ * C API, src/common/worker/pto_runtime_c_api.h:50,73-83). */
+enum {
+    SIMPLER_HIP_OK = 0,
+    SIMPLER_HIP_ERR_INVALID = -1,     /* bad shape / dtype / argument          */
+    SIMPLER_HIP_ERR_UNSUPPORTED = -2, /* == PTO_RUNTIME_ERR_UNSUPPORTED         */
+    SIMPLER_HIP_ERR_WORKSPACE = -4,   /* workspace missing or too small         */
+    SIMPLER_HIP_ERR_LAUNCH = -5,      /* HIP launch / runtime failure           */
+    SIMPLER_HIP_ERR_BAD_BLOCK = -6,   /* block_table entry outside the KV pool  */
+};
+
+/* Output dtypes, using the reference's DataType codes
+ * (src/common/task_interface/data_type.h:47-67). */
+enum { SIMPLER_HIP_DT_FLOAT32 = 0, SIMPLER_HIP_DT_FLOAT16 = 1, SIMPLER_HIP_DT_BFLOAT16 = 6 };
+
+/*
+ * One paged-attention decode call. All pointers are device pointers.
+ *
+ * query        bf16 [batch, q_len, num_heads, head_dim_k]   (q_len = 1: [batch, num_heads, Dk])
+ * key_cache    bf16, element (blk, t, kvh, d) at
+ *              blk*k_block_stride + t*k_token_stride + kvh*k_head_stride + d
+ *              (contiguous BSND [num_blocks, block_size, kv_heads, Dk]:
+ *               strides BS*Hkv*Dk, Hkv*Dk, Dk)
+ * value_cache  bf16, same addressing with the v_* strides and Dv columns.
+ *              MLA: value_cache == key_cache with the K strides and Dv <= Dk
+ *              (V is the first Dv columns of K).
+ * block_table  int32 [batch, max_blocks_per_seq], entries in [0, num_blocks)
+ * context_lens int32 [batch], 0 <= len <= max_blocks_per_seq*block_size
+ * out          [batch, q_len, num_heads, Dv] of out_dtype (FLOAT32 or BFLOAT16)
+ * scale        softmax scale applied to q.k in fp32
+ * causal       q_len > 1 only: query token i sees context_len - (q_len-1-i) tokens
+ */
+typedef struct SimplerHipPaDecodeArgs {
+    const void *query;
+    const void *key_cache;
+    const void *value_cache;
+    const int32_t *block_table;
+    const int32_t *context_lens;
+    void *out;
+    int64_t k_block_stride, k_token_stride, k_head_stride;
+    int64_t v_block_stride, v_token_stride, v_head_stride;
+    int32_t batch;
+    int32_t q_len;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim_k;
+    int32_t head_dim_v;
+    int32_t block_size;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    int32_t out_dtype;
+    float scale;
+    int32_t causal;
+    /* 0 = automatic split plan; > 0 forces KV blocks per split (tuning). */
+    int32_t blocks_per_split;
+    int32_t reserved;
+} SimplerHipPaDecodeArgs;
+
+/* Bytes of device workspace simpler_hip_pa_decode needs for these args
+ * (split partials + self-resetting counters + error word). */
+size_t simpler_hip_pa_decode_workspace_size(const SimplerHipPaDecodeArgs *args);
+
+/* Zero a freshly allocated workspace (counters must start at zero; the kernel
+ * leaves them at zero again after every call). Enqueued on `stream`. */
+int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Enqueue the fused decode kernel on `stream`. `workspace` must be at least
+ * simpler_hip_pa_decode_workspace_size(args) bytes, initialised once with
+ * simpler_hip_pa_decode_workspace_init, and not shared by calls that may run
+ * concurrently. Returns 0 or a negative SIMPLER_HIP_ERR_* code (shape and dtype
+ * checks happen on the host before anything is launched).
+ */
+int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/* After the stream has completed: returns SIMPLER_HIP_ERR_BAD_BLOCK if any
+ * launch since the last check met an out-of-pool block_table entry (such
+ * blocks are skipped, never dereferenced), else 0. Clears the flag. Synchronous. */
+int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream);
+
+/* Kernel-only helpers for measurement: name of the kernel instantiation the
+ * args select, and the split plan (blocks per split, max splits). */
+const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args);
+int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *blocks_per_split, int32_t *max_splits);
+
+#pragma GCC visibility pop
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIMPLER_HIP_PA_DECODE_H */

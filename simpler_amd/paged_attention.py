@@ -1,0 +1,239 @@
+"""Paged-attention decode on the HIP backend, for torch device tensors.
+
+This is the direct form of the path that simpler submits through its
+orchestration function (``examples/a2a3/tensormap_and_ringbuffer/
+paged_attention/kernels/orchestration/paged_attention_orch.cpp:77-291``): the
+same seven arguments — query, key_cache, value_cache, block_table,
+context_lens, out, scale — in the same layouts (``goldens/paged_attention.py
+:76-84``), computed by one fused split-K gfx950 kernel in ``libsimpler_hip.so``.
+
+torch supplies device memory and the current stream only; the arithmetic is
+all in the native library, and there is no fallback when it is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import threading
+
+import torch
+
+from . import _lib
+from .task_interface import ArgDirection, ChipCallable, CoreCallable, DataType
+
+NATIVE_CALLABLE_NAME = "simpler_hip_paged_attention_decode"
+
+_OUT_DTYPES = {torch.float32: int(DataType.FLOAT32), torch.bfloat16: int(DataType.BFLOAT16)}
+_ERRORS = {
+    -1: "invalid argument (shape, dtype, stride or alignment)",
+    -2: "unsupported configuration",
+    -4: "workspace missing or too small",
+    -5: "HIP launch failure",
+    -6: "block_table entry outside the KV pool",
+}
+
+
+class PagedAttentionError(RuntimeError):
+    def __init__(self, rc: int, what: str = "simpler_hip_pa_decode"):
+        super().__init__(f"{what} failed with {rc}: {_ERRORS.get(rc, 'error')}")
+        self.rc = rc
+
+
+class _Workspace:
+    """Grow-only per-device workspace (split partials + self-resetting counters)."""
+
+    def __init__(self) -> None:
+        self._mu = threading.Lock()
+        self._buf: dict[int, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int, stream: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        with self._mu:
+            buf = self._buf.get(idx)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                buf = torch.empty(size + 256, dtype=torch.uint8, device=device)
+                off = (-buf.data_ptr()) % 256
+                buf = buf[off : off + size]
+                rc = _lib.lib().simpler_hip_pa_decode_workspace_init(buf.data_ptr(), buf.numel(), stream)
+                if rc != 0:
+                    raise PagedAttentionError(rc, "simpler_hip_pa_decode_workspace_init")
+                self._buf[idx] = buf
+            return buf
+
+
+_WORKSPACE = _Workspace()
+
+
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype, ndims: tuple[int, ...]) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device (cuda/HIP) tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.dim() not in ndims:
+        raise ValueError(f"{name} must have {ndims} dims, got shape {tuple(t.shape)}")
+
+
+def make_args(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    out: torch.Tensor,
+    scale: float,
+    *,
+    causal: bool = False,
+    blocks_per_split: int = 0,
+) -> _lib.PaDecodeArgs:
+    """Validate torch tensors and fill the C ``SimplerHipPaDecodeArgs``."""
+    _check(query, "query", torch.bfloat16, (3, 4))
+    _check(key_cache, "key_cache", torch.bfloat16, (4,))
+    _check(value_cache, "value_cache", torch.bfloat16, (4,))
+    _check(block_table, "block_table", torch.int32, (2,))
+    _check(context_lens, "context_lens", torch.int32, (1,))
+    if out.dtype not in _OUT_DTYPES:
+        raise ValueError(f"out must be float32 or bfloat16, got {out.dtype}")
+    for name, t in (("query", query), ("block_table", block_table), ("context_lens", context_lens), ("out", out)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if key_cache.stride(-1) != 1 or value_cache.stride(-1) != 1:
+        raise ValueError("key_cache/value_cache need unit stride in the head dim")
+    q4 = query.dim() == 4
+    batch = query.shape[0]
+    q_len = query.shape[1] if q4 else 1
+    hq, dk = query.shape[-2], query.shape[-1]
+    nblk, bs, hkv, kd = key_cache.shape
+    vnb, vbs, vhkv, dv = value_cache.shape
+    if (vnb, vbs, vhkv) != (nblk, bs, hkv) or kd != dk:
+        raise ValueError("key_cache/value_cache/query shapes disagree")
+    expect_out = (batch, q_len, hq, dv) if q4 else (batch, hq, dv)
+    if tuple(out.shape) != expect_out:
+        raise ValueError(f"out must have shape {expect_out}, got {tuple(out.shape)}")
+    if tuple(block_table.shape[:1]) != (batch,) or tuple(context_lens.shape) != (batch,):
+        raise ValueError("block_table/context_lens batch does not match the query")
+    a = _lib.PaDecodeArgs()
+    a.query = query.data_ptr()
+    a.key_cache = key_cache.data_ptr()
+    a.value_cache = value_cache.data_ptr()
+    a.block_table = block_table.data_ptr()
+    a.context_lens = context_lens.data_ptr()
+    a.out = out.data_ptr()
+    a.k_block_stride, a.k_token_stride, a.k_head_stride = key_cache.stride()[:3]
+    a.v_block_stride, a.v_token_stride, a.v_head_stride = value_cache.stride()[:3]
+    a.batch, a.q_len, a.num_heads, a.num_kv_heads = batch, q_len, hq, hkv
+    a.head_dim_k, a.head_dim_v, a.block_size = dk, dv, bs
+    a.max_blocks_per_seq, a.num_blocks = block_table.shape[1], nblk
+    a.out_dtype = _OUT_DTYPES[out.dtype]
+    a.scale = float(scale)
+    a.causal = 1 if causal else 0
+    a.blocks_per_split = int(blocks_per_split)
+    return a
+
+
+def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = None) -> None:
+    """Enqueue one decode on ``stream`` (default: torch's current stream)."""
+    lib = _lib.lib()
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    need = lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(args))
+    if need == 0:
+        raise PagedAttentionError(-1)
+    ws = _WORKSPACE.get(device, need, stream)
+    rc = lib.simpler_hip_pa_decode(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream)
+    if rc != 0:
+        raise PagedAttentionError(rc)
+
+
+def paged_attention_decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    out: torch.Tensor | None = None,
+    scale: float | None = None,
+    *,
+    causal: bool = False,
+    out_dtype: torch.dtype = torch.float32,
+    blocks_per_split: int = 0,
+) -> torch.Tensor:
+    """Fused paged-attention decode; returns ``out`` ``[B, (q_len,) Hq, Dv]``.
+
+    ``scale`` defaults to ``1/sqrt(head_dim_k)``. The reference's orchestration
+    writes FLOAT32 output (``paged_attention_orch.cpp:130``); BFLOAT16 is also
+    accepted. ``value_cache`` may be a view of ``key_cache`` (MLA: V = K[..., :Dv]).
+    """
+    if scale is None:
+        scale = 1.0 / math.sqrt(query.shape[-1])
+    if out is None:
+        shape = (*query.shape[:-1], value_cache.shape[-1])
+        out = torch.empty(shape, dtype=out_dtype, device=query.device)
+    args = make_args(
+        query, key_cache, value_cache, block_table, context_lens, out, scale,
+        causal=causal, blocks_per_split=blocks_per_split,
+    )
+    launch(args, query.device)
+    return out
+
+
+def check_errors(device: torch.device | None = None) -> None:
+    """Synchronise and raise if a launch met an out-of-pool block_table entry."""
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ws = _WORKSPACE.get(device, 1, stream)
+    rc = _lib.lib().simpler_hip_pa_decode_check(ws.data_ptr(), ws.numel(), stream)
+    if rc != 0:
+        raise PagedAttentionError(rc, "paged attention")
+
+
+def plan(args: _lib.PaDecodeArgs) -> tuple[int, int]:
+    """(KV blocks per split, max splits) the launcher picks for ``args``."""
+    bps, ms = ctypes.c_int32(), ctypes.c_int32()
+    rc = _lib.lib().simpler_hip_pa_decode_plan(ctypes.byref(args), ctypes.byref(bps), ctypes.byref(ms))
+    if rc != 0:
+        raise PagedAttentionError(rc, "simpler_hip_pa_decode_plan")
+    return bps.value, ms.value
+
+
+# ---------------------------------------------------------------------------
+# Callables accepted by libsimpler_hip.so's simpler_register_callable
+# ---------------------------------------------------------------------------
+
+D = ArgDirection
+ORCH_SIGNATURE = [D.IN, D.IN, D.IN, D.IN, D.IN, D.OUT]
+INCORE_SIGNATURES = {
+    0: [D.IN, D.IN, D.OUT],  # QK   aic_qk_matmul
+    1: [D.IN, D.OUT, D.OUT, D.OUT],  # SF   aiv_softmax_prepare
+    2: [D.IN, D.IN, D.OUT],  # PV   aic_pv_matmul
+    3: [D.IN, D.IN, D.IN, D.INOUT, D.INOUT, D.INOUT, D.INOUT],  # UP aiv_online_update
+}
+
+
+def reference_chain_callable(orch_binary: bytes = b"", incore_binaries: dict[int, bytes] | None = None) -> ChipCallable:
+    """The reference's paged-attention CALLABLE (test_paged_attention.py:25-61).
+
+    Orchestration ``aicpu_orchestration_entry`` with the QK/SF/PV/UP incores at
+    func ids 0..3. The binaries are carried but not executed: the HIP backend
+    recognises the chain by its signatures and runs the fused kernel.
+    """
+    incore_binaries = incore_binaries or {}
+    children = [
+        (fid, CoreCallable.build(signature=sig, binary=incore_binaries.get(fid, b"")))
+        for fid, sig in INCORE_SIGNATURES.items()
+    ]
+    return ChipCallable.build(
+        signature=ORCH_SIGNATURE,
+        func_name="aicpu_orchestration_entry",
+        binary=orch_binary,
+        children=children,
+        config_name="aicpu_orchestration_config",
+    )
+
+
+def native_callable() -> ChipCallable:
+    """A callable that names the fused decode directly."""
+    return ChipCallable.build(signature=ORCH_SIGNATURE, func_name=NATIVE_CALLABLE_NAME, binary=b"", children=[])

@@ -1,0 +1,212 @@
+"""Synthetic paged-attention decode workloads (seeded), plus their roofline figures.
+
+Plays the role of the reference's input generator
+(``simpler_setup/goldens/paged_attention.py:30-88``): query/K/V in the same
+layouts — query ``[B, Hq, D]`` (``[B, q_len, Hq, D]`` for multi-token decode),
+caches ``[num_blocks, block_size, kv_heads, D]``, ``block_table [B, max_blocks]``
+int32, ``context_lens [B]`` int32 — but seeded and drawn the way the benchmark
+configs specify: context lengths, then the block table, then Q, K, V, each
+value N(0, 1) in fp32 rounded to bf16.
+
+Config names map to the five benchmark configurations (index = position):
+``cfg1_small``, ``cfg2_qwen3_8b``, ``cfg3_long``, ``cfg4_mla``, ``cfg5_verify``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+SEED_BASE = 20261201
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    name: str
+    index: int
+    batch: int
+    num_heads: int
+    kv_heads: int
+    head_dim_k: int
+    head_dim_v: int
+    block_size: int
+    ctx_min: int
+    ctx_max: int
+    q_len: int = 1
+    causal: bool = False
+    mla: bool = False
+    pool: str = "exact"  # "exact": pool = sum of blocks needed; "fixed:<n>": pool of n blocks
+    max_blocks: int | None = None  # block_table width (defaults to ceil(ctx_max/BS))
+    out_dtype: torch.dtype = torch.bfloat16
+    description: str = ""
+
+    @property
+    def group(self) -> int:
+        return self.num_heads // self.kv_heads
+
+
+CONFIGS: dict[str, DecodeConfig] = {
+    c.name: c
+    for c in [
+        DecodeConfig("cfg1_small", 0, 2, 16, 1, 128, 128, 128, 512, 512, pool="fixed:16", max_blocks=8,
+                     description="small decode: B=2, Hq=16, Hkv=1, D=128, BS=128, L=512, pool of 16 blocks"),
+        DecodeConfig("cfg2_qwen3_8b", 1, 32, 32, 8, 128, 128, 128, 1024, 8192,
+                     description="Qwen3-8B GQA decode: B=32, Hq=32, Hkv=8, D=128, BS=128, L~U[1024,8192]"),
+        DecodeConfig("cfg3_long", 2, 8, 64, 8, 128, 128, 128, 32768, 32768,
+                     description="long-context GQA: B=8, Hq=64, Hkv=8, D=128, BS=128, L=32768"),
+        DecodeConfig("cfg4_mla", 3, 128, 128, 1, 576, 512, 64, 512, 8192, mla=True,
+                     description="MLA absorbed MQA: B=128, Hq=128, 1 latent head, Dk=576, Dv=512, BS=64, "
+                                 "L~U[512,8192]"),
+        DecodeConfig("cfg5_verify", 4, 16, 32, 8, 128, 128, 128, 2048 + 8, 16384 + 8, q_len=8, causal=True,
+                     description="speculative verify: B=16, q_len=8 causal, Hq=32, Hkv=8, D=128, BS=128, "
+                                 "prefix~U[2048,16384]"),
+    ]
+}
+
+
+@dataclass
+class DecodeCase:
+    config: DecodeConfig
+    seed: int
+    query: torch.Tensor  # bf16
+    key_cache: torch.Tensor  # bf16 [nblk, BS, Hkv, Dk]
+    value_cache: torch.Tensor  # bf16 [nblk, BS, Hkv, Dv] (a view of key_cache for MLA)
+    block_table: torch.Tensor  # int32 [B, max_blocks]
+    context_lens: torch.Tensor  # int32 [B]
+    scale: float
+    extra: dict = field(default_factory=dict)
+
+    def to(self, device) -> "DecodeCase":
+        k = self.key_cache.to(device)
+        v = k[..., : self.config.head_dim_v] if self.config.mla else self.value_cache.to(device)
+        return DecodeCase(self.config, self.seed, self.query.to(device), k, v, self.block_table.to(device),
+                          self.context_lens.to(device), self.scale, dict(self.extra))
+
+    def out_shape(self) -> tuple[int, ...]:
+        return (*self.query.shape[:-1], self.config.head_dim_v)
+
+
+def _randn_bf16(shape, gen: torch.Generator) -> torch.Tensor:
+    return torch.randn(shape, generator=gen, dtype=torch.float32).to(torch.bfloat16)
+
+
+def make_case(cfg: DecodeConfig | str, seed: int | None = None, *, ctx_override: list[int] | None = None,
+              batch_override: int | None = None) -> DecodeCase:
+    """Generate one seeded case on the CPU (deterministic across machines)."""
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    if batch_override is not None:
+        cfg = DecodeConfig(**{**cfg.__dict__, "batch": batch_override})
+    seed = SEED_BASE + cfg.index if seed is None else seed
+    gen = torch.Generator("cpu").manual_seed(seed)
+    bsz, bs = cfg.batch, cfg.block_size
+    # 1. context lengths
+    if ctx_override is not None:
+        lens = torch.tensor(ctx_override, dtype=torch.int32)
+        if lens.numel() != bsz:
+            raise ValueError("ctx_override must have one length per sequence")
+    elif cfg.ctx_min == cfg.ctx_max:
+        lens = torch.full((bsz,), cfg.ctx_max, dtype=torch.int32)
+    else:
+        lens = torch.randint(cfg.ctx_min, cfg.ctx_max + 1, (bsz,), generator=gen, dtype=torch.int32)
+    nblk_seq = [(int(n) + bs - 1) // bs for n in lens]
+    max_blocks = cfg.max_blocks or max(math.ceil(cfg.ctx_max / bs), max(nblk_seq))
+    # 2. block table: random non-overlapping assignment from the pool
+    if cfg.pool.startswith("fixed:"):
+        pool = int(cfg.pool.split(":")[1])
+    else:
+        pool = sum(nblk_seq)
+    if sum(nblk_seq) > pool:
+        raise ValueError("pool too small for the context lengths")
+    perm = torch.randperm(pool, generator=gen).to(torch.int32)
+    table = torch.zeros((bsz, max_blocks), dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(nblk_seq):
+        table[b, :n] = perm[off : off + n]
+        off += n
+    # 3-5. Q, K, V
+    qshape = (bsz, cfg.q_len, cfg.num_heads, cfg.head_dim_k) if cfg.q_len > 1 else (bsz, cfg.num_heads,
+                                                                                     cfg.head_dim_k)
+    query = _randn_bf16(qshape, gen)
+    key = _randn_bf16((pool, bs, cfg.kv_heads, cfg.head_dim_k), gen)
+    if cfg.mla:
+        value = key[..., : cfg.head_dim_v]
+    else:
+        value = _randn_bf16((pool, bs, cfg.kv_heads, cfg.head_dim_v), gen)
+    return DecodeCase(cfg, seed, query, key, value, table, lens, 1.0 / math.sqrt(cfg.head_dim_k))
+
+
+def make_custom_case(*, batch: int, num_heads: int, kv_heads: int, head_dim: int, block_size: int,
+                     context_lens: list[int], seed: int, q_len: int = 1, causal: bool = False,
+                     head_dim_v: int | None = None, mla: bool = False, max_blocks: int | None = None,
+                     pool_extra: int = 0, scale: float | None = None, value_range: float | None = None) -> DecodeCase:
+    """Arbitrary-shape case (tests): same draw order, pool = blocks needed + ``pool_extra``."""
+    dv = head_dim_v or head_dim
+    cfg = DecodeConfig("custom", -1, batch, num_heads, kv_heads, head_dim, dv, block_size,
+                       min(context_lens), max(context_lens), q_len=q_len, causal=causal, mla=mla,
+                       max_blocks=max_blocks or max(1, math.ceil(max(context_lens) / block_size)))
+    gen = torch.Generator("cpu").manual_seed(seed)
+    lens = torch.tensor(context_lens, dtype=torch.int32)
+    nblk_seq = [(int(n) + block_size - 1) // block_size for n in context_lens]
+    pool = max(1, sum(nblk_seq) + pool_extra)
+    perm = torch.randperm(pool, generator=gen).to(torch.int32)
+    table = torch.zeros((batch, cfg.max_blocks), dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(nblk_seq):
+        table[b, :n] = perm[off : off + n]
+        off += n
+    qshape = (batch, q_len, num_heads, head_dim) if q_len > 1 else (batch, num_heads, head_dim)
+    query = _randn_bf16(qshape, gen)
+    key = _randn_bf16((pool, block_size, kv_heads, head_dim), gen)
+    value = key[..., :dv] if mla else _randn_bf16((pool, block_size, kv_heads, dv), gen)
+    if value_range is not None:
+        query, key = (query.float() * value_range).to(torch.bfloat16), (key.float() * value_range).to(torch.bfloat16)
+        if mla:
+            value = key[..., :dv]
+    return DecodeCase(cfg, seed, query, key, value, table, lens,
+                      scale if scale is not None else 1.0 / math.sqrt(head_dim))
+
+
+# ---------------------------------------------------------------------------
+# Roofline accounting
+# ---------------------------------------------------------------------------
+
+
+def algorithmic_bytes(case: DecodeCase, out_bytes: int = 2) -> int:
+    """HBM bytes the op must move at minimum.
+
+    K and V of the valid tokens (MLA: K only, V is a prefix of K), the query,
+    the output, the used block-table entries and the lengths. Split-K workspace
+    traffic is not counted.
+    """
+    c = case.config
+    lens = [int(x) for x in case.context_lens.tolist()]
+    tok = sum(lens)
+    kv_cols = c.head_dim_k if c.mla else c.head_dim_k + c.head_dim_v
+    kv = tok * c.kv_heads * kv_cols * 2
+    q = c.batch * c.q_len * c.num_heads * c.head_dim_k * 2
+    o = c.batch * c.q_len * c.num_heads * c.head_dim_v * out_bytes
+    tables = 4 * sum((n + c.block_size - 1) // c.block_size for n in lens) + 4 * c.batch
+    return kv + q + o + tables
+
+
+def kv_bytes(case: DecodeCase) -> int:
+    c = case.config
+    tok = sum(int(x) for x in case.context_lens.tolist())
+    kv_cols = c.head_dim_k if c.mla else c.head_dim_k + c.head_dim_v
+    return tok * c.kv_heads * kv_cols * 2
+
+
+def algorithmic_flops(case: DecodeCase) -> int:
+    """QKᵀ + PV multiply-adds ×2 over unmasked (row, token) pairs."""
+    c = case.config
+    total = 0
+    for n in (int(x) for x in case.context_lens.tolist()):
+        if c.causal:
+            pairs = sum(n - (c.q_len - 1 - i) for i in range(c.q_len))
+        else:
+            pairs = c.q_len * n
+        total += pairs * c.num_heads * 2 * (c.head_dim_k + c.head_dim_v)
+    return total

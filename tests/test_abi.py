@@ -1,0 +1,185 @@
+"""CPU checks of the drop-in boundary: byte layouts, exported symbols, host-side logic.
+
+No kernel is launched here (the container has no GPU); everything below runs in
+host code of libsimpler_hip.so or in the Python mirror.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from simpler_amd import _lib
+from simpler_amd import paged_attention as pa
+from simpler_amd.task_interface import (
+    ArgDirection,
+    CallConfig,
+    ChipCallable,
+    ChipStorageTaskArgs,
+    ChipTensor,
+    CoreCallable,
+    DataType,
+    scalar_to_uint64,
+)
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for hdr in (ROOT / "include").rglob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M):
+            if not m.group(0).lstrip().startswith(("typedef", "return", "static")):
+                names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 45, names
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) == names
+
+
+def test_chip_tensor_layout_matches_reference_static_asserts():
+    # src/common/task_interface/tensor.h:489-500
+    assert ctypes.sizeof(ChipTensor) == 128
+    offs = {f[0]: getattr(ChipTensor, f[0]).offset for f in ChipTensor._fields_}
+    assert offs["owner_task_id"] == 16 and offs["start_offset"] == 24 and offs["version"] == 32
+    assert offs["ndims"] == 36 and offs["dtype"] == 40 and offs["manual_dep"] == 41
+    assert offs["is_contiguous"] == 42 and offs["address_space"] == 43 and offs["shapes"] == 44
+    assert offs["extent_elem_cache"] == 64 and offs["strides"] == 72
+
+
+def test_task_args_and_call_config_layout():
+    assert ctypes.sizeof(ChipStorageTaskArgs) == 33856
+    assert ChipStorageTaskArgs.scalars_.offset == 256 * 128
+    assert ChipStorageTaskArgs.tensor_count_.offset == 256 * 128 + 128 * 8
+    assert ctypes.sizeof(CallConfig) == 6 * 4 + 12 * 8 + 1024  # call_config.h:146-150
+    args = ChipStorageTaskArgs()
+    args.add_tensor(ChipTensor.make(0x1000, (2, 3), DataType.FLOAT32))
+    args.add_scalar(1.0)
+    with pytest.raises(RuntimeError):
+        args.add_tensor(ChipTensor.make(0x1000, (2,), DataType.FLOAT32))
+    assert args.scalar(0) == 0x3F800000 and args.tensor_count() == 1
+
+
+def test_chip_tensor_make_fields():
+    t = ChipTensor.make(0xABC0, (4, 8, 2, 16), DataType.BFLOAT16, child_memory=True)
+    assert t.ndims == 4 and list(t.strides)[:4] == [256, 32, 16, 1]
+    assert t.buffer.size == 4 * 8 * 2 * 16 * 2 and t.is_contiguous == 1 and t.address_space == 1
+    v = ChipTensor.make(0xABC0, (4, 8, 1, 12), DataType.BFLOAT16, strides=(8 * 16, 16, 16, 1))
+    assert v.is_contiguous == 0
+
+
+def test_scalar_to_uint64_matches_reference_rules():
+    assert scalar_to_uint64(1.0) == 0x3F800000
+    assert scalar_to_uint64(ctypes.c_float(0.5)) == 0x3F000000
+    assert scalar_to_uint64(ctypes.c_double(1.0)) == 0x3FF0000000000000
+    assert scalar_to_uint64(-1) == 0xFFFFFFFFFFFFFFFF
+
+
+def test_callable_byte_layout():
+    core = CoreCallable.build(signature=[ArgDirection.IN, ArgDirection.OUT], binary=b"\x01\x02\x03")
+    raw = core.buffer
+    assert len(raw) == 192 + 3 and raw[192:] == b"\x01\x02\x03"
+    assert int.from_bytes(raw[128:132], "little") == 2 and int.from_bytes(raw[132:136], "little") == 3
+    chip = pa.reference_chain_callable(orch_binary=b"ORCH")
+    raw = chip.buffer
+    assert raw[1032:1032 + 25] == b"aicpu_orchestration_entry"
+    assert int.from_bytes(raw[9292:9296], "little") == 4  # child_count_
+    assert raw[ChipCallable.STORAGE_OFFSET:ChipCallable.STORAGE_OFFSET + 4] == b"ORCH"
+    first_child = int.from_bytes(raw[5196:5200], "little")
+    assert first_child % 64 == 0 and first_child >= 4
+
+
+def test_register_recognises_the_reference_chain_only():
+    lib = _lib.lib()
+    ctx = lib.create_device_context()
+    try:
+        assert lib.simpler_register_callable(ctx, 0, pa.reference_chain_callable().address()) == 0
+        assert lib.simpler_register_callable(ctx, 1, pa.native_callable().address()) == 0
+        other = ChipCallable.build(signature=[ArgDirection.IN], func_name="vector_add", binary=b"",
+                                   children=[(0, CoreCallable.build([ArgDirection.IN]))])
+        assert lib.simpler_register_callable(ctx, 2, other.address()) == -2
+        # same orchestration signature but a different incore chain is not the PA chain
+        wrong = ChipCallable.build(signature=pa.ORCH_SIGNATURE, func_name="aicpu_orchestration_entry", binary=b"",
+                                   children=[(i, CoreCallable.build([ArgDirection.IN])) for i in range(4)])
+        assert lib.simpler_register_callable(ctx, 3, wrong.address()) == -2
+        assert lib.simpler_register_callable(ctx, 64, pa.native_callable().address()) == -1
+    finally:
+        lib.destroy_device_context(ctx)
+
+
+def test_pipeline_contract_and_sizes():
+    lib = _lib.lib()
+    p = ctypes.cast(lib.get_pipeline_contract(), ctypes.POINTER(ctypes.c_uint32 * 3)).contents
+    assert list(p) == [1, 0, 1]  # abi_version, resource_count, pipeline_depth
+    assert lib.get_runtime_size() >= 256 and lib.get_runtime_alignment() == 64
+
+
+def test_unsupported_entry_points_say_so():
+    lib = _lib.lib()
+    assert lib.comm_init(0, 1, None, b"") is None
+    assert lib.comm_barrier(None) == -2
+    assert lib.ensure_acl_ready_ctx(None, 0) == -2
+    assert lib.simpler_provision_dma_workspace(None, 1, None, 0) == -2
+    assert lib.simpler_provision_dma_workspace(None, 0, None, 0) == 0
+
+
+def _args(**kw) -> _lib.PaDecodeArgs:
+    a = _lib.PaDecodeArgs()
+    base = dict(query=0x1000, key_cache=0x2000, value_cache=0x3000, block_table=0x4000, context_lens=0x5000,
+                out=0x6000, k_block_stride=128 * 8 * 128, k_token_stride=8 * 128, k_head_stride=128,
+                v_block_stride=128 * 8 * 128, v_token_stride=8 * 128, v_head_stride=128, batch=32, q_len=1,
+                num_heads=32, num_kv_heads=8, head_dim_k=128, head_dim_v=128, block_size=128,
+                max_blocks_per_seq=64, num_blocks=1200, out_dtype=6, scale=0.088, causal=0, blocks_per_split=0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_host_validation_rejects_bad_arguments_without_launching():
+    lib = _lib.lib()
+    good = _args()
+    assert lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(good)) > 0
+    bad = [
+        _args(num_heads=30),  # not a multiple of kv heads
+        _args(head_dim_k=100, head_dim_v=100),  # not a multiple of 8
+        _args(k_token_stride=0),
+        _args(query=0x1001),  # misaligned
+        _args(blocks_per_split=65),
+        _args(block_size=0),
+    ]
+    for a in bad:
+        assert lib.simpler_hip_pa_decode(ctypes.byref(a), ctypes.c_void_p(0x100000), 1 << 30, None) == -1
+    assert lib.simpler_hip_pa_decode(ctypes.byref(_args(out_dtype=2)), ctypes.c_void_p(0x100000), 1 << 30,
+                                     None) == -2
+    # unsupported block size (not a multiple of 16)
+    assert lib.simpler_hip_pa_decode(ctypes.byref(_args(block_size=48)), ctypes.c_void_p(0x100000), 1 << 30,
+                                     None) == -2
+    # workspace too small
+    assert lib.simpler_hip_pa_decode(ctypes.byref(good), ctypes.c_void_p(0x100000), 16, None) == -4
+
+
+def test_split_plan():
+    assert pa.plan(_args()) == (4, 16)  # cfg2: 256 tiles x 64 blocks / 4096 waves -> 4 blocks per split
+    assert pa.plan(_args(batch=8, num_heads=64, max_blocks_per_seq=256)) == (4, 64)
+    assert pa.plan(_args(blocks_per_split=7)) == (7, 10)
+    assert pa.plan(_args(batch=1, max_blocks_per_seq=4096 // 128)) == (4, 8)
+
+
+def test_workspace_has_a_fixed_counter_region():
+    lib = _lib.lib()
+    tiny = _args(batch=1, num_heads=8, num_kv_heads=8, max_blocks_per_seq=1)
+    # 65536 counters + error word, 256-byte aligned, precede any partial data
+    assert lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(tiny)) >= 4 * 65537
+    too_many_tiles = _args(batch=65535, num_heads=32, num_kv_heads=8)
+    assert lib.simpler_hip_pa_decode(ctypes.byref(too_many_tiles), ctypes.c_void_p(0x100000), 1 << 40, None) == -2

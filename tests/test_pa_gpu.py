@@ -1,0 +1,191 @@
+"""GPU parity of the fused decode kernel against the CPU oracle (through the C ABI).
+
+Every call goes through ``simpler_hip_pa_decode`` in libsimpler_hip.so. Cases:
+the reference's own scene-test shapes (CaseSmall1/CaseVarSeq2/CaseVarSeq4 of
+examples/a2a3/tensormap_and_ringbuffer/paged_attention/test_paged_attention.py
+:108-168 and the GQA cases of spmd_paged_attention_highperf/
+test_spmd_paged_attention_highperf.py:170-232), the five benchmark configs,
+ragged and edge lengths, every supported block size and head dim, and
+size-independent properties at full size (split invariance, determinism).
+Tolerance: max-abs 2e-2 and rel-L2 1e-3 (bf16 inputs, fp32 accumulation); the
+reference scene tests' allclose(1e-3, 1e-3) is checked where it applies.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from simpler_amd import paged_attention as pa
+from simpler_amd.workloads import CONFIGS, make_case, make_custom_case
+from tests.pa_helpers import REF_ATOL, REF_RTOL, assert_close, oracle_c, oracle_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(case, device, out_dtype=torch.float32, blocks_per_split=0):
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=out_dtype, device=device)
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out, case.scale,
+                              causal=case.config.causal, blocks_per_split=blocks_per_split)
+    torch.cuda.synchronize(device)
+    return out.float().cpu().numpy()
+
+
+REFERENCE_CASES = {
+    "CaseSmall1": dict(batch=1, num_heads=16, kv_heads=1, head_dim=16, block_size=16, context_lens=[33]),
+    "CaseSmall2": dict(batch=1, num_heads=16, kv_heads=1, head_dim=16, block_size=16, context_lens=[128]),
+    "CaseVarSeq2": dict(batch=2, num_heads=16, kv_heads=1, head_dim=16, block_size=16, context_lens=[33, 17]),
+    "CaseVarSeq4": dict(batch=4, num_heads=16, kv_heads=1, head_dim=16, block_size=16,
+                        context_lens=[33, 64, 128, 15]),
+    "highperf_b1_h32_kv8_s128": dict(batch=1, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                     context_lens=[128]),
+    "highperf_b4_h32_kv8_s512": dict(batch=4, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                     context_lens=[512] * 4),
+    "highperf_b1_h32_kv8_s4096": dict(batch=1, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                      context_lens=[4096]),
+    "Case2_h64_bs64_short": dict(batch=2, num_heads=64, kv_heads=1, head_dim=128, block_size=64,
+                                 context_lens=[700, 1000]),
+    "Case3_d256_bs64_short": dict(batch=2, num_heads=64, kv_heads=1, head_dim=256, block_size=64,
+                                  context_lens=[640, 333]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_CASES))
+def test_reference_scene_cases(name, device):
+    print(f"[case] {name}", flush=True)
+    case = make_custom_case(seed=42, **REFERENCE_CASES[name])
+    ref = oracle_numpy(case)
+    got = run_gpu(case, device)
+    assert_close(got, ref, what=name)
+    np.testing.assert_allclose(got, ref, rtol=REF_RTOL, atol=REF_ATOL)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_cfg1_small(out_dtype, device):
+    print(f"[case] cfg1_small out={out_dtype}", flush=True)
+    case = make_case("cfg1_small")
+    ref = oracle_numpy(case)
+    got = run_gpu(case, device, out_dtype=out_dtype)
+    if out_dtype == torch.bfloat16:
+        ref = torch.tensor(ref).to(torch.bfloat16).float().numpy()
+    assert_close(got, ref, what="cfg1")
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
+def test_block_sizes_and_head_dims(bs, d, device):
+    if bs * d > 16384:
+        pytest.skip("block_size*head_dim above the register-resident block limit")
+    print(f"[case] bs={bs} d={d}", flush=True)
+    case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=d, block_size=bs,
+                            context_lens=[1, bs + 3, 5 * bs - 1], seed=100 + bs + d)
+    assert_close(run_gpu(case, device), oracle_numpy(case), what=f"bs{bs}_d{d}")
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 5, 8, 16, 32])
+def test_gqa_groups(group, device):
+    print(f"[case] group={group}", flush=True)
+    case = make_custom_case(batch=2, num_heads=2 * group, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[777, 1500], seed=200 + group)
+    assert_close(run_gpu(case, device), oracle_numpy(case), what=f"g{group}")
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8])
+def test_causal_multi_token(q_len, device):
+    print(f"[case] causal q_len={q_len}", flush=True)
+    case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=128, block_size=128, q_len=q_len,
+                            causal=True, context_lens=[q_len, 129 + q_len, 1000], seed=300 + q_len)
+    assert_close(run_gpu(case, device), oracle_numpy(case), what=f"causal{q_len}")
+
+
+def test_causal_fully_masked_last_block(device):
+    # prefix ends on a block boundary: rows 0..q_len-2 see nothing of the last block
+    case = make_custom_case(batch=1, num_heads=4, kv_heads=1, head_dim=64, block_size=16, q_len=4, causal=True,
+                            context_lens=[33], seed=301)
+    assert_close(run_gpu(case, device), oracle_numpy(case), what="causal_masked_block")
+
+
+@pytest.mark.parametrize("bps", [1, 2, 3, 7, 64])
+def test_split_counts_agree(bps, device):
+    print(f"[case] bps={bps}", flush=True)
+    case = make_custom_case(batch=4, num_heads=16, kv_heads=4, head_dim=128, block_size=128,
+                            context_lens=[1, 128, 4000, 8191], seed=400)
+    assert_close(run_gpu(case, device, blocks_per_split=bps), oracle_numpy(case), what=f"bps{bps}")
+
+
+def test_empty_and_single_token_contexts(device):
+    case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[0, 1, 2], seed=500)
+    got = run_gpu(case, device)
+    assert np.all(got[0] == 0)
+    assert_close(got, oracle_numpy(case), what="empty/single")
+
+
+def test_large_score_magnitudes_stay_finite(device):
+    case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[3000, 2500], seed=600, value_range=8.0)
+    assert_close(run_gpu(case, device, blocks_per_split=2), oracle_numpy(case), what="large scores")
+
+
+def test_garbage_past_context_is_ignored(device):
+    case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[300, 50], seed=700, pool_extra=2)
+    base = run_gpu(case, device)
+    for b, n in enumerate([300, 50]):
+        last = int(case.block_table[b, (n - 1) // 128])
+        case.value_cache[last, n % 128 :] = float("nan")
+        case.key_cache[last, n % 128 :] = float("inf")
+    np.testing.assert_array_equal(run_gpu(case, device), base)
+
+
+def test_out_of_pool_block_is_reported_not_read(device):
+    case = make_custom_case(batch=1, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[300], seed=800)
+    case.block_table[0, 1] = 10_000
+    run_gpu(case, device)
+    with pytest.raises(pa.PagedAttentionError):
+        pa.check_errors(device)
+    pa.check_errors(device)  # cleared
+
+
+@pytest.mark.parametrize("name", ["cfg1_small", "cfg2_qwen3_8b", "cfg5_verify"])
+def test_benchmark_configs_full_size(name, device):
+    print(f"[case] {name} full size", flush=True)
+    case = make_case(name)
+    ref = oracle_c(case, n_threads=16)
+    got = run_gpu(case, device, out_dtype=torch.float32)
+    assert_close(got, ref, what=name)
+
+
+def test_cfg3_long_context_reduced_batch(device):
+    # same shape per sequence as cfg3 (L=32768, 64 q heads, 8 kv heads); two sequences keep the CPU oracle short
+    case = make_case("cfg3_long", batch_override=2)
+    assert_close(run_gpu(case, device), oracle_c(case, n_threads=16), what="cfg3 x2")
+
+
+def test_full_size_split_invariance_and_determinism(device):
+    case = make_case("cfg3_long").to(device)
+    outs = []
+    for bps in (4, 16, 64, 16):
+        out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+        pa.paged_attention_decode(case.query, case.key_cache, case.value_cache, case.block_table,
+                                  case.context_lens, out, case.scale, blocks_per_split=bps)
+        outs.append(out)
+    torch.cuda.synchronize(device)
+    ref = outs[1].cpu().numpy()
+    for o in outs:
+        assert_close(o.cpu().numpy(), ref, max_abs=1e-4, rel_l2=1e-5, what="split invariance")
+    np.testing.assert_array_equal(outs[3].cpu().numpy(), ref)  # same plan, same bits
+
+
+def test_workspace_reused_across_plans_keeps_counters_clean(device):
+    # Regression: a plan with few tiles writes split partials right after its
+    # counters; a later plan with more tiles reusing the same workspace must not
+    # find that data in its own counters (counters sit in a fixed region).
+    small = make_case("cfg3_long", batch_override=2)
+    run_gpu(small, device, blocks_per_split=4)
+    big = make_case("cfg3_long")
+    got = run_gpu(big, device, blocks_per_split=4)
+    assert_close(got, oracle_c(big, n_threads=16), what="workspace reuse")
