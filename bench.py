@@ -36,7 +36,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default=DEFAULT_CONFIG)
-    p.add_argument("--blocks-per-split", type=int, default=0, help="0 = automatic split plan")
+    p.add_argument("--workers", type=int, default=0, help="worker wavefronts; 0 = one per wave slot")
     p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample duration")
@@ -110,8 +110,8 @@ def main() -> int:
     out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
     out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
     pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
-                         case.scale, causal=cfg.causal, blocks_per_split=args.blocks_per_split)
-    bps, max_splits = pa.plan(pargs)
+                         case.scale, causal=cfg.causal, num_workers=args.workers)
+    workers = pa.plan(pargs)
     stream = torch.cuda.current_stream(dev)
 
     print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
@@ -174,8 +174,7 @@ def main() -> int:
             "block_size": cfg.block_size,
             "context_tokens": int(case_cpu.context_lens.sum()),
             "out_dtype": args.out_dtype,
-            "blocks_per_split": bps,
-            "max_splits": max_splits,
+            "workers": workers,
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -187,7 +186,7 @@ def main() -> int:
             "traffic": traffic,
             "algorithmic_bytes": nbytes,
             "kv_bytes": kv_bytes(case_cpu),
-            "kernel": "pa_decode_splitk_kernel",
+            "kernel": "pa_decode_kernel (+ pa_merge_kernel)",
             "tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 3),
         },
         "cpu_baseline": cpu,

@@ -77,25 +77,29 @@ typedef struct SimplerHipPaDecodeArgs {
     int32_t out_dtype;
     float scale;
     int32_t causal;
-    /* 0 = automatic split plan; > 0 forces KV blocks per split (tuning). */
-    int32_t blocks_per_split;
+    /* 0 = one worker wavefront per wave slot of the device; > 0 forces the
+     * number of workers the (tile, KV block) work list is divided among. */
+    int32_t num_workers;
     int32_t reserved;
 } SimplerHipPaDecodeArgs;
 
 /* Bytes of device workspace simpler_hip_pa_decode needs for these args
- * (split partials + self-resetting counters + error word). */
+ * (error word + two partial-result slots per worker). Depends on the current
+ * device (its wave-slot count) when num_workers is 0. */
 size_t simpler_hip_pa_decode_workspace_size(const SimplerHipPaDecodeArgs *args);
 
-/* Zero a freshly allocated workspace (counters must start at zero; the kernel
- * leaves them at zero again after every call). Enqueued on `stream`. */
+/* Zero a freshly allocated workspace (the error word must start at zero).
+ * Enqueued on `stream`. */
 int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 /*
- * Enqueue the fused decode kernel on `stream`. `workspace` must be at least
- * simpler_hip_pa_decode_workspace_size(args) bytes, initialised once with
- * simpler_hip_pa_decode_workspace_init, and not shared by calls that may run
- * concurrently. Returns 0 or a negative SIMPLER_HIP_ERR_* code (shape and dtype
- * checks happen on the host before anything is launched).
+ * Enqueue the decode on `stream`: the fused kernel (one wavefront per worker,
+ * each over an equal slice of the flattened (tile, KV block) work), then the
+ * small kernel that merges tiles cut between workers. `workspace` must be at
+ * least simpler_hip_pa_decode_workspace_size(args) bytes, 256-byte aligned,
+ * initialised once with simpler_hip_pa_decode_workspace_init, and not shared by
+ * calls that may run concurrently. Returns 0 or a negative SIMPLER_HIP_ERR_*
+ * code (shape and dtype checks happen on the host before anything is launched).
  */
 int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *args, void *workspace, size_t workspace_bytes, void *stream);
 
@@ -104,10 +108,10 @@ int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *args, void *workspace, s
  * blocks are skipped, never dereferenced), else 0. Clears the flag. Synchronous. */
 int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream);
 
-/* Kernel-only helpers for measurement: name of the kernel instantiation the
- * args select, and the split plan (blocks per split, max splits). */
+/* Measurement helpers: name of the main kernel the args select, and the
+ * number of worker wavefronts a launch uses. */
 const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args);
-int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *blocks_per_split, int32_t *max_splits);
+int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *num_workers);
 
 #pragma GCC visibility pop
 

@@ -54,7 +54,7 @@ class PaDecodeArgs(ctypes.Structure):
         ("out_dtype", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("causal", ctypes.c_int32),
-        ("blocks_per_split", ctypes.c_int32),
+        ("num_workers", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
     ]
 
@@ -76,7 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_pa_decode": (_I, [_ARGS_P, _VP, _SZ, _VP]),
     "simpler_hip_pa_decode_check": (_I, [_VP, _SZ, _VP]),
     "simpler_hip_pa_decode_kernel_name": (ctypes.c_char_p, [_ARGS_P]),
-    "simpler_hip_pa_decode_plan": (_I, [_ARGS_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+    "simpler_hip_pa_decode_plan": (_I, [_ARGS_P, ctypes.POINTER(_I32)]),
     # include/simpler_hip/pto_runtime_c_api.h
     "get_pipeline_contract": (_VP, []),
     "get_runtime_size": (_SZ, []),

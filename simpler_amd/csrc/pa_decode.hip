@@ -23,9 +23,18 @@
 // A block whose max lies more than kFrameGap below the running max adds less
 // than e^-kFrameGap relative and is skipped, which bounds A by e^kFrameGap * |O|.
 //
-// Work decomposition: one 64-lane wavefront per (split, kv head, row tile,
-// batch). A row is one (query token, head in the GQA group) pair; 16 rows per
-// tile (MFMA N). A split is a contiguous run of KV blocks of one sequence.
+// Work decomposition (stream-K): the work is the flattened list of
+// (tile, KV block) pairs, tile = (batch, kv head, row tile), in that order.
+// A row is one (query token, head in the GQA group) pair; 16 rows per tile
+// (MFMA N). The main kernel launches exactly one 64-lane wavefront per wave
+// slot of the GPU (CUs x waves per CU at this kernel's occupancy) and gives
+// each an equal contiguous slice of that list, computed on the device from
+// context_lens, so ragged lengths cost no imbalance and no tail. A tile that
+// lies inside one slice is finished (normalised and stored) by that wave; a
+// tile cut by slice boundaries leaves one partial (O, m, l) per piece, and a
+// second small kernel merges those by log-sum-exp. The kernel boundary orders
+// the partial writes before the merge; no device-scope fences are used.
+//
 // Lane (qd = lane/16, pc = lane%16):
 //   QK   A operand = K token pc of the tile, dims 32kk+8qd..+7 (one 16-B load)
 //        B operand = Q row pc, same dims
@@ -34,14 +43,17 @@
 //        B operand = V[tokens 4qd..4qd+3][dim 8pc+jj], built from four 16-B row
 //                    loads by an in-register 4x8 bf16 transpose
 //        C         = O[rows 4qd..4qd+3][dim 8pc+jj]
-// K of the next block is prefetched while the current block's softmax and PV
-// run; V of a block is issued before its QK.
+// Within a segment, V of block i is issued before its QK and K of block i+1
+// is issued right after it, so both streams are in flight during the math.
 
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
+
+#include <mutex>
+#include <vector>
 
 #include "simpler_hip/pa_decode.h"
 
@@ -58,20 +70,7 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
-constexpr int kMaxBlocksPerSplit = 64;  // one block-table entry per lane
-constexpr int kMaxSplits = 64;
-// The split counters live in a fixed region at the start of every workspace,
-// sized for kCounterCapacity tiles whatever the plan: partial results of one
-// plan must never land where another plan's counters are, because the
-// counters rely on being zero between launches.
-constexpr int64_t kCounterCapacity = 65536;
-#ifndef SIMPLER_HIP_PREFETCH_K
-#define SIMPLER_HIP_PREFETCH_K 0
-#endif
-// 1: K of block i+1 is loaded while block i's softmax and PV run (costs a
-//    second block of K registers); 0: K and V of a block are both issued at
-//    the top of its iteration.
-constexpr bool kPrefetchK = SIMPLER_HIP_PREFETCH_K != 0;
+constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
 
 struct KernelParams {
     const uint16_t *q;
@@ -80,15 +79,14 @@ struct KernelParams {
     const int32_t *block_table;
     const int32_t *context_lens;
     void *out;
-    float *part_o;       // [n_tiles][max_splits][16][DV]
-    float *part_ml;      // [n_tiles][max_splits][2][16]  (m row values, then l)
-    unsigned *counters;  // [n_tiles], zero between launches
+    float *part_o;   // [workers][2 slots][16 rows][DV]
+    float *part_ml;  // [workers][2 slots][m[16], l[16]]
     unsigned *error_flag;
     int64_t k_block_stride, k_token_stride, k_head_stride;
     int64_t v_block_stride, v_token_stride, v_head_stride;
     int32_t batch, q_len, num_heads, kv_heads, group, rows, row_tiles;
-    int32_t max_blocks, num_pool_blocks;
-    int32_t blocks_per_split, max_splits;
+    int32_t block_size, max_blocks, num_pool_blocks;
+    int32_t workers;
     float scale;
     int32_t causal;
 };
@@ -133,46 +131,73 @@ struct OutStore<__bf16> {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Work partition shared by both kernels
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
+    int ctx = P.context_lens[b];
+    ctx = min(max(ctx, 0), P.max_blocks * P.block_size);
+    return (ctx + P.block_size - 1) / P.block_size;
+}
+
+// Wave-level scan over the batch. Work of batch b = blocks_of(b) * tiles per
+// batch. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
+// before batch want_b; if `pos` >= 0, *b_of_pos / *prefix_of_pos = the batch
+// whose work range contains pos and the work before it. All results are
+// wave-uniform.
+__device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
+                         int *prefix_of_pos) {
+    const int lane = threadIdx.x;
+    const int tpb = P.kv_heads * P.row_tiles;
+    int carry = 0;
+    for (int base = 0; base < P.batch; base += 64) {
+        const int b = base + lane;
+        const int cnt = b < P.batch ? blocks_of(P, b) * tpb : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += y;
+        }
+        const int excl = carry + incl - cnt;
+        if (want_b >= base && want_b < base + 64) *prefix_of_want = __shfl(excl, want_b - base, 64);
+        if (pos >= 0) {
+            const unsigned long long hit = __ballot(cnt > 0 && pos >= excl && pos < excl + cnt);
+            if (hit) {
+                const int src = __ffsll((long long)hit) - 1;
+                *b_of_pos = base + src;
+                *prefix_of_pos = __shfl(excl, src, 64);
+            }
+        }
+        carry += __shfl(incl, 63, 64);
+    }
+    return carry;
+}
+
 // Output element offset of (row r of kv head kvh, dim 0).
 __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, int kvh, int r, int dv) {
     const int i = r / P.group, hh = r - i * P.group;
     return ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * dv;
 }
 
-template <int BS, int DK, int DV, typename OutT>
-__global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams P) {
-    static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
-    static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
-    constexpr int NT = BS / 16;           // 16-token tiles per KV block
-    constexpr int KS = (DK + 31) / 32;    // 32-dim k-steps of QK
-    constexpr int DVS = (DV + 127) / 128; // 128-dim column sets of PV
+// ---------------------------------------------------------------------------
+// One segment: KV blocks [blk_begin, blk_end) of tile (b, kvh, rt)
+// ---------------------------------------------------------------------------
 
+template <int BS, int DK, int DV, typename OutT>
+__device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
+                                            const int nblk, const int blk_begin, const int blk_end,
+                                            float *const part_o, float *const part_ml) {
+    constexpr int NT = BS / 16;            // 16-token tiles per KV block
+    constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
+    constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
     const int lane = threadIdx.x;
     const int qd = lane >> 4;
     const int pc = lane & 15;
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y / P.row_tiles;
-    const int rt = blockIdx.y - kvh * P.row_tiles;
-    const int b = blockIdx.z;
-    const int tile_id = (b * P.kv_heads + kvh) * P.row_tiles + rt;
-
+    const int rows_here = min(16, P.rows - rt * 16);
     int ctx = P.context_lens[b];
     ctx = min(max(ctx, 0), P.max_blocks * BS);
-    const int nblk = (ctx + BS - 1) / BS;
-    const int bps = P.blocks_per_split;
-    const int nsplit = (nblk + bps - 1) / bps;
-    if (split >= (nsplit > 0 ? nsplit : 1)) return;
-
-    const int rows_here = min(16, P.rows - rt * 16);
-
-    if (nblk == 0) {  // empty context: defined as a zero output
-        for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
-            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
-            OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4,
-                                   (f32x4_t){0.f, 0.f, 0.f, 0.f});
-        }
-        return;
-    }
 
     // ---- Q^T operand (row pc, dims 32kk+8qd..) and this row's visible length ----
     int rowlen = 0;
@@ -193,12 +218,10 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
     // blocks that end at or before it need no masking.
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
 
-    const int blk_begin = split * bps;
-    const int blk_end = min(nblk, blk_begin + bps);
-
-    // Block-table entries of this split, one per lane.
+    // Block-table entries of this segment, a window of 64 held one per lane.
     const int32_t *bt_row = P.block_table + (int64_t)b * P.max_blocks;
-    const int bt_val = (blk_begin + lane < blk_end) ? bt_row[blk_begin + lane] : 0;
+    int bt_base = blk_begin;
+    int bt_val = (blk_begin + lane < blk_end) ? bt_row[blk_begin + lane] : 0;
 
     f32x4_t acc[DVS][8];
 #pragma unroll
@@ -210,55 +233,68 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
     u32x4_t kreg[NT][KS];
     u32x4_t vreg[NT][DVS][4];
 
-    const uint16_t *kbase_h = P.k + (int64_t)kvh * P.k_head_stride + 8 * qd;
-    const uint16_t *vbase_h = P.v + (int64_t)kvh * P.v_head_stride + 8 * pc;
+    // Addresses: a wave-uniform byte base plus one 32-bit per-lane offset that
+    // is the same for every block.
+    const int64_t k_tok_b = P.k_token_stride * 2, v_tok_b = P.v_token_stride * 2;
+    const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
+    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 16 * pc);
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
+    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * 2;
 
     auto phys_of = [&](int blk, bool &bad) -> int {
-        const int phys = __builtin_amdgcn_readlane(bt_val, blk - blk_begin);
+        if (blk - bt_base >= kBlockTableWindow) {  // blocks are visited in order
+            bt_base += kBlockTableWindow;
+            bt_val = (bt_base + lane < blk_end) ? bt_row[bt_base + lane] : 0;
+        }
+        const int phys = __builtin_amdgcn_readlane(bt_val, blk - bt_base);
         bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
         return bad ? 0 : phys;
     };
     auto load_k = [&](int phys) {
-        const uint16_t *kb = kbase_h + (int64_t)phys * P.k_block_stride;
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint16_t *kt = kb + (int64_t)(16 * t + pc) * P.k_token_stride;
+            const char *kt = kb + (int64_t)(16 * t) * k_tok_b;
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk) {
                 if (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
-                    kreg[t][kk] = ld16(kt + 32 * kk);
+                    kreg[t][kk] = *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk);
                 else
                     kreg[t][kk] = (u32x4_t){0u, 0u, 0u, 0u};
             }
         }
     };
     auto load_v = [&](int phys) {
-        const uint16_t *vb = vbase_h + (int64_t)phys * P.v_block_stride;
+        const char *vb = v_head + (int64_t)phys * P.v_block_stride * 2;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint16_t *vt = vb + (int64_t)(16 * t + 4 * qd + e) * P.v_token_stride;
+                const char *vt = vb + (int64_t)(16 * t + e) * v_tok_b;
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds) {
                     if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
-                        vreg[t][ds][e] = ld16(vt + 128 * ds);
+                        vreg[t][ds][e] = *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds);
                     else
                         vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                 }
             }
     };
 
+    // Pipeline per block i: V(i) is issued first, then QK(i) consumes K(i)
+    // (issued during block i-1), then K(i+1) is issued, then softmax and PV(i).
+    // The scheduling barriers keep the compiler from sinking loads past the
+    // math, which would serialise the memory latency.
     bool bad = false;
     int phys = phys_of(blk_begin, bad);
-    if (kPrefetchK) load_k(phys);
+    load_k(phys);
 
     for (int blk = blk_begin; blk < blk_end; ++blk) {
         const bool first = (blk == blk_begin);
-        if (blk != blk_begin && !kPrefetchK) phys = phys_of(blk, bad);
-        if (bad && lane == 0) atomicOr(P.error_flag, 1u);
-        if (!kPrefetchK) load_k(phys);
+        const bool blk_bad = bad;
+        if (blk_bad && lane == 0) atomicOr(P.error_flag, 1u);
         load_v(phys);
+        __builtin_amdgcn_sched_barrier(0);
 
         // ---- QK: S^T tiles ----
         f32x4_t s[NT];
@@ -273,11 +309,12 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
         }
 
         // ---- prefetch K of the next block ----
-        const bool blk_bad = bad;
-        if (kPrefetchK && blk + 1 < blk_end) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk + 1 < blk_end) {
             phys = phys_of(blk + 1, bad);
             load_k(phys);
         }
+        __builtin_amdgcn_sched_barrier(0);
 
         // ---- softmax prepare: mask, scale, block max (golden :145-165) ----
         const int blk0 = blk * BS;
@@ -364,7 +401,7 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
         }
     }
 
-    // ---- finish this split: O = e^{f-m} A, l = sum over the four lane groups ----
+    // ---- finish: O = e^{f-m} A, l = sum over the four lane groups ----
     float l_tot = l_part + __shfl_xor(l_part, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
     const float osc = __expf(f_run - m_run);
@@ -375,7 +412,7 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
         o_e[e] = __shfl(osc, 4 * qd + e, 64);
     }
 
-    if (nsplit == 1) {
+    if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int row = 4 * qd + e;
@@ -393,8 +430,7 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
         return;
     }
 
-    // ---- write this split's partial (O relative to m, plus m and l) ----
-    float *po = P.part_o + ((int64_t)tile_id * P.max_splits + split) * 16 * DV;
+    // ---- a piece of the tile: partial (O relative to m, plus m and l) ----
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int row = 4 * qd + e;
@@ -402,55 +438,124 @@ __global__ void __launch_bounds__(64) pa_decode_splitk_kernel(const KernelParams
 #pragma unroll
         for (int ds = 0; ds < DVS; ++ds) {
             if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
-            float *dst = po + row * DV + 128 * ds + 8 * pc;
+            float *dst = part_o + row * DV + 128 * ds + 8 * pc;
             *reinterpret_cast<f32x4_t *>(dst) =
                 (f32x4_t){acc[ds][0][e], acc[ds][1][e], acc[ds][2][e], acc[ds][3][e]} * o_e[e];
             *reinterpret_cast<f32x4_t *>(dst + 4) =
                 (f32x4_t){acc[ds][4][e], acc[ds][5][e], acc[ds][6][e], acc[ds][7][e]} * o_e[e];
         }
     }
-    float *pml = P.part_ml + ((int64_t)tile_id * P.max_splits + split) * 32;
     if (qd == 0) {
-        pml[pc] = m_run;
-        pml[16 + pc] = l_tot;
+        part_ml[pc] = m_run;
+        part_ml[16 + pc] = l_tot;
     }
-    __threadfence();
-    unsigned prev = 0;
-    if (lane == 0) prev = atomicAdd(&P.counters[tile_id], 1u);
-    prev = __shfl(prev, 0, 64);
-    if (prev != (unsigned)(nsplit - 1)) return;
-    __threadfence();
+}
 
-    // ---- last split of this tile: log-sum-exp merge over the splits ----
-    const float *ml = P.part_ml + (int64_t)tile_id * P.max_splits * 32;
-    const float *pob = P.part_o + (int64_t)tile_id * P.max_splits * 16 * DV;
+// ---------------------------------------------------------------------------
+// Main kernel: one wavefront per wave slot, one equal slice of the work each
+// ---------------------------------------------------------------------------
+
+template <int BS, int DK, int DV, typename OutT>
+__global__ void __launch_bounds__(64) pa_decode_kernel(const KernelParams P) {
+    static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
+    static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
+    const int w = blockIdx.x;
+    const int tpb = P.kv_heads * P.row_tiles;
+    const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
+    if (total == 0) return;
+    const int chunk = (total + P.workers - 1) / P.workers;
+    const int start = w * chunk;
+    const int end = min(start + chunk, total);
+    if (start >= end) return;
+    int b = 0, prefix = 0;
+    scan_work(P, -1, nullptr, start, &b, &prefix);
+    int nb = blocks_of(P, b);
+    if (nb == 0) return;  // not reached: the batch holding `start` has work
+    const int rel = start - prefix;
+    int j = rel / nb;
+    int blk = rel - j * nb;
+    int pos = start;
+    int slot = 0;
+    while (pos < end && nb > 0) {
+        const int seg = min(end - pos, nb - blk);
+        const int kvh = j / P.row_tiles, rt = j - kvh * P.row_tiles;
+        // A wave touches at most two tiles partially: the first and the last
+        // of its slice (slots 0 and 1); tiles in between are finished here.
+        float *po = P.part_o + ((int64_t)w * 2 + slot) * 16 * DV;
+        float *pml = P.part_ml + ((int64_t)w * 2 + slot) * 32;
+        run_segment<BS, DK, DV, OutT>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
+        pos += seg;
+        slot = 1;
+        if (pos >= end) break;
+        blk = 0;
+        if (++j == tpb) {
+            j = 0;
+            do {
+                ++b;
+                nb = blocks_of(P, b);
+            } while (nb == 0 && b + 1 < P.batch);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Merge kernel: one wavefront per tile; log-sum-exp merge of the pieces
+// (pa_kernel.cce:1666-1773 CombineScale), and zeros for empty contexts.
+// ---------------------------------------------------------------------------
+
+template <int DV, typename OutT>
+__global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
+    const int lane = threadIdx.x;
+    const int tpb = P.kv_heads * P.row_tiles;
+    const int tile = blockIdx.x;
+    const int b = tile / tpb, j = tile - b * tpb;
+    const int kvh = j / P.row_tiles, rt = j - kvh * P.row_tiles;
+    const int rows_here = min(16, P.rows - rt * 16);
+    int prefix = 0;
+    const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
+    const int nb = blocks_of(P, b);
+    if (nb == 0) {  // empty context: defined as a zero output
+        for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+            OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4,
+                                   (f32x4_t){0.f, 0.f, 0.f, 0.f});
+        }
+        return;
+    }
+    const int chunk = (total + P.workers - 1) / P.workers;
+    const int t0 = prefix + j * nb;
+    const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;
+    if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
     for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
         const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
         float M = -INFINITY;
-        for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, ml[sp * 32 + row]);
+        for (int w = w_first; w <= w_last; ++w) {
+            const int slot = (w * chunk >= t0) ? 0 : 1;
+            M = fmaxf(M, P.part_ml[((int64_t)w * 2 + slot) * 32 + row]);
+        }
         float L = 0.f;
         f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < nsplit; ++sp) {
-            const float w = __expf(ml[sp * 32 + row] - M);
-            L += w * ml[sp * 32 + 16 + row];
-            o += w * *reinterpret_cast<const f32x4_t *>(pob + ((int64_t)sp * 16 + row) * DV + 4 * c4);
+        for (int w = w_first; w <= w_last; ++w) {
+            const int slot = (w * chunk >= t0) ? 0 : 1;
+            const float *ml = P.part_ml + ((int64_t)w * 2 + slot) * 32;
+            const float wt = __expf(ml[row] - M);
+            L += wt * ml[16 + row];
+            o += wt * *reinterpret_cast<const f32x4_t *>(P.part_o + (((int64_t)w * 2 + slot) * 16 + row) * DV + 4 * c4);
         }
         const f32x4_t res = L > 0.f ? o / L : (f32x4_t){0.f, 0.f, 0.f, 0.f};
         OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, res);
     }
-    if (lane == 0) atomicExch(&P.counters[tile_id], 0u);
 }
 
 // ----------------------------------------------------------------------------
-// Host side: validation, split plan, dispatch
+// Host side: validation, worker count, dispatch
 // ----------------------------------------------------------------------------
 
 struct Plan {
-    int bps;
-    int max_splits;
+    int workers;
     int row_tiles;
     int rows;
-    size_t part_o_bytes, part_ml_bytes, counter_bytes;
+    size_t flag_bytes, part_ml_bytes, part_o_bytes;
     size_t total;
 };
 
@@ -469,61 +574,39 @@ int validate(const SimplerHipPaDecodeArgs *a) {
                                 a->v_block_stride, a->v_token_stride, a->v_head_stride};
     for (int64_t s : strides)
         if (s <= 0 || s % 8) return SIMPLER_HIP_ERR_INVALID;  // 16-byte aligned rows
+    if (a->k_token_stride * 2 * a->block_size >= (int64_t)1 << 31 ||
+        a->v_token_stride * 2 * a->block_size >= (int64_t)1 << 31)
+        return SIMPLER_HIP_ERR_INVALID;  // per-lane 32-bit byte offsets within a block
     if (a->out_dtype != SIMPLER_HIP_DT_FLOAT32 && a->out_dtype != SIMPLER_HIP_DT_BFLOAT16)
         return SIMPLER_HIP_ERR_UNSUPPORTED;
     if (!(a->scale == a->scale)) return SIMPLER_HIP_ERR_INVALID;
-    if (a->blocks_per_split < 0 || a->blocks_per_split > kMaxBlocksPerSplit) return SIMPLER_HIP_ERR_INVALID;
-    {
-        const int group = a->num_heads / a->num_kv_heads;
-        const int64_t row_tiles = ((int64_t)group * a->q_len + 15) / 16;
-        if ((int64_t)a->batch * a->num_kv_heads * row_tiles > kCounterCapacity) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    }
+    if (a->num_workers < 0) return SIMPLER_HIP_ERR_INVALID;
     if (((uintptr_t)a->query | (uintptr_t)a->key_cache | (uintptr_t)a->value_cache | (uintptr_t)a->out) & 15)
         return SIMPLER_HIP_ERR_INVALID;
-    return SIMPLER_HIP_OK;
-}
-
-Plan make_plan(const SimplerHipPaDecodeArgs *a) {
-    Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
-    p.rows = group * a->q_len;
-    p.row_tiles = (p.rows + 15) / 16;
-    const int64_t n_tiles = (int64_t)a->batch * a->num_kv_heads * p.row_tiles;
-    int bps = a->blocks_per_split;
-    if (bps <= 0) {
-        // Aim for ~4 KV blocks per wavefront when there is enough work to
-        // fill the chip several times over, and never more than kMaxSplits
-        // splits per tile (bounds the in-kernel merge).
-        const int64_t target_waves = 4096;
-        int64_t work = n_tiles * a->max_blocks_per_seq;
-        int64_t b = (work + target_waves - 1) / target_waves;
-        if (b < 4) b = 4;
-        const int64_t min_for_cap = (a->max_blocks_per_seq + kMaxSplits - 1) / kMaxSplits;
-        if (b < min_for_cap) b = min_for_cap;
-        if (b > kMaxBlocksPerSplit) b = kMaxBlocksPerSplit;
-        bps = (int)b;
-    }
-    p.bps = bps;
-    p.max_splits = (a->max_blocks_per_seq + bps - 1) / bps;
-    const int dv = a->head_dim_v;
-    // Layout: [error word | counters, fixed capacity] [m,l partials] [O partials]
-    p.counter_bytes = align_up((size_t)(kCounterCapacity + 1) * sizeof(unsigned), 256);
-    p.part_ml_bytes = align_up((size_t)n_tiles * p.max_splits * 32 * sizeof(float), 256);
-    p.part_o_bytes = align_up((size_t)n_tiles * p.max_splits * 16 * dv * sizeof(float), 256);
-    p.total = p.counter_bytes + p.part_ml_bytes + p.part_o_bytes;
-    return p;
+    const int64_t row_tiles = ((int64_t)group * a->q_len + 15) / 16;
+    // the flattened (tile, block) work list is indexed with 32-bit integers
+    if ((int64_t)a->batch * a->num_kv_heads * row_tiles * a->max_blocks_per_seq >= (int64_t)1 << 31)
+        return SIMPLER_HIP_ERR_UNSUPPORTED;
+    if ((int64_t)a->batch * a->num_kv_heads * row_tiles >= (int64_t)1 << 31) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    return SIMPLER_HIP_OK;
 }
 
 typedef void (*KernelFn)(KernelParams);
 
+struct KernelPair {
+    KernelFn main;
+    KernelFn merge;
+};
+
 template <int BS, int D, typename OutT>
-KernelFn pick_fn() {
-    return pa_decode_splitk_kernel<BS, D, D, OutT>;
+KernelPair pick_fn() {
+    return {pa_decode_kernel<BS, D, D, OutT>, pa_merge_kernel<D, OutT>};
 }
 
 template <int BS, typename OutT>
-KernelFn pick_d(int dk, int dv) {
-    if (dk != dv) return nullptr;
+KernelPair pick_d(int dk, int dv) {
+    if (dk != dv) return {nullptr, nullptr};
     switch (dk) {
         case 16: return pick_fn<BS, 16, OutT>();
         case 32: return pick_fn<BS, 32, OutT>();
@@ -531,26 +614,75 @@ KernelFn pick_d(int dk, int dv) {
         case 128: return pick_fn<BS, 128, OutT>();
         case 256:
             if constexpr (BS <= 64) return pick_fn<BS, 256, OutT>();
-            return nullptr;
-        default: return nullptr;
+            return {nullptr, nullptr};
+        default: return {nullptr, nullptr};
     }
 }
 
 template <typename OutT>
-KernelFn pick_bs(int bs, int dk, int dv) {
+KernelPair pick_bs(int bs, int dk, int dv) {
     switch (bs) {
         case 16: return pick_d<16, OutT>(dk, dv);
         case 32: return pick_d<32, OutT>(dk, dv);
         case 64: return pick_d<64, OutT>(dk, dv);
         case 128: return pick_d<128, OutT>(dk, dv);
-        default: return nullptr;
+        default: return {nullptr, nullptr};
     }
 }
 
-KernelFn pick_kernel(const SimplerHipPaDecodeArgs *a) {
+KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
     if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_bs<float>(a->block_size, a->head_dim_k, a->head_dim_v);
-    if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16) return pick_bs<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
-    return nullptr;
+    if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
+        return pick_bs<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
+    return {nullptr, nullptr};
+}
+
+// Wave slots of the current device for a one-wave workgroup kernel:
+// compute units x resident waves per CU at the kernel's register footprint.
+// Without a device (host-only builds and tests) an MI355X is assumed:
+// 256 CUs, one wave per SIMD.
+int wave_slots(KernelFn fn) {
+    struct Entry {
+        KernelFn fn;
+        int device;
+        int slots;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const Entry &e : cache)
+        if (e.fn == fn && e.device == dev) return e.slots;
+    int cus = 256, per_cu = 4;
+    if (dev >= 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), 64, 0) ==
+                hipSuccess &&
+            n > 0)
+            per_cu = n;
+    }
+    (void)hipGetLastError();
+    const int slots = cus * per_cu;
+    cache.push_back({fn, dev, slots});
+    return slots;
+}
+
+Plan make_plan(const SimplerHipPaDecodeArgs *a, KernelFn main_fn) {
+    Plan p{};
+    const int group = a->num_heads / a->num_kv_heads;
+    p.rows = group * a->q_len;
+    p.row_tiles = (p.rows + 15) / 16;
+    p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(main_fn);
+    const int dv = a->head_dim_v;
+    // Layout: [error word] [m,l partials] [O partials]; two partial slots per worker.
+    p.flag_bytes = 256;
+    p.part_ml_bytes = align_up((size_t)p.workers * 2 * 32 * sizeof(float), 256);
+    p.part_o_bytes = align_up((size_t)p.workers * 2 * 16 * dv * sizeof(float), 256);
+    p.total = p.flag_bytes + p.part_ml_bytes + p.part_o_bytes;
+    return p;
 }
 
 }  // namespace
@@ -560,7 +692,9 @@ using namespace simpler_hip;
 
 extern "C" size_t simpler_hip_pa_decode_workspace_size(const SimplerHipPaDecodeArgs *args) {
     if (validate(args) != SIMPLER_HIP_OK) return 0;
-    return make_plan(args).total;
+    const KernelPair k = pick_kernel(args);
+    if (!k.main) return 0;
+    return make_plan(args, k.main).total;
 }
 
 extern "C" int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
@@ -569,28 +703,27 @@ extern "C" int simpler_hip_pa_decode_workspace_init(void *workspace, size_t work
     return SIMPLER_HIP_OK;
 }
 
-extern "C" int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *blocks_per_split,
-                                          int32_t *max_splits) {
+extern "C" int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *num_workers) {
     const int rc = validate(args);
     if (rc != SIMPLER_HIP_OK) return rc;
-    const Plan p = make_plan(args);
-    if (blocks_per_split) *blocks_per_split = p.bps;
-    if (max_splits) *max_splits = p.max_splits;
+    const KernelPair k = pick_kernel(args);
+    if (!k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    if (num_workers) *num_workers = make_plan(args, k.main).workers;
     return SIMPLER_HIP_OK;
 }
 
 extern "C" const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args) {
-    if (validate(args) != SIMPLER_HIP_OK || !pick_kernel(args)) return "";
-    return "pa_decode_splitk_kernel";
+    if (validate(args) != SIMPLER_HIP_OK || !pick_kernel(args).main) return "";
+    return "pa_decode_kernel";
 }
 
 extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
                                      void *stream) {
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
-    KernelFn fn = pick_kernel(a);
-    if (!fn) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    const Plan plan = make_plan(a);
+    const KernelPair k = pick_kernel(a);
+    if (!k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    const Plan plan = make_plan(a, k.main);
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
     if (a->batch == 0) return SIMPLER_HIP_OK;
 
@@ -603,9 +736,8 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
     P.out = a->out;
     char *ws = (char *)workspace;
     P.error_flag = (unsigned *)ws;
-    P.counters = (unsigned *)ws + 1;
-    P.part_ml = (float *)(ws + plan.counter_bytes);
-    P.part_o = (float *)(ws + plan.counter_bytes + plan.part_ml_bytes);
+    P.part_ml = (float *)(ws + plan.flag_bytes);
+    P.part_o = (float *)(ws + plan.flag_bytes + plan.part_ml_bytes);
     P.k_block_stride = a->k_block_stride;
     P.k_token_stride = a->k_token_stride;
     P.k_head_stride = a->k_head_stride;
@@ -619,16 +751,17 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
     P.group = a->num_heads / a->num_kv_heads;
     P.rows = plan.rows;
     P.row_tiles = plan.row_tiles;
+    P.block_size = a->block_size;
     P.max_blocks = a->max_blocks_per_seq;
     P.num_pool_blocks = a->num_blocks;
-    P.blocks_per_split = plan.bps;
-    P.max_splits = plan.max_splits;
+    P.workers = plan.workers;
     P.scale = a->scale;
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
 
-    if ((int64_t)a->num_kv_heads * plan.row_tiles > 65535 || a->batch > 65535) return SIMPLER_HIP_ERR_INVALID;
-    dim3 grid((unsigned)plan.max_splits, (unsigned)(a->num_kv_heads * plan.row_tiles), (unsigned)a->batch);
-    hipLaunchKernelGGL(fn, grid, dim3(64), 0, (hipStream_t)stream, P);
+    const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
+    hipLaunchKernelGGL(k.main, dim3((unsigned)plan.workers), dim3(64), 0, (hipStream_t)stream, P);
+    if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(64), 0, (hipStream_t)stream, P);
     if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     return SIMPLER_HIP_OK;
 }

@@ -41,7 +41,7 @@ class PagedAttentionError(RuntimeError):
 
 
 class _Workspace:
-    """Grow-only per-device workspace (split partials + self-resetting counters)."""
+    """Grow-only per-device workspace (error word + per-worker partial slots)."""
 
     def __init__(self) -> None:
         self._mu = threading.Lock()
@@ -87,7 +87,7 @@ def make_args(
     scale: float,
     *,
     causal: bool = False,
-    blocks_per_split: int = 0,
+    num_workers: int = 0,
 ) -> _lib.PaDecodeArgs:
     """Validate torch tensors and fill the C ``SimplerHipPaDecodeArgs``."""
     _check(query, "query", torch.bfloat16, (3, 4))
@@ -130,7 +130,7 @@ def make_args(
     a.out_dtype = _OUT_DTYPES[out.dtype]
     a.scale = float(scale)
     a.causal = 1 if causal else 0
-    a.blocks_per_split = int(blocks_per_split)
+    a.num_workers = int(num_workers)
     return a
 
 
@@ -159,7 +159,7 @@ def paged_attention_decode(
     *,
     causal: bool = False,
     out_dtype: torch.dtype = torch.float32,
-    blocks_per_split: int = 0,
+    num_workers: int = 0,
 ) -> torch.Tensor:
     """Fused paged-attention decode; returns ``out`` ``[B, (q_len,) Hq, Dv]``.
 
@@ -174,7 +174,7 @@ def paged_attention_decode(
         out = torch.empty(shape, dtype=out_dtype, device=query.device)
     args = make_args(
         query, key_cache, value_cache, block_table, context_lens, out, scale,
-        causal=causal, blocks_per_split=blocks_per_split,
+        causal=causal, num_workers=num_workers,
     )
     launch(args, query.device)
     return out
@@ -190,13 +190,13 @@ def check_errors(device: torch.device | None = None) -> None:
         raise PagedAttentionError(rc, "paged attention")
 
 
-def plan(args: _lib.PaDecodeArgs) -> tuple[int, int]:
-    """(KV blocks per split, max splits) the launcher picks for ``args``."""
-    bps, ms = ctypes.c_int32(), ctypes.c_int32()
-    rc = _lib.lib().simpler_hip_pa_decode_plan(ctypes.byref(args), ctypes.byref(bps), ctypes.byref(ms))
+def plan(args: _lib.PaDecodeArgs) -> int:
+    """Number of worker wavefronts a launch with ``args`` uses on the current device."""
+    n = ctypes.c_int32()
+    rc = _lib.lib().simpler_hip_pa_decode_plan(ctypes.byref(args), ctypes.byref(n))
     if rc != 0:
         raise PagedAttentionError(rc, "simpler_hip_pa_decode_plan")
-    return bps.value, ms.value
+    return n.value
 
 
 # ---------------------------------------------------------------------------

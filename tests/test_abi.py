@@ -139,7 +139,7 @@ def _args(**kw) -> _lib.PaDecodeArgs:
                 out=0x6000, k_block_stride=128 * 8 * 128, k_token_stride=8 * 128, k_head_stride=128,
                 v_block_stride=128 * 8 * 128, v_token_stride=8 * 128, v_head_stride=128, batch=32, q_len=1,
                 num_heads=32, num_kv_heads=8, head_dim_k=128, head_dim_v=128, block_size=128,
-                max_blocks_per_seq=64, num_blocks=1200, out_dtype=6, scale=0.088, causal=0, blocks_per_split=0)
+                max_blocks_per_seq=64, num_blocks=1200, out_dtype=6, scale=0.088, causal=0, num_workers=0)
     base.update(kw)
     for k, v in base.items():
         setattr(a, k, v)
@@ -155,7 +155,7 @@ def test_host_validation_rejects_bad_arguments_without_launching():
         _args(head_dim_k=100, head_dim_v=100),  # not a multiple of 8
         _args(k_token_stride=0),
         _args(query=0x1001),  # misaligned
-        _args(blocks_per_split=65),
+        _args(num_workers=-1),
         _args(block_size=0),
     ]
     for a in bad:
@@ -169,17 +169,17 @@ def test_host_validation_rejects_bad_arguments_without_launching():
     assert lib.simpler_hip_pa_decode(ctypes.byref(good), ctypes.c_void_p(0x100000), 16, None) == -4
 
 
-def test_split_plan():
-    assert pa.plan(_args()) == (4, 16)  # cfg2: 256 tiles x 64 blocks / 4096 waves -> 4 blocks per split
-    assert pa.plan(_args(batch=8, num_heads=64, max_blocks_per_seq=256)) == (4, 64)
-    assert pa.plan(_args(blocks_per_split=7)) == (7, 10)
-    assert pa.plan(_args(batch=1, max_blocks_per_seq=4096 // 128)) == (4, 8)
+def test_worker_plan():
+    # without a device the launcher assumes an MI355X: 256 CUs x 4 SIMDs, one wave each
+    assert pa.plan(_args()) == 1024
+    assert pa.plan(_args(num_workers=7)) == 7
+    ws = lambda **kw: _lib.lib().simpler_hip_pa_decode_workspace_size(ctypes.byref(_args(**kw)))
+    # error word + two (m, l) and two O partial slots per worker, 256-byte aligned sections
+    assert ws(num_workers=7) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
+    assert ws(num_workers=1) == 256 + 256 + 2 * 16 * 128 * 4
 
 
-def test_workspace_has_a_fixed_counter_region():
+def test_work_list_must_fit_32_bit_indices():
     lib = _lib.lib()
-    tiny = _args(batch=1, num_heads=8, num_kv_heads=8, max_blocks_per_seq=1)
-    # 65536 counters + error word, 256-byte aligned, precede any partial data
-    assert lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(tiny)) >= 4 * 65537
-    too_many_tiles = _args(batch=65535, num_heads=32, num_kv_heads=8)
-    assert lib.simpler_hip_pa_decode(ctypes.byref(too_many_tiles), ctypes.c_void_p(0x100000), 1 << 40, None) == -2
+    huge = _args(batch=65535, num_heads=32, num_kv_heads=8, max_blocks_per_seq=8192)
+    assert lib.simpler_hip_pa_decode(ctypes.byref(huge), ctypes.c_void_p(0x100000), 1 << 40, None) == -2
