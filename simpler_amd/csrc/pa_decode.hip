@@ -71,6 +71,7 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
 constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
+constexpr int kWorkersPerCu = 2;       // default worker wavefronts per compute unit
 
 struct KernelParams {
     const uint16_t *q;
@@ -92,6 +93,15 @@ struct KernelParams {
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
+
+// V rows are read as whole 128-byte lines exactly once: non-temporal loads
+// keep them from displacing useful lines (measured ~11% more read bandwidth on
+// MI355X than plain loads). K is read as 64-byte halves of a line by two
+// consecutive instructions, so K uses plain loads, which let the L1 merge the
+// two halves into one line request (non-temporal K measured 5-10% slower).
+__device__ __forceinline__ u32x4_t stream_ld16(const char *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
 
 __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
     // fp32 -> bf16 round-to-nearest-even (gfx950: v_cvt_pk_bf16_f32)
@@ -143,9 +153,11 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
 
 // Wave-level scan over the batch. Work of batch b = blocks_of(b) * tiles per
 // batch. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
-// before batch want_b; if `pos` >= 0, *b_of_pos / *prefix_of_pos = the batch
-// whose work range contains pos and the work before it. All results are
-// wave-uniform.
+// before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
+// *prefix_of_pos = the batch whose work range contains pos and the work before
+// it. `pos` may be given as a fraction of the total (pos_num / pos_den of it,
+// rounded up to whole chunks) so that one pass suffices. All results are
+// wave-uniform. One context_lens load per 64 sequences.
 __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
                          int *prefix_of_pos) {
     const int lane = threadIdx.x;
@@ -173,6 +185,41 @@ __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want,
         carry += __shfl(incl, 63, 64);
     }
     return carry;
+}
+
+// Worker w's slice start in one pass over the batch (the common case of at
+// most 64 sequences): total work, then the batch containing w*chunk.
+__device__ int locate_slice(const KernelParams &P, int w, int *start, int *end, int *b_of_start,
+                            int *prefix_of_start) {
+    const int lane = threadIdx.x;
+    if (P.batch > 64) {
+        const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
+        const int chunk = (total + P.workers - 1) / max(P.workers, 1);
+        *start = w * chunk;
+        *end = min(*start + chunk, total);
+        if (*start < *end) scan_work(P, -1, nullptr, *start, b_of_start, prefix_of_start);
+        return total;
+    }
+    const int tpb = P.kv_heads * P.row_tiles;
+    const int cnt = lane < P.batch ? blocks_of(P, lane) * tpb : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+    }
+    const int total = __shfl(incl, 63, 64);
+    const int chunk = (total + P.workers - 1) / max(P.workers, 1);
+    *start = w * chunk;
+    *end = min(*start + chunk, total);
+    const int excl = incl - cnt;
+    const unsigned long long hit = __ballot(cnt > 0 && *start >= excl && *start < excl + cnt);
+    if (hit) {
+        const int src = __ffsll((long long)hit) - 1;
+        *b_of_start = src;
+        *prefix_of_start = __shfl(excl, src, 64);
+    }
+    return total;
 }
 
 // Output element offset of (row r of kv head kvh, dim 0).
@@ -274,7 +321,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds) {
                     if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
-                        vreg[t][ds][e] = *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds);
+                        vreg[t][ds][e] = stream_ld16(vt + v_lane + 256 * ds);
                     else
                         vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                 }
@@ -461,14 +508,9 @@ __global__ void __launch_bounds__(64) pa_decode_kernel(const KernelParams P) {
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
     const int w = blockIdx.x;
     const int tpb = P.kv_heads * P.row_tiles;
-    const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
-    if (total == 0) return;
-    const int chunk = (total + P.workers - 1) / P.workers;
-    const int start = w * chunk;
-    const int end = min(start + chunk, total);
+    int start = 0, end = 0, b = 0, prefix = 0;
+    locate_slice(P, w, &start, &end, &b, &prefix);
     if (start >= end) return;
-    int b = 0, prefix = 0;
-    scan_work(P, -1, nullptr, start, &b, &prefix);
     int nb = blocks_of(P, b);
     if (nb == 0) return;  // not reached: the batch holding `start` has work
     const int rel = start - prefix;
@@ -526,21 +568,23 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     const int t0 = prefix + j * nb;
     const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;
     if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
+    // Online log-sum-exp over the pieces in one pass: every piece's loads are
+    // independent, so they are all in flight together.
     for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
         const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
-        float M = -INFINITY;
-        for (int w = w_first; w <= w_last; ++w) {
-            const int slot = (w * chunk >= t0) ? 0 : 1;
-            M = fmaxf(M, P.part_ml[((int64_t)w * 2 + slot) * 32 + row]);
-        }
-        float L = 0.f;
+        float M = -INFINITY, L = 0.f;
         f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
         for (int w = w_first; w <= w_last; ++w) {
             const int slot = (w * chunk >= t0) ? 0 : 1;
-            const float *ml = P.part_ml + ((int64_t)w * 2 + slot) * 32;
-            const float wt = __expf(ml[row] - M);
-            L += wt * ml[16 + row];
-            o += wt * *reinterpret_cast<const f32x4_t *>(P.part_o + (((int64_t)w * 2 + slot) * 16 + row) * DV + 4 * c4);
+            const int64_t piece = (int64_t)w * 2 + slot;
+            const float m = P.part_ml[piece * 32 + row];
+            const float l = P.part_ml[piece * 32 + 16 + row];
+            const f32x4_t po = *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
+            const float Mn = fmaxf(M, m);
+            const float a = __expf(M - Mn), c = __expf(m - Mn);
+            L = a * L + c * l;
+            o = a * o + c * po;
+            M = Mn;
         }
         const f32x4_t res = L > 0.f ? o / L : (f32x4_t){0.f, 0.f, 0.f, 0.f};
         OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, res);
@@ -637,10 +681,14 @@ KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
     return {nullptr, nullptr};
 }
 
-// Wave slots of the current device for a one-wave workgroup kernel:
-// compute units x resident waves per CU at the kernel's register footprint.
+// Default worker count for a one-wave workgroup kernel: compute units x
+// kWorkersPerCu, capped by the waves per CU the kernel's register footprint
+// allows. Two streaming waves per CU measured fastest on MI355X for every
+// benchmark shape (512 workers: 112.8 us on the Qwen3-8B bs=32 shape, against
+// 119.2 us with four per CU and 137 us with 1.5 per CU): more waves per CU
+// make the K streams of different waves evict each other's L1 lines.
 // Without a device (host-only builds and tests) an MI355X is assumed:
-// 256 CUs, one wave per SIMD.
+// 256 CUs.
 int wave_slots(KernelFn fn) {
     struct Entry {
         KernelFn fn;
@@ -654,7 +702,7 @@ int wave_slots(KernelFn fn) {
     std::lock_guard<std::mutex> lk(mu);
     for (const Entry &e : cache)
         if (e.fn == fn && e.device == dev) return e.slots;
-    int cus = 256, per_cu = 4;
+    int cus = 256, per_cu = kWorkersPerCu;
     if (dev >= 0) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
@@ -662,7 +710,7 @@ int wave_slots(KernelFn fn) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), 64, 0) ==
                 hipSuccess &&
             n > 0)
-            per_cu = n;
+            per_cu = n < kWorkersPerCu ? n : kWorkersPerCu;
     }
     (void)hipGetLastError();
     const int slots = cus * per_cu;

@@ -170,8 +170,8 @@ def test_host_validation_rejects_bad_arguments_without_launching():
 
 
 def test_worker_plan():
-    # without a device the launcher assumes an MI355X: 256 CUs x 4 SIMDs, one wave each
-    assert pa.plan(_args()) == 1024
+    # without a device the launcher assumes an MI355X: 256 CUs x 2 worker waves each
+    assert pa.plan(_args()) == 512
     assert pa.plan(_args(num_workers=7)) == 7
     ws = lambda **kw: _lib.lib().simpler_hip_pa_decode_workspace_size(ctypes.byref(_args(**kw)))
     # error word + two (m, l) and two O partial slots per worker, 256-byte aligned sections
