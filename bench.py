@@ -43,6 +43,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                    help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
+    p.add_argument("--calibrate-copy-mib", type=int, default=0,
+                   help="before the timed region, run 3 device copies of this many MiB (a kernel of known "
+                        "traffic that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE in the same run)")
     return p.parse_args()
 
 
@@ -114,6 +117,14 @@ def main() -> int:
     workers = pa.plan(pargs)
     stream = torch.cuda.current_stream(dev)
 
+    if args.calibrate_copy_mib > 0:
+        src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
+
     print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         pa.launch(pargs, dev, stream.cuda_stream)
@@ -134,9 +145,23 @@ def main() -> int:
     print(f"[bench] timed {args.steps} steps: {kernel_ms * 1e3:.1f} us/step (events), wall {wall:.3f} s",
           file=sys.stderr, flush=True)
 
+    # The dominant kernel alone, for the roofline: events around each main
+    # launch (the merge kernel still runs after it, outside the events).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize(dev)
+    for e0, e1 in evs:
+        e0.record(stream)
+        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)
+        e1.record(stream)
+        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
+    torch.cuda.synchronize(dev)
+    main_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / args.steps
+    print(f"[bench] main kernel alone: {main_ms * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+
     out_bytes = 2 if out_dtype == torch.bfloat16 else 4
     nbytes = algorithmic_bytes(case_cpu, out_bytes=out_bytes)
-    gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+    gbs = nbytes / (kernel_ms * 1e-3) / 1e9  # whole step (main + merge kernels)
+    main_gbs = nbytes / (main_ms * 1e-3) / 1e9
     flops = algorithmic_flops(case_cpu)
     traffic = None
     tf = Path(args.traffic_file)
@@ -179,15 +204,17 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gbs, 2),
+            "achieved": round(main_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "frac": round(main_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "kernel": "pa_decode_kernel",
+            "kernel_us": round(main_ms * 1e3, 2),
             "algorithmic_bytes": nbytes,
             "kv_bytes": kv_bytes(case_cpu),
-            "kernel": "pa_decode_kernel (+ pa_merge_kernel)",
-            "tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 3),
+            "step_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (main_ms * 1e-3) / 1e12, 3),
         },
         "cpu_baseline": cpu,
     }

@@ -103,6 +103,14 @@ int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes
  */
 int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *args, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The two kernels of simpler_hip_pa_decode, separately (measurement: lets a
+ * caller put timing events between them). Running MAIN then MERGE on one
+ * stream is exactly simpler_hip_pa_decode; MERGE reads what MAIN wrote to the
+ * workspace, so it must follow a MAIN with the same args and workspace. */
+enum { SIMPLER_HIP_PHASE_MAIN = 1, SIMPLER_HIP_PHASE_MERGE = 2 };
+int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *args, void *workspace, size_t workspace_bytes,
+                                void *stream, int phases);
+
 /* After the stream has completed: returns SIMPLER_HIP_ERR_BAD_BLOCK if any
  * launch since the last check met an out-of-pool block_table entry (such
  * blocks are skipped, never dereferenced), else 0. Clears the flag. Synchronous. */

@@ -767,6 +767,13 @@ extern "C" const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecod
 
 extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
                                      void *stream) {
+    return simpler_hip_pa_decode_phase(a, workspace, workspace_bytes, stream,
+                                       SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE);
+}
+
+extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
+                                           void *stream, int phases) {
+    if (phases & ~(SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE)) return SIMPLER_HIP_ERR_INVALID;
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
     const KernelPair k = pick_kernel(a);
@@ -807,10 +814,14 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
-    hipLaunchKernelGGL(k.main, dim3((unsigned)plan.workers), dim3(64), 0, (hipStream_t)stream, P);
-    if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
-    hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(64), 0, (hipStream_t)stream, P);
-    if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    if (phases & SIMPLER_HIP_PHASE_MAIN) {
+        hipLaunchKernelGGL(k.main, dim3((unsigned)plan.workers), dim3(64), 0, (hipStream_t)stream, P);
+        if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    }
+    if (phases & SIMPLER_HIP_PHASE_MERGE) {
+        hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(64), 0, (hipStream_t)stream, P);
+        if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    }
     return SIMPLER_HIP_OK;
 }
 

@@ -5,7 +5,8 @@ orchestration function (``examples/a2a3/tensormap_and_ringbuffer/
 paged_attention/kernels/orchestration/paged_attention_orch.cpp:77-291``): the
 same seven arguments — query, key_cache, value_cache, block_table,
 context_lens, out, scale — in the same layouts (``goldens/paged_attention.py
-:76-84``), computed by one fused split-K gfx950 kernel in ``libsimpler_hip.so``.
+:76-84``), computed by the fused gfx950 decode kernel (plus a small merge kernel) in
+``libsimpler_hip.so``.
 
 torch supplies device memory and the current stream only; the arithmetic is
 all in the native library, and there is no fallback when it is missing.
@@ -134,8 +135,16 @@ def make_args(
     return a
 
 
-def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = None) -> None:
-    """Enqueue one decode on ``stream`` (default: torch's current stream)."""
+PHASE_MAIN, PHASE_MERGE = 1, 2
+
+
+def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = None,
+           phases: int = PHASE_MAIN | PHASE_MERGE) -> None:
+    """Enqueue one decode on ``stream`` (default: torch's current stream).
+
+    ``phases`` selects the main kernel, the merge kernel or both (the default);
+    a merge must follow a main launch with the same args.
+    """
     lib = _lib.lib()
     if stream is None:
         stream = torch.cuda.current_stream(device).cuda_stream
@@ -143,7 +152,10 @@ def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = N
     if need == 0:
         raise PagedAttentionError(-1)
     ws = _WORKSPACE.get(device, need, stream)
-    rc = lib.simpler_hip_pa_decode(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream)
+    if phases == PHASE_MAIN | PHASE_MERGE:
+        rc = lib.simpler_hip_pa_decode(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream)
+    else:
+        rc = lib.simpler_hip_pa_decode_phase(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream, phases)
     if rc != 0:
         raise PagedAttentionError(rc)
 
