@@ -71,7 +71,8 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
 constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
-constexpr int kWorkersPerCu = 2;       // default worker wavefronts per compute unit
+constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit
+constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
 
 struct KernelParams {
     const uint16_t *q;
@@ -86,6 +87,8 @@ struct KernelParams {
     int64_t k_block_stride, k_token_stride, k_head_stride;
     int64_t v_block_stride, v_token_stride, v_head_stride;
     int32_t batch, q_len, num_heads, kv_heads, group, rows, row_tiles;
+    int32_t waves_per_worker;  // row tiles a worker workgroup runs side by side (one wave each)
+    int32_t row_groups;        // ceil(row_tiles / waves_per_worker): work-list tiles per kv head
     int32_t block_size, max_blocks, num_pool_blocks;
     int32_t workers;
     float scale;
@@ -160,8 +163,8 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
 // wave-uniform. One context_lens load per 64 sequences.
 __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
                          int *prefix_of_pos) {
-    const int lane = threadIdx.x;
-    const int tpb = P.kv_heads * P.row_tiles;
+    const int lane = threadIdx.x & 63;
+    const int tpb = P.kv_heads * P.row_groups;
     int carry = 0;
     for (int base = 0; base < P.batch; base += 64) {
         const int b = base + lane;
@@ -191,7 +194,7 @@ __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want,
 // most 64 sequences): total work, then the batch containing w*chunk.
 __device__ int locate_slice(const KernelParams &P, int w, int *start, int *end, int *b_of_start,
                             int *prefix_of_start) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     if (P.batch > 64) {
         const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
         const int chunk = (total + P.workers - 1) / max(P.workers, 1);
@@ -200,7 +203,7 @@ __device__ int locate_slice(const KernelParams &P, int w, int *start, int *end, 
         if (*start < *end) scan_work(P, -1, nullptr, *start, b_of_start, prefix_of_start);
         return total;
     }
-    const int tpb = P.kv_heads * P.row_tiles;
+    const int tpb = P.kv_heads * P.row_groups;
     const int cnt = lane < P.batch ? blocks_of(P, lane) * tpb : 0;
     int incl = cnt;
 #pragma unroll
@@ -232,14 +235,14 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // One segment: KV blocks [blk_begin, blk_end) of tile (b, kvh, rt)
 // ---------------------------------------------------------------------------
 
-template <int BS, int DK, int DV, typename OutT>
+template <int BS, int DK, int DV, typename OutT, bool V_SHARED>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
     constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
     constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
     const int rows_here = min(16, P.rows - rt * 16);
@@ -321,7 +324,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds) {
                     if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
-                        vreg[t][ds][e] = stream_ld16(vt + v_lane + 256 * ds);
+                        vreg[t][ds][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds)
+                                                  : stream_ld16(vt + v_lane + 256 * ds);
                     else
                         vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                 }
@@ -502,12 +506,17 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 // Main kernel: one wavefront per wave slot, one equal slice of the work each
 // ---------------------------------------------------------------------------
 
-template <int BS, int DK, int DV, typename OutT>
-__global__ void __launch_bounds__(64) pa_decode_kernel(const KernelParams P) {
+// MAXW = 1: one wave per worker (one row tile per kv head); MAXW = 4: up to
+// four sibling waves, one per row tile, walk the same KV blocks, so V is loaded
+// through the caches (the siblings hit each other's lines) rather than
+// streamed past them.
+template <int BS, int DK, int DV, typename OutT, int MAXW>
+__global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
     const int w = blockIdx.x;
-    const int tpb = P.kv_heads * P.row_tiles;
+    const int wave = MAXW == 1 ? 0 : (int)(threadIdx.x >> 6);
+    const int tpb = P.kv_heads * P.row_groups;
     int start = 0, end = 0, b = 0, prefix = 0;
     locate_slice(P, w, &start, &end, &b, &prefix);
     if (start >= end) return;
@@ -520,12 +529,14 @@ __global__ void __launch_bounds__(64) pa_decode_kernel(const KernelParams P) {
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        const int kvh = j / P.row_tiles, rt = j - kvh * P.row_tiles;
-        // A wave touches at most two tiles partially: the first and the last
+        const int kvh = j / P.row_groups, rg = j - kvh * P.row_groups;
+        const int rt = rg * P.waves_per_worker + wave;  // this wave's row tile
+        // A worker touches at most two tiles partially: the first and the last
         // of its slice (slots 0 and 1); tiles in between are finished here.
-        float *po = P.part_o + ((int64_t)w * 2 + slot) * 16 * DV;
-        float *pml = P.part_ml + ((int64_t)w * 2 + slot) * 32;
-        run_segment<BS, DK, DV, OutT>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
+        const int64_t piece = ((int64_t)w * P.waves_per_worker + wave) * 2 + slot;
+        float *po = P.part_o + piece * 16 * DV;
+        float *pml = P.part_ml + piece * 32;
+        if (rt < P.row_tiles) run_segment<BS, DK, DV, OutT, (MAXW > 1)>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -549,9 +560,11 @@ template <int DV, typename OutT>
 __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     const int lane = threadIdx.x;
     const int tpb = P.kv_heads * P.row_tiles;
-    const int tile = blockIdx.x;
-    const int b = tile / tpb, j = tile - b * tpb;
-    const int kvh = j / P.row_tiles, rt = j - kvh * P.row_tiles;
+    const int tile = blockIdx.x;  // (batch, kv head, row tile)
+    const int b = tile / tpb, jr = tile - b * tpb;
+    const int kvh = jr / P.row_tiles, rt = jr - kvh * P.row_tiles;
+    const int rg = rt / P.waves_per_worker, wave = rt - rg * P.waves_per_worker;
+    const int j = kvh * P.row_groups + rg;  // work-list tile
     const int rows_here = min(16, P.rows - rt * 16);
     int prefix = 0;
     const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
@@ -576,7 +589,7 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
         f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
         for (int w = w_first; w <= w_last; ++w) {
             const int slot = (w * chunk >= t0) ? 0 : 1;
-            const int64_t piece = (int64_t)w * 2 + slot;
+            const int64_t piece = ((int64_t)w * P.waves_per_worker + wave) * 2 + slot;
             const float m = P.part_ml[piece * 32 + row];
             const float l = P.part_ml[piece * 32 + 16 + row];
             const f32x4_t po = *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
@@ -595,10 +608,15 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
 // Host side: validation, worker count, dispatch
 // ----------------------------------------------------------------------------
 
+typedef void (*KernelFn)(KernelParams);
+
 struct Plan {
     int workers;
     int row_tiles;
     int rows;
+    int waves_per_worker;
+    int row_groups;
+    KernelFn main;
     size_t flag_bytes, part_ml_bytes, part_o_bytes;
     size_t total;
 };
@@ -636,21 +654,21 @@ int validate(const SimplerHipPaDecodeArgs *a) {
     return SIMPLER_HIP_OK;
 }
 
-typedef void (*KernelFn)(KernelParams);
-
 struct KernelPair {
-    KernelFn main;
+    KernelFn main;        // one wave per worker
+    KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     KernelFn merge;
 };
 
 template <int BS, int D, typename OutT>
 KernelPair pick_fn() {
-    return {pa_decode_kernel<BS, D, D, OutT>, pa_merge_kernel<D, OutT>};
+    return {pa_decode_kernel<BS, D, D, OutT, 1>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker>,
+            pa_merge_kernel<D, OutT>};
 }
 
 template <int BS, typename OutT>
 KernelPair pick_d(int dk, int dv) {
-    if (dk != dv) return {nullptr, nullptr};
+    if (dk != dv) return {nullptr, nullptr, nullptr};
     switch (dk) {
         case 16: return pick_fn<BS, 16, OutT>();
         case 32: return pick_fn<BS, 32, OutT>();
@@ -658,8 +676,8 @@ KernelPair pick_d(int dk, int dv) {
         case 128: return pick_fn<BS, 128, OutT>();
         case 256:
             if constexpr (BS <= 64) return pick_fn<BS, 256, OutT>();
-            return {nullptr, nullptr};
-        default: return {nullptr, nullptr};
+            return {nullptr, nullptr, nullptr};
+        default: return {nullptr, nullptr, nullptr};
     }
 }
 
@@ -670,7 +688,7 @@ KernelPair pick_bs(int bs, int dk, int dv) {
         case 32: return pick_d<32, OutT>(dk, dv);
         case 64: return pick_d<64, OutT>(dk, dv);
         case 128: return pick_d<128, OutT>(dk, dv);
-        default: return {nullptr, nullptr};
+        default: return {nullptr, nullptr, nullptr};
     }
 }
 
@@ -678,21 +696,21 @@ KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
     if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_bs<float>(a->block_size, a->head_dim_k, a->head_dim_v);
     if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
         return pick_bs<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
-    return {nullptr, nullptr};
+    return {nullptr, nullptr, nullptr};
 }
 
-// Default worker count for a one-wave workgroup kernel: compute units x
-// kWorkersPerCu, capped by the waves per CU the kernel's register footprint
-// allows. Two streaming waves per CU measured fastest on MI355X for every
+// Default worker count: compute units x kWorkersPerCu workgroups, capped by
+// the workgroups per CU the kernel's register footprint allows. Two streaming waves per CU measured fastest on MI355X for every
 // benchmark shape (512 workers: 112.8 us on the Qwen3-8B bs=32 shape, against
 // 119.2 us with four per CU and 137 us with 1.5 per CU): more waves per CU
 // make the K streams of different waves evict each other's L1 lines.
 // Without a device (host-only builds and tests) an MI355X is assumed:
 // 256 CUs.
-int wave_slots(KernelFn fn) {
+int wave_slots(KernelFn fn, int waves_per_worker) {
     struct Entry {
         KernelFn fn;
         int device;
+        int waves;
         int slots;
     };
     static std::mutex mu;
@@ -701,34 +719,48 @@ int wave_slots(KernelFn fn) {
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     std::lock_guard<std::mutex> lk(mu);
     for (const Entry &e : cache)
-        if (e.fn == fn && e.device == dev) return e.slots;
-    int cus = 256, per_cu = kWorkersPerCu;
+        if (e.fn == fn && e.device == dev && e.waves == waves_per_worker) return e.slots;
+    // kWorkersPerCu workgroups per CU, or as many as fit (a 4-wave workgroup
+    // fills a CU at one wave per SIMD). Two 2-wave workers per CU measured
+    // 195.5 us on the speculative-verify shape against 213.9 us with one.
+    int per_cu = kWorkersPerCu;
+    int cus = 256;
+    // Without a device: the kernels use the whole register file of a SIMD
+    // (one wave per SIMD, four SIMDs per CU).
+    if (4 / waves_per_worker < per_cu) per_cu = 4 / waves_per_worker > 0 ? 4 / waves_per_worker : 1;
     if (dev >= 0) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), 64, 0) ==
-                hipSuccess &&
-            n > 0)
-            per_cu = n < kWorkersPerCu ? n : kWorkersPerCu;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn),
+                                                         64 * waves_per_worker, 0) == hipSuccess &&
+            n > 0 && n < per_cu)
+            per_cu = n;
     }
     (void)hipGetLastError();
     const int slots = cus * per_cu;
-    cache.push_back({fn, dev, slots});
+    cache.push_back({fn, dev, waves_per_worker, slots});
     return slots;
 }
 
-Plan make_plan(const SimplerHipPaDecodeArgs *a, KernelFn main_fn) {
+Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
     Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
     p.row_tiles = (p.rows + 15) / 16;
-    p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(main_fn);
+    // Row tiles of one kv head run as sibling waves of one worker workgroup
+    // (up to four), so K/V of a block is fetched once for all of them.
+    p.waves_per_worker = p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker;
+    p.row_groups = (p.row_tiles + p.waves_per_worker - 1) / p.waves_per_worker;
+    p.main = p.waves_per_worker > 1 ? k.main_multi : k.main;
+    p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.waves_per_worker);
     const int dv = a->head_dim_v;
-    // Layout: [error word] [m,l partials] [O partials]; two partial slots per worker.
+    // Layout: [error word] [m,l partials] [O partials]; two partial slots per
+    // worker wave.
+    const size_t pieces = (size_t)p.workers * p.waves_per_worker * 2;
     p.flag_bytes = 256;
-    p.part_ml_bytes = align_up((size_t)p.workers * 2 * 32 * sizeof(float), 256);
-    p.part_o_bytes = align_up((size_t)p.workers * 2 * 16 * dv * sizeof(float), 256);
+    p.part_ml_bytes = align_up(pieces * 32 * sizeof(float), 256);
+    p.part_o_bytes = align_up(pieces * 16 * dv * sizeof(float), 256);
     p.total = p.flag_bytes + p.part_ml_bytes + p.part_o_bytes;
     return p;
 }
@@ -742,7 +774,7 @@ extern "C" size_t simpler_hip_pa_decode_workspace_size(const SimplerHipPaDecodeA
     if (validate(args) != SIMPLER_HIP_OK) return 0;
     const KernelPair k = pick_kernel(args);
     if (!k.main) return 0;
-    return make_plan(args, k.main).total;
+    return make_plan(args, k).total;
 }
 
 extern "C" int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
@@ -756,7 +788,7 @@ extern "C" int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, in
     if (rc != SIMPLER_HIP_OK) return rc;
     const KernelPair k = pick_kernel(args);
     if (!k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    if (num_workers) *num_workers = make_plan(args, k.main).workers;
+    if (num_workers) *num_workers = make_plan(args, k).workers;
     return SIMPLER_HIP_OK;
 }
 
@@ -778,7 +810,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     if (rc != SIMPLER_HIP_OK) return rc;
     const KernelPair k = pick_kernel(a);
     if (!k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    const Plan plan = make_plan(a, k.main);
+    const Plan plan = make_plan(a, k);
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
     if (a->batch == 0) return SIMPLER_HIP_OK;
 
@@ -806,6 +838,8 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.group = a->num_heads / a->num_kv_heads;
     P.rows = plan.rows;
     P.row_tiles = plan.row_tiles;
+    P.waves_per_worker = plan.waves_per_worker;
+    P.row_groups = plan.row_groups;
     P.block_size = a->block_size;
     P.max_blocks = a->max_blocks_per_seq;
     P.num_pool_blocks = a->num_blocks;
@@ -815,7 +849,8 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
-        hipLaunchKernelGGL(k.main, dim3((unsigned)plan.workers), dim3(64), 0, (hipStream_t)stream, P);
+        hipLaunchKernelGGL(plan.main, dim3((unsigned)plan.workers), dim3(64 * plan.waves_per_worker), 0,
+                           (hipStream_t)stream, P);
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     if (phases & SIMPLER_HIP_PHASE_MERGE) {

@@ -177,6 +177,12 @@ def test_worker_plan():
     # error word + two (m, l) and two O partial slots per worker, 256-byte aligned sections
     assert ws(num_workers=7) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
     assert ws(num_workers=1) == 256 + 256 + 2 * 16 * 128 * 4
+    # q_len 8 x group 4 = 32 rows = 2 row tiles: a worker is a 2-wave workgroup
+    # and keeps two partial slots per wave
+    assert pa.plan(_args(q_len=8, causal=1)) == 512
+    assert ws(q_len=8, causal=1, num_workers=7) == 256 + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
+    # 25 row tiles: 4-wave workgroups, one per CU
+    assert pa.plan(_args(num_heads=80, num_kv_heads=1, q_len=5, causal=1)) == 256
 
 
 def test_work_list_must_fit_32_bit_indices():

@@ -100,6 +100,19 @@ def test_causal_multi_token(q_len, device):
     assert_close(run_gpu(case, device), oracle_numpy(case), what=f"causal{q_len}")
 
 
+@pytest.mark.parametrize("heads,q_len,workers", [(8, 8, 0), (12, 4, 0), (12, 4, 7), (80, 5, 0), (80, 5, 1),
+                                                 (80, 5, 333)])
+def test_row_tiles_share_a_worker(heads, q_len, workers, device):
+    # one kv head, 16 rows per tile: 64 rows -> 4 tiles (one workgroup of 4
+    # waves), 48 -> 3, 400 -> 25 tiles (7 row groups of 4 waves, the last one
+    # with a single live wave)
+    print(f"[case] heads={heads} q_len={q_len} workers={workers}", flush=True)
+    case = make_custom_case(batch=3, num_heads=heads, kv_heads=1, head_dim=128,
+                            block_size=64, q_len=q_len, causal=True,
+                            context_lens=[q_len, 700, 2100], seed=310 + heads + q_len)
+    assert_close(run_gpu(case, device, num_workers=workers), oracle_numpy(case), what=f"rowtiles{heads}x{q_len}")
+
+
 def test_causal_fully_masked_last_block(device):
     # prefix ends on a block boundary: rows 0..q_len-2 see nothing of the last block
     case = make_custom_case(batch=1, num_heads=4, kv_heads=1, head_dim=64, block_size=16, q_len=4, causal=True,
