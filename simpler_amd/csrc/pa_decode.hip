@@ -67,6 +67,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+#define LDS_AS __attribute__((address_space(3)))
 
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
@@ -84,11 +86,12 @@ struct KernelParams {
     float *part_o;   // [workers][2 slots][16 rows][DV]
     float *part_ml;  // [workers][2 slots][m[16], l[16]]
     unsigned *error_flag;
+    const char *zeros;  // 256 bytes of the workspace that stay zero (LDS fill source)
     int64_t k_block_stride, k_token_stride, k_head_stride;
     int64_t v_block_stride, v_token_stride, v_head_stride;
     int32_t batch, q_len, num_heads, kv_heads, group, rows, row_tiles;
-    int32_t waves_per_worker;  // row tiles a worker workgroup runs side by side (one wave each)
-    int32_t row_groups;        // ceil(row_tiles / waves_per_worker): work-list tiles per kv head
+    int32_t tiles_per_worker;  // row tiles a worker workgroup runs side by side (one wave each)
+    int32_t row_groups;        // ceil(row_tiles / tiles_per_worker): work-list tiles per kv head
     int32_t block_size, max_blocks, num_pool_blocks;
     int32_t workers;
     float scale;
@@ -530,10 +533,10 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
         const int kvh = j / P.row_groups, rg = j - kvh * P.row_groups;
-        const int rt = rg * P.waves_per_worker + wave;  // this wave's row tile
+        const int rt = rg * P.tiles_per_worker + wave;  // this wave's row tile
         // A worker touches at most two tiles partially: the first and the last
         // of its slice (slots 0 and 1); tiles in between are finished here.
-        const int64_t piece = ((int64_t)w * P.waves_per_worker + wave) * 2 + slot;
+        const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
         float *po = P.part_o + piece * 16 * DV;
         float *pml = P.part_ml + piece * 32;
         if (rt < P.row_tiles) run_segment<BS, DK, DV, OutT, (MAXW > 1)>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
@@ -563,7 +566,7 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     const int tile = blockIdx.x;  // (batch, kv head, row tile)
     const int b = tile / tpb, jr = tile - b * tpb;
     const int kvh = jr / P.row_tiles, rt = jr - kvh * P.row_tiles;
-    const int rg = rt / P.waves_per_worker, wave = rt - rg * P.waves_per_worker;
+    const int rg = rt / P.tiles_per_worker, wave = rt - rg * P.tiles_per_worker;
     const int j = kvh * P.row_groups + rg;  // work-list tile
     const int rows_here = min(16, P.rows - rt * 16);
     int prefix = 0;
@@ -589,7 +592,7 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
         f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
         for (int w = w_first; w <= w_last; ++w) {
             const int slot = (w * chunk >= t0) ? 0 : 1;
-            const int64_t piece = ((int64_t)w * P.waves_per_worker + wave) * 2 + slot;
+            const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
             const float m = P.part_ml[piece * 32 + row];
             const float l = P.part_ml[piece * 32 + 16 + row];
             const f32x4_t po = *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
@@ -604,18 +607,359 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// MLA decode: one latent KV head shared by every query head (Hkv = 1 in the
+// DeepSeek shape, Dk = 576, Dv = 512), V = the first Dv dims of K.
+//
+// A worker workgroup of four waves owns 64 query rows (a "row group", 16 rows
+// per wave). Each KV block is copied from HBM into LDS with direct
+// global->LDS loads (double buffered: the next block is in flight during the
+// math on this one) and consumed by the four waves. The row groups of one
+// work slice run as sibling workgroups whose ids differ by multiples of 8, so
+// they land on the same XCD and the second reader of a block hits its L2.
+// Q (Dk/32 operand quads) and O^T (Dv x 16 rows, fp32) stay in registers:
+//   QK  S^T[token][row] = K[token][:] . Q[row][:]   MFMA 16x16x32 bf16,
+//       A = K rows from LDS (16-B reads), B = Q registers.
+//   PV  O^T[dim][row] += V^T[dim][token] . P^T[token][row]   MFMA 16x16x32,
+//       A = V^T from LDS by transposing reads (ds_read_b64_tr_b16),
+//       B = P^T, which is the QK result layout itself: lane l holds row l%16
+//       and, per 32-token k-step, tokens {4q..4q+3, 16+4q..16+4q+3}
+//       (q = l/16); the V^T reads pick the same token order.
+// Every lane of O^T holds a single query row, so the per-block rescale is one
+// scalar per lane. Numerics are the same per-block recipe as the decode kernel.
+//
+// LDS row layout: a token's Dk*2 bytes as 16-byte chunks, padded to a chunk
+// count = 12 (mod 16), with the low two chunk-index bits XORed by
+// sw(row) = ((row >> 1) & 2) | ((row >> 3) & 1). Then a K-operand read (16
+// rows x 16 B per 16 lanes) and a transposing V^T read (8 rows x 32 B per
+// half-wave) both touch 16 distinct 16-byte bank groups.
+// ---------------------------------------------------------------------------
+
+template <int DK>
+struct MlaLayout {
+    static constexpr int kChunks = DK / 8;                                           // 16-B chunks per token
+    static constexpr int kRowChunks = kChunks + ((12 - kChunks % 16) % 16 + 16) % 16;  // = 12 (mod 16)
+    static constexpr int kRowBytes = kRowChunks * 16;
+};
+
+__device__ __forceinline__ int mla_swizzle(int row) { return ((row >> 1) & 2) | ((row >> 3) & 1); }
+
+__device__ __forceinline__ u32x4_t lds_ld16(const char *base, uint32_t off) {
+    return *reinterpret_cast<const LDS_AS u32x4_t *>((const LDS_AS char *)base + off);
+}
+
+__device__ __forceinline__ i16x4_t lds_ld_tr(const char *base, uint32_t off) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4_t *)((LDS_AS char *)base + off));
+}
+
+constexpr int kMlaRowsPerGroup = 64;  // four waves x 16 rows
+
+// Work slice and row group of workgroup w. Row groups of a slice are
+// w, w+8, w+16, ...: the same XCD under round-robin workgroup dispatch.
+__device__ __forceinline__ void mla_worker(int w, int slices, int groups, int *slice, int *group) {
+    const int full = slices / 8;  // complete sets of 8 slices
+    const int per_set = 8 * groups;
+    const int set = w / per_set;
+    if (set < full) {
+        *slice = set * 8 + (w & 7);
+        *group = (w / 8) % groups;
+    } else {
+        const int rem = slices - full * 8;  // > 0 here
+        const int x = w - full * per_set;
+        *slice = full * 8 + x % rem;
+        *group = x / rem;
+    }
+}
+
+template <int BS, int DK, int DV, typename OutT>
+__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp, const int b,
+                                                const int kvh, const int nblk, const int blk_begin,
+                                                const int blk_end, const int slot, char *const smem0,
+                                                char *const smem1) {
+    using L = MlaLayout<DK>;
+    constexpr int RB = L::kRowBytes;
+    constexpr int RC = L::kRowChunks;
+    constexpr int KC = L::kChunks;
+    constexpr int NI = BS * RC / 64;  // 1 KB direct-to-LDS loads per block
+    constexpr int KS = DK / 32;       // QK k-steps
+    constexpr int NT = BS / 16;       // 16-token tiles
+    constexpr int PS = BS / 32;       // PV k-steps
+    constexpr int NC = DV / 16;       // O^T column tiles
+    static_assert(BS % 32 == 0 && (BS * RC) % 64 == 0, "block of whole 32-token k-steps");
+    static_assert(DK % 32 == 0 && DV % 32 == 0 && DV <= DK, "V is a prefix of K");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int q = lane >> 4, pc = lane & 15;
+    const int r0 = rgrp * kMlaRowsPerGroup + 16 * wave;  // first query row of this wave
+    const int rows_here = min(16, P.rows - r0);
+    const bool active = rows_here > 0;
+    int ctx = P.context_lens[b];
+    ctx = min(max(ctx, 0), P.max_blocks * BS);
+
+    // ---- Q (B operand of QK): row pc, dims 32kk+8q..+7 ----
+    u32x4_t qv[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+    int rowlen = 0;
+    if (pc < rows_here) {
+        const int r = r0 + pc;
+        const int i = r / P.group, hh = r - i * P.group;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK + 8 * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) qv[kk] = ld16(qrow + 32 * kk);
+        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+    }
+    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - r0 / P.group) : ctx;
+
+    const int32_t *bt_row = P.block_table + (int64_t)b * P.max_blocks;
+    int bt_base = blk_begin;
+    int bt_val = (blk_begin + lane < blk_end) ? bt_row[blk_begin + lane] : 0;
+    auto phys_of = [&](int blk, bool &bad) -> int {
+        if (blk - bt_base >= kBlockTableWindow) {
+            bt_base += kBlockTableWindow;
+            bt_val = (bt_base + lane < blk_end) ? bt_row[bt_base + lane] : 0;
+        }
+        const int phys = __builtin_amdgcn_readlane(bt_val, blk - bt_base);
+        bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
+        return bad ? 0 : phys;
+    };
+
+    const uint32_t tok_b32 = (uint32_t)(P.k_token_stride * 2);  // block bytes < 2^31 (host-checked)
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
+
+    // Direct-to-LDS fill of one block: LDS chunk p = 64*i + lane holds token
+    // p / RC, chunk (p % RC) ^ sw(token); tokens past the context, pad chunks
+    // and out-of-pool blocks read zeros. Wave `wave` issues loads i = wave (mod 4).
+    auto issue = [&](int blk, char *dst) -> bool {
+        bool bad = false;
+        const int phys = phys_of(blk, bad);
+        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
+        // (row, pos) of chunk 64*i + lane, stepped by 256 chunks per load; the
+        // empty asm keeps the compiler from hoisting all of them out of the
+        // block loop into registers.
+        int row = (64 * wave + lane) / RC;
+        int pos = (64 * wave + lane) - row * RC;
+        asm volatile("" : "+v"(row), "+v"(pos));
+#pragma unroll
+        for (int ii = 0; ii < (NI + 3) / 4; ++ii) {
+            const int i = ii * 4 + wave;
+            if (i < NI) {
+                const bool ok = row < vvalid && pos < KC;
+                const uint32_t off = (uint32_t)row * tok_b32 + ((uint32_t)(pos ^ mla_swizzle(row)) << 4);
+                const char *src = ok ? kb + off : P.zeros;
+                __builtin_amdgcn_global_load_lds(src, (LDS_AS void *)((LDS_AS char *)dst + 1024 * i), 16, 0, 0);
+            }
+            pos += 256 % RC;
+            row += 256 / RC;
+            if (pos >= RC) {
+                pos -= RC;
+                ++row;
+            }
+        }
+        return bad;
+    };
+
+    f32x4_t acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegClamp, f_run = kNegClamp, l_part = 0.f;
+
+    // per-lane LDS byte offsets within a block buffer
+    const uint32_t kofs = pc * RB + 16 * (q ^ mla_swizzle(pc));
+    const int vrow = 4 * q + (pc >> 2);
+    const int swv = mla_swizzle(vrow);
+    const uint32_t vbase = vrow * RB + 8 * (pc & 1);
+    const uint32_t vofs_even = vbase + 16 * (((pc & 3) >> 1) ^ swv);
+    const uint32_t vofs_odd = vbase + 16 * ((2 + ((pc & 3) >> 1)) ^ swv);
+
+    auto compute = [&](const char *kb, int blk, bool blk_bad) {
+        const bool first = (blk == blk_begin);
+        // ---- QK: one k-step per stage, the next k-step's K reads in flight ----
+        f32x4_t s[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) s[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        u32x4_t kf[2][NT];
+        auto load_k = [&](int kk, u32x4_t (&dst)[NT]) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) dst[t] = lds_ld16(kb, kofs + 64 * kk + t * 16 * RB);
+        };
+        load_k(0, kf[0]);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            if (kk + 1 < KS) load_k(kk + 1, kf[(kk + 1) & 1]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kk & 1][t]),
+                                                              __builtin_bit_cast(bf16x8_t, qv[kk]), s[t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- mask, scale, block max (golden :145-165) ----
+        const int blk0 = blk * BS;
+        const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
+        const int rvalid = blk_bad ? 0 : rowlen - blk0;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x = s[t][e] * P.scale;
+                if (!full) x = (16 * t + 4 * q + e < rvalid) ? x : -INFINITY;
+                s[t][e] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mb = fmaxf(mx, kNegClamp);
+        // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
+        const float mnew = first ? mb : fmaxf(m_run, mb);
+        const bool use = first || (mb >= mnew - kFrameGap);
+        const float alpha = first ? 0.f : __expf(m_run - mnew);
+        const float beta = __expf(mb - mnew);
+        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        // ---- p = bf16(exp(s - m_blk)), the PV B operand per 32-token k-step ----
+        u32x4_t pk[PS];
+        float lb = 0.f;
+#pragma unroll
+        for (int u = 0; u < PS; ++u) {
+            unsigned wv[4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const float p0 = use ? __expf(s[2 * u + hf][2 * e2] - mb) : 0.f;
+                    const float p1 = use ? __expf(s[2 * u + hf][2 * e2 + 1] - mb) : 0.f;
+                    const unsigned wd = pack_bf16x2(p0, p1);
+                    wv[2 * hf + e2] = wd;
+                    lb += bf16lo_to_f32(wd) + bf16hi_to_f32(wd);
+                }
+            pk[u] = (u32x4_t){wv[0], wv[1], wv[2], wv[3]};
+        }
+        l_part = first ? lb : alpha * l_part + beta * lb;
+        m_run = mnew;
+        if (use) f_run = mb;
+        // ---- A' = e^{f - m_blk} A + P V, column tile by column tile with the
+        // next tile's V^T reads in flight ----
+        i16x4_t vf[2][PS][2];
+        auto load_v = [&](int c, i16x4_t (&dst)[PS][2]) {
+            const uint32_t co = ((c & 1) ? vofs_odd : vofs_even) + 64 * (c >> 1);
+#pragma unroll
+            for (int u = 0; u < PS; ++u) {
+                dst[u][0] = lds_ld_tr(kb, co + u * 32 * RB);
+                dst[u][1] = lds_ld_tr(kb, co + u * 32 * RB + 16 * RB);
+            }
+        };
+        load_v(0, vf[0]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (c + 1 < NC) load_v(c + 1, vf[(c + 1) & 1]);
+            acc[c] *= cf;
+#pragma unroll
+            for (int u = 0; u < PS; ++u) {
+                const bf16x8_t va = __builtin_bit_cast(
+                    bf16x8_t, __builtin_shufflevector(vf[c & 1][u][0], vf[c & 1][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, __builtin_bit_cast(bf16x8_t, pk[u]), acc[c],
+                                                                0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- block loop: wait + barrier, prefetch the next block, math on this one ----
+    bool bad_cur = issue(blk_begin, smem0);
+    for (int blk = blk_begin; blk < blk_end; ++blk) {
+        const bool even = ((blk - blk_begin) & 1) == 0;
+        __syncthreads();  // this block's loads landed in every wave; the other buffer is free
+        bool bad_next = false;
+        if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
+        if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, 1u);
+        if (active) compute(even ? smem0 : smem1, blk, bad_cur);
+        bad_cur = bad_next;
+    }
+    __syncthreads();  // the buffers are refilled by the next segment
+    if (!active) return;
+
+    // ---- finish: l over the four lane groups; O = e^{f-m} A ----
+    float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    const float osc = __expf(f_run - m_run);
+    if (pc >= rows_here) return;
+    if (blk_begin == 0 && blk_end == nblk) {
+        const float inv = l_tot > 0.f ? osc / l_tot : 0.f;
+        const int64_t off = out_row_offset(P, b, kvh, r0 + pc, DV) + 4 * q;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) OutStore<OutT>::store4(P.out, off + 16 * c, acc[c] * inv);
+        return;
+    }
+    const int rt = rgrp * 4 + wave;  // row tile within the slice's tile
+    const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rt) * 2 + slot;
+    float *dst = P.part_o + (piece * 16 + pc) * DV + 4 * q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4_t *>(dst + 16 * c) = acc[c] * osc;
+    if (q == 0) {
+        P.part_ml[piece * 32 + pc] = m_run;
+        P.part_ml[piece * 32 + 16 + pc] = l_tot;
+    }
+}
+
+// Worker workgroup = four waves = one row group of one work slice. The work
+// list holds (batch, kv head, KV block) entries; every row group of a slice
+// walks the same entries.
+template <int BS, int DK, int DV, typename OutT>
+__global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
+    using L = MlaLayout<DK>;
+    __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
+    __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
+    const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
+    int slice = 0, rgrp = 0;
+    mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
+    const int tpb = P.kv_heads;  // work-list tiles per batch
+    int start = 0, end = 0, b = 0, prefix = 0;
+    locate_slice(P, slice, &start, &end, &b, &prefix);  // identical in every wave
+    if (start >= end) return;
+    int nb = blocks_of(P, b);
+    if (nb == 0) return;
+    const int rel = start - prefix;
+    int kvh = rel / nb;
+    int blk = rel - kvh * nb;
+    int pos = start;
+    int slot = 0;
+    while (pos < end && nb > 0) {
+        const int seg = min(end - pos, nb - blk);
+        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, b, kvh, nb, blk, blk + seg, slot, smem0, smem1);
+        pos += seg;
+        slot = 1;
+        if (pos >= end) break;
+        blk = 0;
+        if (++kvh == tpb) {
+            kvh = 0;
+            do {
+                ++b;
+                nb = blocks_of(P, b);
+            } while (nb == 0 && b + 1 < P.batch);
+        }
+    }
+}
+
 // ----------------------------------------------------------------------------
 // Host side: validation, worker count, dispatch
 // ----------------------------------------------------------------------------
 
 typedef void (*KernelFn)(KernelParams);
 
+constexpr int kZeroOffset = 128;  // workspace bytes [128, 256) are never written after init
+
 struct Plan {
     int workers;
     int row_tiles;
     int rows;
-    int waves_per_worker;
+    int tiles_per_worker;
     int row_groups;
+    int threads;  // per worker workgroup
+    int groups;   // workgroups per worker (MLA row groups), else 1
+    int64_t grid;
     KernelFn main;
     size_t flag_bytes, part_ml_bytes, part_o_bytes;
     size_t total;
@@ -655,20 +999,21 @@ int validate(const SimplerHipPaDecodeArgs *a) {
 }
 
 struct KernelPair {
-    KernelFn main;        // one wave per worker
+    KernelFn main;        // one wave per worker (MLA: the four-wave LDS kernel)
     KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     KernelFn merge;
+    bool mla;
 };
 
 template <int BS, int D, typename OutT>
 KernelPair pick_fn() {
     return {pa_decode_kernel<BS, D, D, OutT, 1>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker>,
-            pa_merge_kernel<D, OutT>};
+            pa_merge_kernel<D, OutT>, false};
 }
 
 template <int BS, typename OutT>
 KernelPair pick_d(int dk, int dv) {
-    if (dk != dv) return {nullptr, nullptr, nullptr};
+    if (dk != dv) return {nullptr, nullptr, nullptr, false};
     switch (dk) {
         case 16: return pick_fn<BS, 16, OutT>();
         case 32: return pick_fn<BS, 32, OutT>();
@@ -676,8 +1021,8 @@ KernelPair pick_d(int dk, int dv) {
         case 128: return pick_fn<BS, 128, OutT>();
         case 256:
             if constexpr (BS <= 64) return pick_fn<BS, 256, OutT>();
-            return {nullptr, nullptr, nullptr};
-        default: return {nullptr, nullptr, nullptr};
+            return {nullptr, nullptr, nullptr, false};
+        default: return {nullptr, nullptr, nullptr, false};
     }
 }
 
@@ -688,15 +1033,40 @@ KernelPair pick_bs(int bs, int dk, int dv) {
         case 32: return pick_d<32, OutT>(dk, dv);
         case 64: return pick_d<64, OutT>(dk, dv);
         case 128: return pick_d<128, OutT>(dk, dv);
-        default: return {nullptr, nullptr, nullptr};
+        default: return {nullptr, nullptr, nullptr, false};
+    }
+}
+
+// MLA: V is the first head_dim_v dims of K (same buffer, same strides).
+constexpr int kMlaDk = 576, kMlaDv = 512;
+
+bool is_mla_shape(const SimplerHipPaDecodeArgs *a) { return a->head_dim_k == kMlaDk && a->head_dim_v == kMlaDv; }
+
+bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
+    return a->value_cache == a->key_cache && a->v_block_stride == a->k_block_stride &&
+           a->v_token_stride == a->k_token_stride && a->v_head_stride == a->k_head_stride;
+}
+
+template <typename OutT>
+KernelPair pick_mla(int bs) {
+    switch (bs) {
+        case 32: return {pa_mla_kernel<32, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true};
+        case 64: return {pa_mla_kernel<64, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true};
+        default: return {nullptr, nullptr, nullptr, false};
     }
 }
 
 KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
+    if (is_mla_shape(a)) {
+        if (!v_is_k_prefix(a)) return {nullptr, nullptr, nullptr, false};
+        if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_mla<float>(a->block_size);
+        if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16) return pick_mla<__bf16>(a->block_size);
+        return {nullptr, nullptr, nullptr, false};
+    }
     if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_bs<float>(a->block_size, a->head_dim_k, a->head_dim_v);
     if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
         return pick_bs<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
-    return {nullptr, nullptr, nullptr};
+    return {nullptr, nullptr, nullptr, false};
 }
 
 // Default worker count: compute units x kWorkersPerCu workgroups, capped by
@@ -706,11 +1076,11 @@ KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
 // make the K streams of different waves evict each other's L1 lines.
 // Without a device (host-only builds and tests) an MI355X is assumed:
 // 256 CUs.
-int wave_slots(KernelFn fn, int waves_per_worker) {
+int wave_slots(KernelFn fn, int threads) {
     struct Entry {
         KernelFn fn;
         int device;
-        int waves;
+        int threads;
         int slots;
     };
     static std::mutex mu;
@@ -719,27 +1089,28 @@ int wave_slots(KernelFn fn, int waves_per_worker) {
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     std::lock_guard<std::mutex> lk(mu);
     for (const Entry &e : cache)
-        if (e.fn == fn && e.device == dev && e.waves == waves_per_worker) return e.slots;
+        if (e.fn == fn && e.device == dev && e.threads == threads) return e.slots;
     // kWorkersPerCu workgroups per CU, or as many as fit (a 4-wave workgroup
     // fills a CU at one wave per SIMD). Two 2-wave workers per CU measured
     // 195.5 us on the speculative-verify shape against 213.9 us with one.
     int per_cu = kWorkersPerCu;
     int cus = 256;
     // Without a device: the kernels use the whole register file of a SIMD
-    // (one wave per SIMD, four SIMDs per CU).
-    if (4 / waves_per_worker < per_cu) per_cu = 4 / waves_per_worker > 0 ? 4 / waves_per_worker : 1;
+    // (one wave per SIMD, four SIMDs per CU), the MLA kernel most of the LDS.
+    const int fit = 256 / threads;
+    if (fit < per_cu) per_cu = fit > 0 ? fit : 1;
     if (dev >= 0) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn),
-                                                         64 * waves_per_worker, 0) == hipSuccess &&
+                                                         threads, 0) == hipSuccess &&
             n > 0 && n < per_cu)
             per_cu = n;
     }
     (void)hipGetLastError();
     const int slots = cus * per_cu;
-    cache.push_back({fn, dev, waves_per_worker, slots});
+    cache.push_back({fn, dev, threads, slots});
     return slots;
 }
 
@@ -748,17 +1119,37 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
     p.row_tiles = (p.rows + 15) / 16;
-    // Row tiles of one kv head run as sibling waves of one worker workgroup
-    // (up to four), so K/V of a block is fetched once for all of them.
-    p.waves_per_worker = p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker;
-    p.row_groups = (p.row_tiles + p.waves_per_worker - 1) / p.waves_per_worker;
-    p.main = p.waves_per_worker > 1 ? k.main_multi : k.main;
-    p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.waves_per_worker);
+    if (k.mla) {
+        // A work slice runs as `groups` sibling workgroups of 64 rows (4 row
+        // tiles) each; `workers` counts slices.
+        p.groups = (p.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
+        p.tiles_per_worker = 4 * p.groups;
+        p.row_groups = 1;
+        p.threads = 256;
+        p.main = k.main;
+        if (a->num_workers > 0) {
+            p.workers = a->num_workers;
+        } else {
+            const int wgs = wave_slots(p.main, p.threads);
+            p.workers = wgs / p.groups > 0 ? wgs / p.groups : 1;
+        }
+        p.grid = (int64_t)p.workers * p.groups;
+    } else {
+        // Row tiles of one kv head run as sibling waves of one worker workgroup
+        // (up to four), so K/V of a block is fetched once for all of them.
+        p.tiles_per_worker = p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker;
+        p.threads = 64 * p.tiles_per_worker;
+        p.main = p.tiles_per_worker > 1 ? k.main_multi : k.main;
+        p.groups = 1;
+        p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
+        p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads);
+        p.grid = p.workers;
+    }
     const int dv = a->head_dim_v;
     // Layout: [error word] [m,l partials] [O partials]; two partial slots per
     // worker wave.
-    const size_t pieces = (size_t)p.workers * p.waves_per_worker * 2;
-    p.flag_bytes = 256;
+    const size_t pieces = (size_t)p.workers * p.tiles_per_worker * 2;
+    p.flag_bytes = 256;  // error word at 0, zeros at [kZeroOffset, 256)
     p.part_ml_bytes = align_up(pieces * 32 * sizeof(float), 256);
     p.part_o_bytes = align_up(pieces * 16 * dv * sizeof(float), 256);
     p.total = p.flag_bytes + p.part_ml_bytes + p.part_o_bytes;
@@ -793,8 +1184,10 @@ extern "C" int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, in
 }
 
 extern "C" const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args) {
-    if (validate(args) != SIMPLER_HIP_OK || !pick_kernel(args).main) return "";
-    return "pa_decode_kernel";
+    if (validate(args) != SIMPLER_HIP_OK) return "";
+    const KernelPair k = pick_kernel(args);
+    if (!k.main) return "";
+    return k.mla ? "pa_mla_kernel" : "pa_decode_kernel";
 }
 
 extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
@@ -823,6 +1216,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.out = a->out;
     char *ws = (char *)workspace;
     P.error_flag = (unsigned *)ws;
+    P.zeros = ws + kZeroOffset;
     P.part_ml = (float *)(ws + plan.flag_bytes);
     P.part_o = (float *)(ws + plan.flag_bytes + plan.part_ml_bytes);
     P.k_block_stride = a->k_block_stride;
@@ -838,7 +1232,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.group = a->num_heads / a->num_kv_heads;
     P.rows = plan.rows;
     P.row_tiles = plan.row_tiles;
-    P.waves_per_worker = plan.waves_per_worker;
+    P.tiles_per_worker = plan.tiles_per_worker;
     P.row_groups = plan.row_groups;
     P.block_size = a->block_size;
     P.max_blocks = a->max_blocks_per_seq;
@@ -849,7 +1243,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
-        hipLaunchKernelGGL(plan.main, dim3((unsigned)plan.workers), dim3(64 * plan.waves_per_worker), 0,
+        hipLaunchKernelGGL(plan.main, dim3((unsigned)plan.grid), dim3((unsigned)plan.threads), 0,
                            (hipStream_t)stream, P);
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }

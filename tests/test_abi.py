@@ -169,6 +169,34 @@ def test_host_validation_rejects_bad_arguments_without_launching():
     assert lib.simpler_hip_pa_decode(ctypes.byref(good), ctypes.c_void_p(0x100000), 16, None) == -4
 
 
+def _mla_args(**kw) -> _lib.PaDecodeArgs:
+    # DeepSeek MLA shape: V = the first 512 dims of the 576-dim latent K (same buffer, same strides)
+    base = dict(key_cache=0x2000, value_cache=0x2000, k_block_stride=64 * 576, k_token_stride=576,
+                k_head_stride=576, v_block_stride=64 * 576, v_token_stride=576, v_head_stride=576,
+                batch=128, num_heads=128, num_kv_heads=1, head_dim_k=576, head_dim_v=512, block_size=64,
+                max_blocks_per_seq=128)
+    base.update(kw)
+    return _args(**base)
+
+
+def test_mla_dispatch_and_plan():
+    lib = _lib.lib()
+    name = lambda a: lib.simpler_hip_pa_decode_kernel_name(ctypes.byref(a)).decode()
+    assert name(_mla_args()) == "pa_mla_kernel"
+    assert name(_mla_args(block_size=32)) == "pa_mla_kernel"
+    assert name(_args()) == "pa_decode_kernel"
+    # 128 query rows = two 64-row groups: 128 slices x 2 workgroups on a 256-CU device
+    assert pa.plan(_mla_args()) == 128
+    assert pa.plan(_mla_args(num_heads=16)) == 256
+    ws = lambda **kw: lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(_mla_args(**kw)))
+    # two partial slots per row tile (8 per slice), 16 rows x 512 fp32 each
+    assert ws(num_workers=3) == 256 + 3 * 8 * 2 * 32 * 4 + 3 * 8 * 2 * 16 * 512 * 4
+    # V that is not the K prefix (other buffer or strides), or a block size without 32-token steps
+    for bad in (_mla_args(value_cache=0x3000), _mla_args(v_token_stride=1152), _mla_args(block_size=16),
+                _mla_args(block_size=128)):
+        assert lib.simpler_hip_pa_decode(ctypes.byref(bad), ctypes.c_void_p(0x100000), 1 << 30, None) == -2
+
+
 def test_worker_plan():
     # without a device the launcher assumes an MI355X: 256 CUs x 2 worker waves each
     assert pa.plan(_args()) == 512

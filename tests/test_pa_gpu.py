@@ -195,6 +195,73 @@ def test_full_size_split_invariance_and_determinism(device):
     np.testing.assert_array_equal(outs[3].cpu().numpy(), ref)  # same plan, same bits
 
 
+# ---- MLA (one latent KV head, Dk=576, V = K[..., :512]) -------------------------------------------
+
+def _mla_case(*, heads, lens, seed, block_size=64, **kw):
+    return make_custom_case(batch=len(lens), num_heads=heads, kv_heads=1, head_dim=576, head_dim_v=512,
+                            block_size=block_size, context_lens=lens, seed=seed, mla=True, **kw)
+
+
+@pytest.mark.parametrize("heads,block_size,workers", [(128, 64, 0), (128, 64, 1), (128, 64, 7), (128, 32, 0),
+                                                       (16, 64, 0), (100, 64, 5), (192, 32, 3)])
+def test_mla_rows_blocks_and_workers(heads, block_size, workers, device):
+    # 128 rows = two 64-row groups; 16 rows leave three waves idle; 100 and 192
+    # rows leave part of the last group idle; 1..7 workers cut tiles into pieces
+    print(f"[case] mla heads={heads} bs={block_size} workers={workers}", flush=True)
+    case = _mla_case(heads=heads, lens=[1, block_size + 5, 700, 2100], seed=700 + heads + block_size)
+    assert_close(run_gpu(case, device, num_workers=workers), oracle_numpy(case), what=f"mla h{heads}")
+
+
+def test_mla_empty_context_and_bf16_out(device):
+    case = _mla_case(heads=128, lens=[0, 33, 64, 1000], seed=710)
+    got = run_gpu(case, device, out_dtype=torch.bfloat16)
+    assert np.all(got[0] == 0)
+    ref = torch.tensor(oracle_numpy(case)).to(torch.bfloat16).float().numpy()
+    assert_close(got, ref, what="mla empty/bf16")
+
+
+def test_mla_garbage_past_context_is_ignored(device):
+    case = _mla_case(heads=128, lens=[100, 70], seed=720)
+    ref = oracle_numpy(case)
+    kc = case.key_cache.clone()
+    for b, n in enumerate(case.context_lens.tolist()):
+        blk = int(case.block_table[b, n // 64])
+        kc[blk, n % 64:] = float("nan")  # tokens past the context in the last block
+    case.key_cache, case.value_cache = kc, kc[..., :512]
+    assert_close(run_gpu(case, device), ref, what="mla garbage tail")
+
+
+def test_mla_out_of_pool_block_is_reported(device):
+    case = _mla_case(heads=128, lens=[200], seed=730)
+    case.block_table[0, 1] = 10_000
+    got = run_gpu(case, device)
+    with pytest.raises(pa.PagedAttentionError):
+        pa.check_errors(device)
+    pa.check_errors(device)  # cleared
+    assert np.all(np.isfinite(got))
+
+
+def test_mla_cfg4_reduced_batch(device):
+    # cfg4 per-sequence shape (128 heads, Dk 576, BS 64, L~U[512,8192]) on 16 sequences against the C oracle
+    case = make_case("cfg4_mla", batch_override=16)
+    assert_close(run_gpu(case, device), oracle_c(case, n_threads=16), what="cfg4 x16")
+
+
+def test_mla_cfg4_full_size_invariance(device):
+    case = make_case("cfg4_mla").to(device)
+    outs = []
+    for workers in (0, 61, 0):
+        out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+        pa.paged_attention_decode(case.query, case.key_cache, case.value_cache, case.block_table,
+                                  case.context_lens, out, case.scale, num_workers=workers)
+        outs.append(out)
+    torch.cuda.synchronize(device)
+    ref = outs[0].cpu().numpy()
+    assert np.all(np.isfinite(ref))
+    assert_close(outs[1].cpu().numpy(), ref, max_abs=1e-4, rel_l2=1e-5, what="mla worker-count invariance")
+    np.testing.assert_array_equal(outs[2].cpu().numpy(), ref)  # same plan, same bits
+
+
 def test_workspace_reused_across_plans(device):
     # Regression: a workspace reused by a call with a different shape and worker
     # count must not leak state from the previous call into the next.
