@@ -42,6 +42,10 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
         "-fvisibility=hidden",
         # packed fp32 ops (v_pk_*_f32) are disabled for all device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: the kernels rescale them with VALU ops
+        # every KV block, which AGPR accumulators would route through
+        # v_accvgpr moves (measured 10% on the MLA kernel, neutral elsewhere)
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         f"-I{ROOT / 'include'}",
         "-Wno-unused-command-line-argument",
         *(extra_flags or []),

@@ -629,21 +629,20 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
 // Every lane of O^T holds a single query row, so the per-block rescale is one
 // scalar per lane. Numerics are the same per-block recipe as the decode kernel.
 //
-// LDS row layout: a token's Dk*2 bytes as 16-byte chunks, padded to a chunk
-// count = 12 (mod 16), with the low two chunk-index bits XORed by
-// sw(row) = ((row >> 1) & 2) | ((row >> 3) & 1). Then a K-operand read (16
-// rows x 16 B per 16 lanes) and a transposing V^T read (8 rows x 32 B per
-// half-wave) both touch 16 distinct 16-byte bank groups.
+// LDS row layout: a token's Dk*2 bytes as 16-byte chunks, the row padded to a
+// chunk count = 10 (mod 16): 74 chunks (1184 B) for Dk = 576. Measured on
+// MI355X with the kernel's exact access patterns, that stride runs both the
+// K-operand reads (16 rows x 16 B per 16 lanes) and the transposing V^T reads
+// at full LDS speed (534-548 and 420-427 B/ns per CU), where 73, 76 and 77
+// chunks, with or without XOR swizzles of the chunk index, halve one of them.
 // ---------------------------------------------------------------------------
 
 template <int DK>
 struct MlaLayout {
     static constexpr int kChunks = DK / 8;                                           // 16-B chunks per token
-    static constexpr int kRowChunks = kChunks + ((12 - kChunks % 16) % 16 + 16) % 16;  // = 12 (mod 16)
+    static constexpr int kRowChunks = kChunks + ((10 - kChunks % 16) % 16 + 16) % 16;  // = 10 (mod 16)
     static constexpr int kRowBytes = kRowChunks * 16;
 };
-
-__device__ __forceinline__ int mla_swizzle(int row) { return ((row >> 1) & 2) | ((row >> 3) & 1); }
 
 __device__ __forceinline__ u32x4_t lds_ld16(const char *base, uint32_t off) {
     return *reinterpret_cast<const LDS_AS u32x4_t *>((const LDS_AS char *)base + off);
@@ -672,16 +671,57 @@ __device__ __forceinline__ void mla_worker(int w, int slices, int groups, int *s
     }
 }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer loads straight into LDS (lane l -> LDS base + size*l). Lanes whose
+// offset is at or past the descriptor's record count are not fetched and
+// write zeros. Issued as inline asm on purpose: the compiler's wait
+// insertion would otherwise treat every later LDS read (the transposing reads
+// in particular) as possibly aliasing the fill and wait for all outstanding
+// vector memory before it, which serialises the next block's fill with this
+// block's math. Completion is instead awaited explicitly (s_waitcnt vmcnt at
+// the block barrier); loads the compiler does not count can only make its
+// own vmcnt waits stricter, since vector memory completes in order.
+// m0 holds the wave's LDS destination; nothing else in these kernels uses it.
+// One wait state separates the m0 write from the LDS-DMA load that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_fill16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_fill4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr_of(const char *p) {
+    return (uint32_t)(uintptr_t)(const LDS_AS char *)p;
+}
+
+// Raw buffer descriptor (stride 0, num_records in bytes). The values are
+// wave-uniform; readfirstlane puts them in scalar registers so the load needs
+// no per-lane descriptor loop.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t num_records) {
+    const uint64_t a = (uint64_t)base;
+    return (i32x4_t){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                     __builtin_amdgcn_readfirstlane((int)num_records), 0x00020000};
+}
+
 template <int BS, int DK, int DV, typename OutT>
-__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp, const int b,
-                                                const int kvh, const int nblk, const int blk_begin,
-                                                const int blk_end, const int slot, char *const smem0,
-                                                char *const smem1) {
+__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
+                                                const int groups, const int b, const int kvh, const int nblk,
+                                                const int blk_begin, const int blk_end, const int slot,
+                                                char *const smem0, char *const smem1, char *const sink) {
     using L = MlaLayout<DK>;
     constexpr int RB = L::kRowBytes;
     constexpr int RC = L::kRowChunks;
     constexpr int KC = L::kChunks;
     constexpr int NI = BS * RC / 64;  // 1 KB direct-to-LDS loads per block
+    constexpr int NII = (NI + 3) / 4; // of which each wave issues at most NII
     constexpr int KS = DK / 32;       // QK k-steps
     constexpr int NT = BS / 16;       // 16-token tiles
     constexpr int PS = BS / 32;       // PV k-steps
@@ -713,115 +753,171 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
     }
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - r0 / P.group) : ctx;
 
-    const int32_t *bt_row = P.block_table + (int64_t)b * P.max_blocks;
-    int bt_base = blk_begin;
-    int bt_val = (blk_begin + lane < blk_end) ? bt_row[blk_begin + lane] : 0;
+    // Block-table entries are read through the scalar cache (constant
+    // address space): the load is counted by lgkmcnt, so waiting for it never
+    // waits for the vector-memory loads in flight (block fill, L2 prefetch).
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
     auto phys_of = [&](int blk, bool &bad) -> int {
-        if (blk - bt_base >= kBlockTableWindow) {
-            bt_base += kBlockTableWindow;
-            bt_val = (bt_base + lane < blk_end) ? bt_row[bt_base + lane] : 0;
-        }
-        const int phys = __builtin_amdgcn_readlane(bt_val, blk - bt_base);
+        const int phys = bt_row[blk];
         bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
         return bad ? 0 : phys;
     };
 
-    const uint32_t tok_b32 = (uint32_t)(P.k_token_stride * 2);  // block bytes < 2^31 (host-checked)
+    // ---- direct-to-LDS fill: LDS chunk p = 64*i + lane holds token p / RC,
+    // chunk p % RC. The per-lane byte offsets within a KV block
+    // are the same for every block; pad chunks re-read chunk 0 of their token.
+    // The descriptor's record count (valid tokens x token bytes, 0 for an
+    // out-of-pool block) makes every later token read zeros. ----
+    const uint32_t tok_b = (uint32_t)(P.k_token_stride * 2);  // block bytes < 2^31 (host-checked)
     const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
-
-    // Direct-to-LDS fill of one block: LDS chunk p = 64*i + lane holds token
-    // p / RC, chunk (p % RC) ^ sw(token); tokens past the context, pad chunks
-    // and out-of-pool blocks read zeros. Wave `wave` issues loads i = wave (mod 4).
+    uint32_t voff[NII];
+#pragma unroll
+    for (int ii = 0; ii < NII; ++ii) {
+        const int pch = 64 * (4 * ii + wave) + lane;
+        const int row = pch / RC, pos = pch - row * RC;
+        voff[ii] = (uint32_t)row * tok_b + (pos < KC ? (uint32_t)pos << 4 : 0u);
+    }
+    // ---- L2 prefetch two blocks ahead: this row group's share of the block's
+    // 128-byte lines (tokens r with r % groups == rgrp), each touched by one
+    // 4-byte load into a scratch LDS slot, so the block's later fill is an L2
+    // hit for both row groups. Tokens past the context are not fetched. ----
+    constexpr int LPR = (DK * 2 + 127) / 128;  // lines per token
+    constexpr int NPF = (BS * LPR + 255) / 256;
+    // Every lane issues all NPF loads (lanes without a line of their own touch
+    // the group's first line again), so each wave has exactly NPF prefetch
+    // loads outstanding after its block fill: see the barrier below.
+    uint32_t pfoff[NPF];
+#pragma unroll
+    for (int pi = 0; pi < NPF; ++pi) {
+        const int idx = pi * 256 + (int)threadIdx.x;
+        const int rl = idx / LPR, ln = idx - rl * LPR;
+        const int row = rl * groups + rgrp;
+        pfoff[pi] = row < BS ? (uint32_t)row * tok_b + 128u * ln : (uint32_t)rgrp * tok_b;
+    }
+    auto prefetch = [&](int blk) {
+        bool bad = false;
+        const int phys = phys_of(blk, bad);
+        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
+        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
+        const uint32_t sink_addr = lds_addr_of(sink);
+#pragma unroll
+        for (int pi = 0; pi < NPF; ++pi) lds_fill4(rsrc, pfoff[pi], sink_addr);
+    };
     auto issue = [&](int blk, char *dst) -> bool {
         bool bad = false;
         const int phys = phys_of(blk, bad);
         const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
-        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
-        // (row, pos) of chunk 64*i + lane, stepped by 256 chunks per load; the
-        // empty asm keeps the compiler from hoisting all of them out of the
-        // block loop into registers.
-        int row = (64 * wave + lane) / RC;
-        int pos = (64 * wave + lane) - row * RC;
-        asm volatile("" : "+v"(row), "+v"(pos));
+        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
+        const uint32_t dst_addr = lds_addr_of(dst) + 1024u * wave;
 #pragma unroll
-        for (int ii = 0; ii < (NI + 3) / 4; ++ii) {
-            const int i = ii * 4 + wave;
-            if (i < NI) {
-                const bool ok = row < vvalid && pos < KC;
-                const uint32_t off = (uint32_t)row * tok_b32 + ((uint32_t)(pos ^ mla_swizzle(row)) << 4);
-                const char *src = ok ? kb + off : P.zeros;
-                __builtin_amdgcn_global_load_lds(src, (LDS_AS void *)((LDS_AS char *)dst + 1024 * i), 16, 0, 0);
-            }
-            pos += 256 % RC;
-            row += 256 / RC;
-            if (pos >= RC) {
-                pos -= RC;
-                ++row;
-            }
+        for (int ii = 0; ii < NII; ++ii) {
+            const int i = 4 * ii + wave;
+            if (NI % 4 == 0 || i < NI) lds_fill16(rsrc, voff[ii], dst_addr + 4096u * ii);
         }
         return bad;
     };
 
+    // O^T accumulators and the row-sum tile (ones x P^T: every lane holds its
+    // row's sum), both in the frame of the latest used block max f.
     f32x4_t acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegClamp, f_run = kNegClamp, l_part = 0.f;
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegClamp, f_run = kNegClamp;
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    constexpr float kLog2e = 1.4426950408889634f;
 
     // per-lane LDS byte offsets within a block buffer
-    const uint32_t kofs = pc * RB + 16 * (q ^ mla_swizzle(pc));
-    const int vrow = 4 * q + (pc >> 2);
-    const int swv = mla_swizzle(vrow);
-    const uint32_t vbase = vrow * RB + 8 * (pc & 1);
-    const uint32_t vofs_even = vbase + 16 * (((pc & 3) >> 1) ^ swv);
-    const uint32_t vofs_odd = vbase + 16 * ((2 + ((pc & 3) >> 1)) ^ swv);
+    const uint32_t kofs = pc * RB + 16 * q;
+    const uint32_t vbase = (4 * q + (pc >> 2)) * RB + 8 * (pc & 1);
+    const uint32_t vofs_even = vbase + 16 * ((pc & 3) >> 1);
+    const uint32_t vofs_odd = vofs_even + 32;
 
+    // Scheduling: LDS reads are issued two stages ahead of the MFMAs that
+    // consume them (an LDS read takes longer than one stage of MFMAs), and the
+    // group barriers pin the order of reads, VALU work and MFMAs in a stage.
+    constexpr int kDsRead = 0x100, kValu = 0x002, kMfma = 0x008;
     auto compute = [&](const char *kb, int blk, bool blk_bad) {
         const bool first = (blk == blk_begin);
-        // ---- QK: one k-step per stage, the next k-step's K reads in flight ----
+        // ---- QK: stage = one 32-dim k-step over the NT token tiles ----
         f32x4_t s[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) s[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-        u32x4_t kf[2][NT];
+        u32x4_t kf[3][NT];
         auto load_k = [&](int kk, u32x4_t (&dst)[NT]) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) dst[t] = lds_ld16(kb, kofs + 64 * kk + t * 16 * RB);
         };
         load_k(0, kf[0]);
+        load_k(1, kf[1]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
-            if (kk + 1 < KS) load_k(kk + 1, kf[(kk + 1) & 1]);
+            if (kk + 2 < KS) load_k(kk + 2, kf[(kk + 2) % 3]);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
-                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kk & 1][t]),
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kk % 3][t]),
                                                               __builtin_bit_cast(bf16x8_t, qv[kk]), s[t], 0, 0, 0);
+            if (kk + 2 < KS) __builtin_amdgcn_sched_group_barrier(kDsRead, NT, 0);
+            __builtin_amdgcn_sched_group_barrier(kMfma, NT, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // ---- mask, scale, block max (golden :145-165) ----
+
+        // ---- PV operand reads for the first two stages go out before the
+        // softmax math (they do not depend on it) ----
+        constexpr int NSC = NC / 2;  // PV stages of two O^T column tiles
+        i16x4_t vf[3][2][PS][2];
+        auto load_v = [&](int sc, i16x4_t (&dst)[2][PS][2]) {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int c = 2 * sc + cc;
+                const uint32_t co = (cc ? vofs_odd : vofs_even) + 64 * (c >> 1);
+#pragma unroll
+                for (int u = 0; u < PS; ++u) {
+                    dst[cc][u][0] = lds_ld_tr(kb, co + u * 32 * RB);
+                    dst[cc][u][1] = lds_ld_tr(kb, co + u * 32 * RB + 16 * RB);
+                }
+            }
+        };
+        load_v(0, vf[0]);
+        load_v(1, vf[1]);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- mask, block max of s*scale (golden :145-165). For scale > 0 the
+        // max of the scaled scores is the scaled max; otherwise scale first ----
+        float sc = P.scale;
+        if (!(sc > 0.f)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
         const int blk0 = blk * BS;
         const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
-        const int rvalid = blk_bad ? 0 : rowlen - blk0;
+        if (!full) {
+            const int rvalid = blk_bad ? 0 : rowlen - blk0;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * q + e >= rvalid) s[t][e] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x = s[t][e] * P.scale;
-                if (!full) x = (16 * t + 4 * q + e < rvalid) ? x : -INFINITY;
-                s[t][e] = x;
-                mx = fmaxf(mx, x);
-            }
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mb = fmaxf(mx, kNegClamp);
-        // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
+        const float mb = fmaxf(mx * sc, kNegClamp);
+        // ---- online merge (aiv_online_update.cpp:183-207) in the block frame ----
         const float mnew = first ? mb : fmaxf(m_run, mb);
         const bool use = first || (mb >= mnew - kFrameGap);
-        const float alpha = first ? 0.f : __expf(m_run - mnew);
-        const float beta = __expf(mb - mnew);
         const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
-        // ---- p = bf16(exp(s - m_blk)), the PV B operand per 32-token k-step ----
+        // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e - m_blk*log2e)) ----
+        const float mb2 = use ? mb * kLog2e : INFINITY;  // a skipped block gives p = 0
+        const float sc2 = sc * kLog2e;
         u32x4_t pk[PS];
-        float lb = 0.f;
 #pragma unroll
         for (int u = 0; u < PS; ++u) {
             unsigned wv[4];
@@ -829,51 +925,77 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int e2 = 0; e2 < 2; ++e2) {
-                    const float p0 = use ? __expf(s[2 * u + hf][2 * e2] - mb) : 0.f;
-                    const float p1 = use ? __expf(s[2 * u + hf][2 * e2 + 1] - mb) : 0.f;
-                    const unsigned wd = pack_bf16x2(p0, p1);
-                    wv[2 * hf + e2] = wd;
-                    lb += bf16lo_to_f32(wd) + bf16hi_to_f32(wd);
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2], sc2, -mb2));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2 + 1], sc2, -mb2));
+                    wv[2 * hf + e2] = pack_bf16x2(p0, p1);
                 }
             pk[u] = (u32x4_t){wv[0], wv[1], wv[2], wv[3]};
         }
-        l_part = first ? lb : alpha * l_part + beta * lb;
         m_run = mnew;
         if (use) f_run = mb;
-        // ---- A' = e^{f - m_blk} A + P V, column tile by column tile with the
-        // next tile's V^T reads in flight ----
-        i16x4_t vf[2][PS][2];
-        auto load_v = [&](int c, i16x4_t (&dst)[PS][2]) {
-            const uint32_t co = ((c & 1) ? vofs_odd : vofs_even) + 64 * (c >> 1);
+        // l (sum of the rounded p) on the matrix unit: ones x P^T
+        lacc *= cf;
 #pragma unroll
-            for (int u = 0; u < PS; ++u) {
-                dst[u][0] = lds_ld_tr(kb, co + u * 32 * RB);
-                dst[u][1] = lds_ld_tr(kb, co + u * 32 * RB + 16 * RB);
+        for (int u = 0; u < PS; ++u)
+            lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8_t, pk[u]), lacc, 0, 0, 0);
+        acc[0] *= cf;
+        acc[1] *= cf;
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- A' = e^{f - m_blk} A + P V: stage sc = column tiles 2sc, 2sc+1;
+        // the next stage's tiles are rescaled between this stage's MFMAs ----
+#pragma unroll
+        for (int sc = 0; sc < NSC; ++sc) {
+            if (sc + 2 < NSC) load_v(sc + 2, vf[(sc + 2) % 3]);
+            if (sc + 1 < NSC) {
+                acc[2 * sc + 2] *= cf;
+                acc[2 * sc + 3] *= cf;
             }
-        };
-        load_v(0, vf[0]);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            if (c + 1 < NC) load_v(c + 1, vf[(c + 1) & 1]);
-            acc[c] *= cf;
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-            for (int u = 0; u < PS; ++u) {
-                const bf16x8_t va = __builtin_bit_cast(
-                    bf16x8_t, __builtin_shufflevector(vf[c & 1][u][0], vf[c & 1][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
-                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, __builtin_bit_cast(bf16x8_t, pk[u]), acc[c],
-                                                                0, 0, 0);
+                for (int u = 0; u < PS; ++u) {
+                    const bf16x8_t va = __builtin_bit_cast(
+                        bf16x8_t,
+                        __builtin_shufflevector(vf[sc % 3][cc][u][0], vf[sc % 3][cc][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[2 * sc + cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        va, __builtin_bit_cast(bf16x8_t, pk[u]), acc[2 * sc + cc], 0, 0, 0);
+                }
+            if (sc + 2 < NSC) __builtin_amdgcn_sched_group_barrier(kDsRead, 4 * PS, 0);
+#pragma unroll
+            for (int g2 = 0; g2 < 2 * PS; ++g2) {
+                __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+                if (sc + 1 < NSC) __builtin_amdgcn_sched_group_barrier(kValu, 8 / (2 * PS), 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // ---- block loop: wait + barrier, prefetch the next block, math on this one ----
+    // ---- block loop: wait + barrier, fill the other buffer with the next
+    // block, prefetch the one after into L2, math on this one ----
+    // Vector memory ops complete in order. At the top of iteration blk this
+    // wave has outstanding: the fill of blk, then (if issued) the NPF prefetch
+    // loads of blk+1. Waiting for "at most NPF outstanding" therefore
+    // completes the fill and leaves the prefetch in flight; with no prefetch
+    // issued the wait is for zero. lgkmcnt(0): this wave's LDS reads of the
+    // buffer about to be refilled are done.
+    // s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    constexpr unsigned kWaitFillOnly = 0x0070u | ((unsigned)NPF & 15u) | (((unsigned)NPF >> 4) << 14);
+    constexpr unsigned kWaitAll = 0x0070u;  // vmcnt(0) expcnt(7) lgkmcnt(0)
+    static_assert(NPF < 64, "vmcnt range");
     bool bad_cur = issue(blk_begin, smem0);
     for (int blk = blk_begin; blk < blk_end; ++blk) {
         const bool even = ((blk - blk_begin) & 1) == 0;
-        __syncthreads();  // this block's loads landed in every wave; the other buffer is free
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk > blk_begin && blk + 1 < blk_end)  // prefetch of blk+1 was issued after the fill of blk
+            __builtin_amdgcn_s_waitcnt(kWaitFillOnly);
+        else
+            __builtin_amdgcn_s_waitcnt(kWaitAll);
+        __builtin_amdgcn_s_barrier();  // every wave's fill landed; the other buffer is free
+        __builtin_amdgcn_sched_barrier(0);
         bool bad_next = false;
         if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
+        if (blk + 2 < blk_end) prefetch(blk + 2);
         if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, 1u);
         if (active) compute(even ? smem0 : smem1, blk, bad_cur);
         bad_cur = bad_next;
@@ -881,13 +1003,12 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
     __syncthreads();  // the buffers are refilled by the next segment
     if (!active) return;
 
-    // ---- finish: l over the four lane groups; O = e^{f-m} A ----
-    float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
+    // ---- finish: O = e^{f-m} A, l = e^{f-m} L ----
     const float osc = __expf(f_run - m_run);
+    const float l_tot = lacc[0] * osc;
     if (pc >= rows_here) return;
     if (blk_begin == 0 && blk_end == nblk) {
-        const float inv = l_tot > 0.f ? osc / l_tot : 0.f;
+        const float inv = lacc[0] > 0.f ? 1.f / lacc[0] : 0.f;  // the frame factor cancels
         const int64_t off = out_row_offset(P, b, kvh, r0 + pc, DV) + 4 * q;
 #pragma unroll
         for (int c = 0; c < NC; ++c) OutStore<OutT>::store4(P.out, off + 16 * c, acc[c] * inv);
@@ -912,12 +1033,18 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     using L = MlaLayout<DK>;
     __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
+    __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
     const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
     int slice = 0, rgrp = 0;
     mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
     const int tpb = P.kv_heads;  // work-list tiles per batch
     int start = 0, end = 0, b = 0, prefix = 0;
     locate_slice(P, slice, &start, &end, &b, &prefix);  // identical in every wave
+    // wave-uniform values, kept in scalar registers
+    start = __builtin_amdgcn_readfirstlane(start);
+    end = __builtin_amdgcn_readfirstlane(end);
+    b = __builtin_amdgcn_readfirstlane(b);
+    prefix = __builtin_amdgcn_readfirstlane(prefix);
     if (start >= end) return;
     int nb = blocks_of(P, b);
     if (nb == 0) return;
@@ -928,7 +1055,8 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, b, kvh, nb, blk, blk + seg, slot, smem0, smem1);
+        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0, smem1,
+                                          sink);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
