@@ -26,8 +26,11 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 DEFAULT_CONFIG = "cfg2_qwen3_8b"
-METRIC = "decode-attn KV-read GB/s (Qwen3-8B GQA decode, bs=32)"
+# The headline metric, quoted on the default workload; other --config runs
+# carry their workload name after it.
+METRIC = "decode-attn KV-read GB/s & % HBM peak; µs/step at Qwen3-8B shape bs=32"
 
 
 def parse() -> argparse.Namespace:
@@ -115,6 +118,7 @@ def main() -> int:
     pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
                          case.scale, causal=cfg.causal, num_workers=args.workers)
     workers = pa.plan(pargs)
+    kernel_name = pa.kernel_name(pargs)
     stream = torch.cuda.current_stream(dev)
 
     if args.calibrate_copy_mib > 0:
@@ -174,7 +178,7 @@ def main() -> int:
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
     line = {
-        "metric": METRIC,
+        "metric": METRIC if cfg.name == DEFAULT_CONFIG else f"{METRIC} [{cfg.name}]",
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -209,12 +213,13 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(main_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "pa_decode_kernel",
+            "kernel": kernel_name,
             "kernel_us": round(main_ms * 1e3, 2),
             "algorithmic_bytes": nbytes,
             "kv_bytes": kv_bytes(case_cpu),
             "step_frac": round(gbs / HBM_PEAK_GBS, 4),
             "tflops": round(flops / (main_ms * 1e-3) / 1e12, 3),
+            "mfma_frac": round(flops / (main_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         },
         "cpu_baseline": cpu,
     }

@@ -555,13 +555,15 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
 }
 
 // ---------------------------------------------------------------------------
-// Merge kernel: one wavefront per tile; log-sum-exp merge of the pieces
+// Merge kernel: one 256-thread workgroup per tile; log-sum-exp merge of the pieces
 // (pa_kernel.cce:1666-1773 CombineScale), and zeros for empty contexts.
 // ---------------------------------------------------------------------------
 
+constexpr int kMergeThreads = 256;
+
 template <int DV, typename OutT>
-__global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
-    const int lane = threadIdx.x;
+__global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelParams P) {
+    const int tid = threadIdx.x;
     const int tpb = P.kv_heads * P.row_tiles;
     const int tile = blockIdx.x;  // (batch, kv head, row tile)
     const int b = tile / tpb, jr = tile - b * tpb;
@@ -573,7 +575,7 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
     const int nb = blocks_of(P, b);
     if (nb == 0) {  // empty context: defined as a zero output
-        for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
+        for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
             const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
             OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4,
                                    (f32x4_t){0.f, 0.f, 0.f, 0.f});
@@ -584,23 +586,25 @@ __global__ void __launch_bounds__(64) pa_merge_kernel(const KernelParams P) {
     const int t0 = prefix + j * nb;
     const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;
     if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
-    // Online log-sum-exp over the pieces in one pass: every piece's loads are
-    // independent, so they are all in flight together.
-    for (int idx = lane; idx < rows_here * (DV / 4); idx += 64) {
+    // Log-sum-exp over the pieces: the row max and total l from the (m, l)
+    // pairs first, then O = sum_w e^{m_w - M} O_w / L, whose piece loads do not
+    // depend on each other and stay in flight together.
+    auto piece_of = [&](int w) -> int64_t {
+        const int slot = (w * chunk >= t0) ? 0 : 1;
+        return ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
+    };
+    for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
         const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
-        float M = -INFINITY, L = 0.f;
+        float M = -INFINITY;
+        for (int w = w_first; w <= w_last; ++w) M = fmaxf(M, P.part_ml[piece_of(w) * 32 + row]);
+        float L = 0.f;
         f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
         for (int w = w_first; w <= w_last; ++w) {
-            const int slot = (w * chunk >= t0) ? 0 : 1;
-            const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
-            const float m = P.part_ml[piece * 32 + row];
-            const float l = P.part_ml[piece * 32 + 16 + row];
-            const f32x4_t po = *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
-            const float Mn = fmaxf(M, m);
-            const float a = __expf(M - Mn), c = __expf(m - Mn);
-            L = a * L + c * l;
-            o = a * o + c * po;
-            M = Mn;
+            const int64_t piece = piece_of(w);
+            const float c = __expf(P.part_ml[piece * 32 + row] - M);
+            L += c * P.part_ml[piece * 32 + 16 + row];
+            o += c * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
         }
         const f32x4_t res = L > 0.f ? o / L : (f32x4_t){0.f, 0.f, 0.f, 0.f};
         OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, res);
@@ -1376,7 +1380,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     if (phases & SIMPLER_HIP_PHASE_MERGE) {
-        hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(64), 0, (hipStream_t)stream, P);
+        hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(kMergeThreads), 0, (hipStream_t)stream, P);
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     return SIMPLER_HIP_OK;

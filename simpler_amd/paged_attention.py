@@ -203,12 +203,21 @@ def check_errors(device: torch.device | None = None) -> None:
 
 
 def plan(args: _lib.PaDecodeArgs) -> int:
-    """Number of worker wavefronts a launch with ``args`` uses on the current device."""
+    """Number of workers (work-list slices) a launch with ``args`` uses on the current device.
+
+    A worker is one workgroup for the decode kernel and one slice run by
+    ceil(rows / 64) sibling workgroups for the MLA kernel.
+    """
     n = ctypes.c_int32()
     rc = _lib.lib().simpler_hip_pa_decode_plan(ctypes.byref(args), ctypes.byref(n))
     if rc != 0:
         raise PagedAttentionError(rc, "simpler_hip_pa_decode_plan")
     return n.value
+
+
+def kernel_name(args: _lib.PaDecodeArgs) -> str:
+    """Name of the main kernel a launch with ``args`` runs ("" if unsupported)."""
+    return _lib.lib().simpler_hip_pa_decode_kernel_name(ctypes.byref(args)).decode()
 
 
 # ---------------------------------------------------------------------------
