@@ -39,6 +39,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default=DEFAULT_CONFIG)
+    p.add_argument("--op", default="decode", choices=["decode", "kv_append", "prelude"],
+                   help="decode (the headline path); kv_append / prelude: the cache-write step before it")
+    p.add_argument("--tokens", type=int, default=32768,
+                   help="--op kv_append: tokens written per call (32 = one decode step of bs=32)")
     p.add_argument("--workers", type=int, default=0, help="worker wavefronts; 0 = one per wave slot")
     p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -93,12 +97,102 @@ def cpu_baseline(case, args) -> dict | None:
     }
 
 
+def bench_kv(args) -> int:
+    """Time the KV-cache append or the fused decode prelude (Qwen3-8B layer shape)."""
+    import numpy as np
+    import torch
+
+    from simpler_amd import kv_cache as kvc
+
+    dev = torch.device("cuda", 0)
+    hq, hkv, d, bs = 32, 8, 128, 128
+    g = torch.Generator().manual_seed(20261210)
+    stream = torch.cuda.current_stream(dev)
+    if args.op == "kv_append":
+        n = args.tokens
+        nblk = (2 * n + bs - 1) // bs
+        kc = torch.zeros(nblk, bs, hkv, d, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        key = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        val = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        slots = torch.randperm(nblk * bs, generator=g)[:n].to(torch.int32).to(dev)
+        pargs = kvc.append_args(key, val, slots, kc, vc)
+        call = lambda: kvc.launch_append(pargs, stream=stream.cuda_stream)
+        nbytes = n * (4 * hkv * d * 2 + 4)
+        workload = f"kv_append: {n} tokens, Hkv={hkv}, D={d}, block_size={bs}, random slots in a {nblk}-block pool"
+        kernel = "kv_append_kernel"
+        metric = "kv-append GB/s (K+V rows read and written)"
+    else:
+        b = 32
+        seq = torch.randint(1024, 8192, (b,), generator=g, dtype=torch.int32)
+        max_blocks = 64
+        table = torch.arange(b * max_blocks, dtype=torch.int32).reshape(b, max_blocks)
+        from simpler_amd.workloads import current_token_slots, rope_tables
+        cos, sin = (t.to(dev) for t in rope_tables(max_blocks * bs, d))
+        slots = current_token_slots(table, seq, bs).to(dev)
+        rn = lambda *sh: torch.randn(*sh, generator=g).to(dev)
+        qp, kp, vp = rn(b, hq * d), rn(b, hkv * d), rn(b, hkv * d)
+        ir = rn(b).abs() + 0.5
+        qw, kw = rn(d) * 0.1 + 1, rn(d) * 0.1 + 1
+        kc = torch.zeros(b * max_blocks, bs, hkv, d, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        q_out = torch.empty(b, hq, d, dtype=torch.bfloat16, device=dev)
+        seq_d = seq.to(dev)
+        pargs = kvc.prelude_args(qp, kp, vp, ir, qw, kw, cos, sin, seq_d, slots, kc, vc, hq, q_out)
+        call = lambda: kvc.launch_prelude(pargs, stream=stream.cuda_stream)
+        nbytes = b * ((hq + 2 * hkv) * d * 4 + 4 + 2 * d * 4 + 8 + hq * d * 2 + 2 * hkv * d * 2) + 2 * d * 4
+        workload = f"prelude: B={b}, Hq={hq}, Hkv={hkv}, D={d}: q/k RMS norm + RoPE + K/V append"
+        kernel = "qk_norm_rope_append_kernel"
+        metric = "decode prelude (q/k norm + RoPE + KV append) GB/s"
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline and args.op == "kv_append":
+        from oracle import kv_oracle as ko
+        sample = min(n, 4096)
+        kcn = np.zeros((nblk, bs, hkv, d), np.uint16)
+        kn = np.ones((sample, hkv, d), np.uint16)
+        sl = slots[:sample].cpu().numpy()
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 5.0):
+            ko.kv_append(kcn, kcn, kn, kn, sl)
+            reps += 1
+        el = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(sample * (4 * hkv * d * 2 + 4) / el / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port", "sample": f"oracle kv_append of {sample} tokens ({reps} repetitions, numpy, 1 thread; "
+                                         "includes the oracle's cache copies)"}
+    line = {
+        "metric": metric, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": workload, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+                     "kernel_us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the path shards by batch / kv head with no exchange, see DESIGN.md", file=sys.stderr)
         return 2
+    if args.op != "decode":
+        return bench_kv(args)
 
     import torch
 

@@ -59,6 +59,39 @@ class PaDecodeArgs(ctypes.Structure):
     ]
 
 
+class KvAppendArgs(ctypes.Structure):
+    """Mirror of ``SimplerHipKvAppendArgs`` (include/simpler_hip/kv_cache.h)."""
+
+    _fields_ = [
+        ("key", ctypes.c_void_p),
+        ("value", ctypes.c_void_p),
+        ("slot_mapping", ctypes.c_void_p),
+        ("key_cache", ctypes.c_void_p),
+        ("value_cache", ctypes.c_void_p),
+        ("error_count", ctypes.c_void_p),
+        *[(n, ctypes.c_int64) for n in ("key_token_stride", "key_head_stride", "value_token_stride",
+                                         "value_head_stride", "k_block_stride", "k_token_stride", "k_head_stride",
+                                         "v_block_stride", "v_token_stride", "v_head_stride")],
+        *[(n, ctypes.c_int32) for n in ("num_tokens", "num_kv_heads", "head_dim_k", "head_dim_v", "block_size",
+                                         "num_blocks")],
+    ]
+
+
+class QkNormRopeAppendArgs(ctypes.Structure):
+    """Mirror of ``SimplerHipQkNormRopeAppendArgs`` (include/simpler_hip/kv_cache.h)."""
+
+    _fields_ = [
+        *[(n, ctypes.c_void_p) for n in ("q_proj", "k_proj", "v_proj", "inv_rms", "q_norm_weight", "k_norm_weight",
+                                          "rope_cos", "rope_sin", "seq_lens", "slot_mapping", "q_out", "key_cache",
+                                          "value_cache", "error_count")],
+        *[(n, ctypes.c_int64) for n in ("k_block_stride", "k_token_stride", "k_head_stride", "v_block_stride",
+                                         "v_token_stride", "v_head_stride")],
+        *[(n, ctypes.c_int32) for n in ("batch", "num_heads", "num_kv_heads", "head_dim", "block_size", "num_blocks",
+                                         "max_position")],
+        ("eps", ctypes.c_float),
+    ]
+
+
 # Every symbol the public headers declare, with its ctypes signature.
 _VP, _SZ, _I32, _U32, _U64, _I = (
     ctypes.c_void_p,
@@ -78,6 +111,9 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_pa_decode_check": (_I, [_VP, _SZ, _VP]),
     "simpler_hip_pa_decode_kernel_name": (ctypes.c_char_p, [_ARGS_P]),
     "simpler_hip_pa_decode_plan": (_I, [_ARGS_P, ctypes.POINTER(_I32)]),
+    # include/simpler_hip/kv_cache.h
+    "simpler_hip_kv_append": (_I, [ctypes.POINTER(KvAppendArgs), _VP]),
+    "simpler_hip_qk_norm_rope_append": (_I, [ctypes.POINTER(QkNormRopeAppendArgs), _VP]),
     # include/simpler_hip/pto_runtime_c_api.h
     "get_pipeline_contract": (_VP, []),
     "get_runtime_size": (_SZ, []),

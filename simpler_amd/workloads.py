@@ -210,3 +210,26 @@ def algorithmic_flops(case: DecodeCase) -> int:
             pairs = c.q_len * n
         total += pairs * c.num_heads * 2 * (c.head_dim_k + c.head_dim_v)
     return total
+
+
+# ---------------------------------------------------------------------------
+# Decode-layer prelude inputs (the KV-append step before attention)
+# ---------------------------------------------------------------------------
+
+
+def rope_tables(max_position: int, head_dim: int, theta: float = 1.0e4) -> tuple[torch.Tensor, torch.Tensor]:
+    """RoPE tables ``[max_position, head_dim]`` fp32 with both halves sharing the angles,
+    as simpler's Qwen3 decode inputs build them (``goldens/qwen3_14b_decode.py:149-153``)."""
+    half = head_dim // 2
+    inv_freq = 1.0 / (theta ** (torch.arange(0, half).float() / half))
+    ang = torch.arange(max_position).float().unsqueeze(1) * inv_freq.unsqueeze(0)
+    return torch.cat([ang.cos(), ang.cos()], dim=1).float(), torch.cat([ang.sin(), ang.sin()], dim=1).float()
+
+
+def current_token_slots(block_table: torch.Tensor, seq_lens: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Slot of each sequence's current token (position ``seq_len - 1``):
+    ``block_table[b, p // block_size] * block_size + p % block_size``
+    (``goldens/qwen3_14b_decode.py:106-115``)."""
+    pos = seq_lens.long() - 1
+    phys = block_table[torch.arange(len(pos)), pos // block_size].long()
+    return (phys * block_size + pos % block_size).to(torch.int32)

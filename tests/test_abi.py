@@ -217,3 +217,42 @@ def test_work_list_must_fit_32_bit_indices():
     lib = _lib.lib()
     huge = _args(batch=65535, num_heads=32, num_kv_heads=8, max_blocks_per_seq=8192)
     assert lib.simpler_hip_pa_decode(ctypes.byref(huge), ctypes.c_void_p(0x100000), 1 << 40, None) == -2
+
+
+def test_kv_cache_entry_points_validate_on_the_host():
+    lib = _lib.lib()
+
+    def app(**kw):
+        a = _lib.KvAppendArgs()
+        base = dict(key=0x1000, value=0x2000, slot_mapping=0x3000, key_cache=0x4000, value_cache=0x5000,
+                    key_token_stride=8 * 128, key_head_stride=128, value_token_stride=8 * 128, value_head_stride=128,
+                    k_block_stride=128 * 8 * 128, k_token_stride=8 * 128, k_head_stride=128,
+                    v_block_stride=128 * 8 * 128, v_token_stride=8 * 128, v_head_stride=128, num_tokens=0,
+                    num_kv_heads=8, head_dim_k=128, head_dim_v=128, block_size=128, num_blocks=10)
+        base.update(kw)
+        for k, v in base.items():
+            setattr(a, k, v)
+        return lib.simpler_hip_kv_append(ctypes.byref(a), None)
+
+    assert app() == 0  # zero tokens: valid, nothing launched
+    for bad in (dict(head_dim_k=100), dict(key_cache=0x4008), dict(k_token_stride=4), dict(value=0),
+                dict(num_kv_heads=0), dict(head_dim_k=2048)):
+        assert app(**bad) == -1, bad
+    assert app(value=0, value_cache=0) == 0  # K-only cache (MLA latent)
+
+    def pre(**kw):
+        a = _lib.QkNormRopeAppendArgs()
+        ptrs = ("q_proj", "k_proj", "v_proj", "inv_rms", "q_norm_weight", "k_norm_weight", "rope_cos", "rope_sin",
+                "seq_lens", "slot_mapping", "q_out", "key_cache", "value_cache")
+        base = {n: 0x1000 * (i + 1) for i, n in enumerate(ptrs)}
+        base.update(k_block_stride=128 * 8 * 128, k_token_stride=8 * 128, k_head_stride=128,
+                    v_block_stride=128 * 8 * 128, v_token_stride=8 * 128, v_head_stride=128, batch=0, num_heads=32,
+                    num_kv_heads=8, head_dim=128, block_size=128, num_blocks=10, max_position=4096, eps=1e-6)
+        base.update(kw)
+        for k, v in base.items():
+            setattr(a, k, v)
+        return lib.simpler_hip_qk_norm_rope_append(ctypes.byref(a), None)
+
+    assert pre() == 0
+    for bad in (dict(head_dim=127), dict(q_out=0), dict(max_position=0), dict(eps=-1.0), dict(v_head_stride=0)):
+        assert pre(**bad) == -1, bad
