@@ -148,6 +148,16 @@ int comm_destroy(CommHandle h);
  * context, so callers can order their own work against simpler_run. */
 void *simpler_hip_context_stream(DeviceContextHandle ctx);
 
+/* simpler_hip extension (no reference counterpart): how a context executes a
+ * paged-attention callable from now on. FUSED (default): the fused split-K
+ * decode kernel. TASK_GRAPH: the reference's orchestration (QK -> SF -> PV ->
+ * UP per KV block) on the task-graph backend, each task launched as it is
+ * submitted. TASK_GRAPH_HIPGRAPH: the same DAG captured as one hipGraph with
+ * the inferred dependencies as edges. SIMPLER_HIP_EXECUTION=eager|graph in the
+ * environment at simpler_init selects the same. Returns 0 or -1. */
+enum { SIMPLER_HIP_EXEC_FUSED = 0, SIMPLER_HIP_EXEC_TASK_GRAPH = 1, SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH = 2 };
+int simpler_hip_set_execution(DeviceContextHandle ctx, int32_t execution);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

@@ -197,3 +197,62 @@ def attention_fp64(
                 w = np.exp(s - s.max())
                 out[b, i, h] = (w / w.sum()) @ vals[:n]
     return out[:, 0] if squeeze else out
+
+
+# ---------------------------------------------------------------------------
+# The four per-block kernels one at a time (the task-graph backend runs them
+# as separate tasks). Composing them block by block reproduces
+# paged_attention_decode exactly; tests/test_task_graph_oracle.py checks that
+# and the closed forms of each step.
+# ---------------------------------------------------------------------------
+
+
+def qk_matmul(qi: np.ndarray, kj: np.ndarray) -> np.ndarray:
+    """``sij = qi · kjᵀ`` in fp32 (``aic_qk_matmul.cpp:38-100``); qi ``[M, D]``, kj ``[N, D]``."""
+    return (np.asarray(qi, np.float32) @ np.asarray(kj, np.float32).T).astype(np.float32)
+
+
+def softmax_prepare(sij: np.ndarray, valid_len: int, scale: float) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """``aiv_softmax_prepare.cpp:96-131``: columns ``>= valid_len`` → −inf, ``s·scale``,
+    ``m = rowmax``, ``p = exp(s − m)`` rounded to bf16, ``l = rowsum(p)``.
+
+    Returns ``(p, m, l)`` with p as fp32 values on the bf16 grid. A block with no
+    valid column gives m = −1e30, l = 0, p = 0 (``batch_paged_attention/kernels/aiv/
+    aiv_softmax_prepare.cpp:105-121``).
+    """
+    s = np.asarray(sij, np.float32)
+    n = s.shape[1]
+    valid = np.arange(n)[None, :] < valid_len
+    x = np.where(valid, s * np.float32(scale), np.float32(-np.inf)).astype(np.float32)
+    if valid_len <= 0:
+        m = np.full(s.shape[0], NEG_CLAMP, np.float32)
+        return np.zeros_like(s), m, np.zeros(s.shape[0], np.float32)
+    m = x.max(axis=1).astype(np.float32)
+    p = bf16_round(np.exp(x - m[:, None]).astype(np.float32))
+    return p, m, p.sum(axis=1, dtype=np.float32)
+
+
+def pv_matmul(pij: np.ndarray, vj: np.ndarray) -> np.ndarray:
+    """``oi_new = pij · vj`` in fp32 (``aic_pv_matmul.cpp:38-99``)."""
+    return (np.asarray(pij, np.float32) @ np.asarray(vj, np.float32)).astype(np.float32)
+
+
+def online_update(mij, lij, oi_new, mi, li, oi, is_first: bool, is_last: bool):
+    """``aiv_online_update.cpp:125-224``. Returns ``(mi, li, oi, dst)``; dst is None unless is_last.
+
+    First block: the block's (m, l, o) are taken as they are (dst = o / l if also
+    last). Otherwise ``m' = max(mi, mij)``, ``α = e^{mi−m'}``, ``β = e^{mij−m'}``,
+    ``li = α·li + β·lij``, ``oi = α·oi + β·oi_new``; dst = oi / li when last.
+    """
+    mij, lij, oi_new = (np.asarray(x, np.float32) for x in (mij, lij, oi_new))
+    if is_first:
+        dst = (oi_new / lij[:, None]).astype(np.float32) if is_last else None
+        return mij.copy(), lij.copy(), oi_new.copy(), dst
+    mi, li, oi = (np.asarray(x, np.float32) for x in (mi, li, oi))
+    mn = np.maximum(mi, mij)
+    alpha = np.exp(mi - mn).astype(np.float32)
+    beta = np.exp(mij - mn).astype(np.float32)
+    l2 = (alpha * li + beta * lij).astype(np.float32)
+    o2 = (oi * alpha[:, None] + oi_new * beta[:, None]).astype(np.float32)
+    dst = (o2 / l2[:, None]).astype(np.float32) if is_last else None
+    return mn, l2, o2, dst

@@ -158,6 +158,26 @@ SIGNATURES: dict[str, tuple] = {
     "comm_barrier": (_I, [_VP]),
     "comm_destroy": (_I, [_VP]),
     "simpler_hip_context_stream": (_VP, [_VP]),
+    "simpler_hip_set_execution": (_I, [_VP, _I32]),
+    # include/simpler_hip/task_graph.h (tensor arrays are SimplerChipTensor[], passed as void*)
+    "simpler_hip_tg_create": (_VP, [_I32, _VP]),
+    "simpler_hip_tg_destroy": (None, [_VP]),
+    "simpler_hip_tg_bind": (_I, [_VP, _I32, _I32]),
+    "simpler_hip_tg_scope_begin": (_I, [_VP]),
+    "simpler_hip_tg_scope_end": (_I, [_VP]),
+    "simpler_hip_tg_submit": (ctypes.c_int64, [_VP, _I32, _VP, ctypes.POINTER(_I32), _I32, ctypes.POINTER(_U64),
+                                               _I32, ctypes.POINTER(_U64), _I32, _VP]),
+    "simpler_hip_tg_alloc": (ctypes.c_int64, [_VP, _VP, _I32, _VP]),
+    "simpler_hip_tg_get_tensor_data": (_I, [_VP, _VP, _U32, ctypes.POINTER(_U32), ctypes.POINTER(_U64)]),
+    "simpler_hip_tg_copy_to_host": (_I, [_VP, _VP, _VP, _U64]),
+    "simpler_hip_tg_launch": (_I, [_VP]),
+    "simpler_hip_tg_wait": (_I, [_VP]),
+    "simpler_hip_tg_reset": (_I, [_VP]),
+    "simpler_hip_tg_orchestrate_paged_attention": (_I, [_VP, _VP, _U64]),
+    "simpler_hip_tg_orchestrate_vector_example": (_I, [_VP, _VP]),
+    "simpler_hip_tg_task_count": (ctypes.c_int64, [_VP]),
+    "simpler_hip_tg_fanin": (_I32, [_VP, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _I32]),
+    "simpler_hip_tg_arena_bytes": (_U64, [_VP]),
 }
 
 

@@ -18,7 +18,14 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "lib"
 LIB_PATH = LIB_DIR / "libsimpler_hip.so"
-SOURCES = [CSRC / "pa_decode.hip", CSRC / "kv_cache.hip", CSRC / "host_runtime.cpp"]
+SOURCES = [
+    CSRC / "pa_decode.hip",
+    CSRC / "kv_cache.hip",
+    CSRC / "incore_kernels.hip",
+    CSRC / "task_graph.cpp",
+    CSRC / "orchestrations.cpp",
+    CSRC / "host_runtime.cpp",
+]
 ARCH = os.environ.get("SIMPLER_HIP_ARCH", "gfx950")
 
 

@@ -16,10 +16,17 @@
 // (src/a2a3/runtime/tensormap_and_ringbuffer/host/runtime_maker.cpp:575-652):
 // copied to the device unless the signature says OUT, copied back unless IN.
 // Tensors whose address_space is DEVICE (tensor.h:105) pass through untouched.
+//
+// Execution of a paged-attention callable is the fused decode kernel by
+// default. With the task-graph execution selected (simpler_hip_set_execution
+// or SIMPLER_HIP_EXECUTION=eager|graph at init) the reference's orchestration
+// runs instead, QK -> SF -> PV -> UP per KV block, on the task-graph backend
+// (task_graph.h). The reference's vector example callable always runs there.
 
 #include <hip/hip_runtime.h>
 
 #include <memory>
+#include <stdlib.h>
 #include <mutex>
 #include <new>
 #include <stdarg.h>
@@ -31,11 +38,14 @@
 #include "simpler_hip/abi_types.h"
 #include "simpler_hip/pa_decode.h"
 #include "simpler_hip/pto_runtime_c_api.h"
+#include "simpler_hip/task_graph.h"
 
 namespace {
 
 constexpr int kMaxCallables = 64;  // callable ids 0..63 (pto_runtime_c_api.h:285-287)
 constexpr int kPaTensors = 6;
+constexpr int kVecTensors = 3;
+constexpr int kMaxRunTensors = 8;
 constexpr uint32_t kRunMagic = 0x53485052u;  // "SHPR"
 const char *const kNativePaName = "simpler_hip_paged_attention_decode";
 
@@ -48,7 +58,7 @@ void logf(const char *fmt, ...) {
     va_end(ap);
 }
 
-enum CallableKind { kNone = 0, kPagedAttention = 1 };
+enum CallableKind { kNone = 0, kPagedAttention = 1, kVectorExample = 2 };
 
 struct Callable {
     CallableKind kind = kNone;
@@ -66,6 +76,8 @@ struct DeviceContext {
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
     size_t runs = 0;
+    int32_t execution = SIMPLER_HIP_EXEC_FUSED;
+    SimplerHipTaskGraph *graphs[2] = {nullptr, nullptr};  // eager, hipGraph
 };
 
 // Native-run state lives in caller-owned storage of get_runtime_size() bytes
@@ -74,12 +86,17 @@ struct NativeRun {
     uint32_t magic;
     uint32_t state;  // 0 idle, 1 prepared, 2 launched
     int32_t callable_id;
+    int32_t kind;       // CallableKind
+    int32_t execution;  // SIMPLER_HIP_EXEC_* chosen at prepare
+    int32_t n_tensors;
     int32_t n_staged;
     hipEvent_t done;
-    void *staged_dev[kPaTensors];
-    void *host_ptr[kPaTensors];
-    size_t staged_bytes[kPaTensors];
-    int32_t dir[kPaTensors];
+    void *staged_dev[kMaxRunTensors];
+    void *host_ptr[kMaxRunTensors];
+    size_t staged_bytes[kMaxRunTensors];
+    int32_t dir[kMaxRunTensors];
+    uint64_t scale_bits;
+    SimplerChipTensor tensors[kMaxRunTensors];  // the run's tensors as device work sees them
     SimplerHipPaDecodeArgs args;
 };
 
@@ -110,6 +127,28 @@ bool sig_equals(const int32_t *a, int32_t na, const int32_t *b, int32_t nb) {
     return true;
 }
 
+// The vector example (examples/a2a3/tensormap_and_ringbuffer/vector_example/
+// test_vector_example.py:24-49): orchestration [IN, IN, OUT]; children
+// 0 kernel_add [IN, IN, OUT], 1 kernel_add_scalar [IN, OUT], 2 kernel_mul [IN, IN, OUT].
+const int32_t kVecOrchSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_OUT};
+const int32_t kVecUnarySig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_OUT};
+
+CallableKind classify_vector(const SimplerChipCallableHeader &h, const uint8_t *blob) {
+    const uint8_t *storage = blob + SIMPLER_CHIP_CALLABLE_STORAGE_OFFSET;
+    bool seen[3] = {false, false, false};
+    for (int i = 0; i < 3; ++i) {
+        const int fid = h.child_func_ids_[i];
+        if (fid < 0 || fid > 2 || seen[fid]) return kNone;
+        seen[fid] = true;
+        SimplerCoreCallableHeader ch;
+        memcpy(&ch, storage + h.child_offsets_[i], sizeof(ch));
+        const bool ok = fid == 1 ? sig_equals(ch.signature_, ch.sig_count_, kVecUnarySig, 2)
+                                 : sig_equals(ch.signature_, ch.sig_count_, kVecOrchSig, 3);
+        if (!ok) return kNone;
+    }
+    return kVectorExample;
+}
+
 CallableKind classify(const uint8_t *blob, Callable &out) {
     SimplerChipCallableHeader h;
     memcpy(&h, blob, sizeof(h));
@@ -120,6 +159,7 @@ CallableKind classify(const uint8_t *blob, Callable &out) {
     char name[SIMPLER_CALLABLE_FUNC_NAME_MAX + 1] = {};
     memcpy(name, h.func_name_, SIMPLER_CALLABLE_FUNC_NAME_MAX);
     if (strcmp(name, kNativePaName) == 0 && h.sig_count_ >= kPaTensors) return kPagedAttention;
+    if (sig_equals(h.signature_, h.sig_count_, kVecOrchSig, 3) && h.child_count_ == 3) return classify_vector(h, blob);
     if (!sig_equals(h.signature_, h.sig_count_, kOrchSig, 6) || h.child_count_ != 4) return kNone;
     const uint8_t *storage = blob + SIMPLER_CHIP_CALLABLE_STORAGE_OFFSET;
     bool seen[4] = {false, false, false, false};
@@ -288,6 +328,44 @@ int ensure_workspace(DeviceContext *c, size_t need) {
     return simpler_hip_pa_decode_workspace_init(c->workspace, sz, c->stream);
 }
 
+int check_vector_args(const SimplerChipStorageTaskArgs *a) {
+    if (a->tensor_count_ < kVecTensors) {
+        logf("vector example needs 3 tensors (a, b, f)");
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    const SimplerChipTensor &x = tensor_at(a, 0);
+    for (int i = 0; i < kVecTensors; ++i) {
+        const SimplerChipTensor &t = tensor_at(a, i);
+        if (t.dtype != SIMPLER_DT_FLOAT32 || t.ndims != 1 || t.shapes[0] != x.shapes[0] || !contiguous(t)) {
+            logf("vector example tensors must be contiguous fp32 [n] of one size");
+            return SIMPLER_HIP_ERR_INVALID;
+        }
+    }
+    return SIMPLER_HIP_OK;
+}
+
+// Runs the callable's orchestration on the context's task graph for the
+// run's execution mode (eager launches, or one hipGraph launched at the end).
+int run_task_graph(DeviceContext *c, NativeRun *r) {
+    const int slot = r->execution == SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH ? 1 : 0;
+    SimplerHipTaskGraph *&g = c->graphs[slot];
+    if (!g) {
+        g = simpler_hip_tg_create(slot ? SIMPLER_HIP_TG_GRAPH : SIMPLER_HIP_TG_EAGER, c->stream);
+        if (!g) return SIMPLER_HIP_ERR_LAUNCH;
+    }
+    int rc = simpler_hip_tg_reset(g);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    simpler_hip_tg_scope_begin(g);  // the executor's outer scope
+    rc = r->kind == kPagedAttention ? simpler_hip_tg_orchestrate_paged_attention(g, r->tensors, r->scale_bits)
+                                    : simpler_hip_tg_orchestrate_vector_example(g, r->tensors);
+    if (rc != SIMPLER_HIP_OK) {
+        simpler_hip_tg_reset(g);
+        return rc;
+    }
+    simpler_hip_tg_scope_end(g);
+    return simpler_hip_tg_launch(g);
+}
+
 void release_staged(NativeRun *r) {
     for (int i = 0; i < r->n_staged; ++i) {
         if (r->staged_dev[i]) hipFree(r->staged_dev[i]);
@@ -329,6 +407,10 @@ int simpler_init(DeviceContextHandle h, int device_id, const uint8_t *, size_t, 
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return -1;
     c->device_id = device_id;
     c->stream = s;
+    if (const char *e = getenv("SIMPLER_HIP_EXECUTION")) {
+        if (strcmp(e, "eager") == 0) c->execution = SIMPLER_HIP_EXEC_TASK_GRAPH;
+        else if (strcmp(e, "graph") == 0) c->execution = SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH;
+    }
     return 0;
 }
 
@@ -339,6 +421,10 @@ int finalize_device(DeviceContextHandle h) {
     if (c->device_id < 0) return 0;
     hipSetDevice(c->device_id);
     if (c->stream) hipStreamSynchronize(c->stream);
+    for (SimplerHipTaskGraph *&g : c->graphs) {
+        simpler_hip_tg_destroy(g);
+        g = nullptr;
+    }
     for (auto &kv : c->allocs) hipFree(kv.first);
     c->allocs.clear();
     c->committed = 0;
@@ -401,7 +487,8 @@ int simpler_register_callable(DeviceContextHandle h, int32_t id, const void *cal
     Callable cb;
     const CallableKind kind = classify(static_cast<const uint8_t *>(callable), cb);
     if (kind == kNone) {
-        logf("callable %d is not a paged-attention decode chain; the HIP backend runs only that path", id);
+        logf("callable %d is neither the paged-attention chain nor the vector example; the HIP backend runs those",
+             id);
         return PTO_RUNTIME_ERR_UNSUPPORTED;
     }
     cb.kind = kind;
@@ -427,11 +514,13 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
     if (!set_device(c) || !r || !args_v || id < 0 || id >= kMaxCallables) return -1;
     if (r->magic == kRunMagic && r->state != 0) return PTO_RUNTIME_ERR_PREPARED_INCOMPATIBLE;
     Callable cb;
+    int32_t execution;
     {
         std::lock_guard<std::mutex> lk(c->mu);
         cb = c->callables[id];
+        execution = c->execution;
     }
-    if (cb.kind != kPagedAttention) {
+    if (cb.kind == kNone) {
         logf("callable %d is not registered", id);
         return -1;
     }
@@ -448,20 +537,43 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
     memset(r, 0, sizeof(*r));
     r->magic = kRunMagic;
     r->callable_id = id;
-    int rc = decode_pa_args(a, r->args, 1);
-    if (rc == SIMPLER_HIP_OK) rc = check_host_tables(a, r->args);
+    r->kind = cb.kind;
+    r->execution = cb.kind == kVectorExample && execution == SIMPLER_HIP_EXEC_FUSED ? SIMPLER_HIP_EXEC_TASK_GRAPH
+                                                                                    : execution;
+    int rc = SIMPLER_HIP_OK;
+    if (cb.kind == kPagedAttention) {
+        r->n_tensors = kPaTensors;
+        rc = decode_pa_args(a, r->args, 1);
+        if (rc == SIMPLER_HIP_OK) rc = check_host_tables(a, r->args);
+        if (rc == SIMPLER_HIP_OK && r->execution != SIMPLER_HIP_EXEC_FUSED &&
+            (r->args.num_kv_heads != 1 || r->args.q_len != 1 || r->args.head_dim_k != r->args.head_dim_v)) {
+            logf("task-graph paged attention runs the reference orchestration: one KV head, one query token, "
+                 "Dk == Dv");
+            rc = SIMPLER_HIP_ERR_UNSUPPORTED;
+        }
+        r->scale_bits = a->scalars_[0];
+    } else {
+        r->n_tensors = kVecTensors;
+        rc = check_vector_args(a);
+    }
     if (rc != SIMPLER_HIP_OK) {
         r->magic = 0;
         return rc;
     }
-    // Stage host tensors; directions from the callable signature (IN x5, OUT).
-    const void *dev[kPaTensors];
-    for (int i = 0; i < kPaTensors; ++i) {
+    // Stage host tensors; directions from the callable signature.
+    const void *dev[kMaxRunTensors];
+    for (int i = 0; i < r->n_tensors; ++i) {
         const SimplerChipTensor &t = tensor_at(a, i);
         const size_t esz = simpler_dtype_size(t.dtype);
         const int dir = i < cb.sig_count ? cb.sig[i] : SIMPLER_ARG_IN;
+        r->tensors[i] = t;
         if (t.address_space == SIMPLER_ADDR_DEVICE) {
             dev[i] = (const void *)(uintptr_t)(t.buffer.addr + t.start_offset * esz);
+            continue;
+        }
+        // Tables the task-graph orchestration only reads on the host stay there.
+        if (cb.kind == kPagedAttention && r->execution != SIMPLER_HIP_EXEC_FUSED && (i == 3 || i == 4)) {
+            dev[i] = nullptr;
             continue;
         }
         const size_t bytes = extent_bytes(t);
@@ -485,27 +597,32 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
             return SIMPLER_HIP_ERR_LAUNCH;
         }
         dev[i] = (const char *)d + t.start_offset * esz;
+        r->tensors[i].buffer.addr = (uint64_t)(uintptr_t)d;
+        r->tensors[i].buffer.size = bytes;
+        r->tensors[i].address_space = SIMPLER_ADDR_DEVICE;
     }
-    r->args.query = dev[0];
-    r->args.key_cache = dev[1];
-    r->args.value_cache = dev[2];
-    r->args.block_table = (const int32_t *)dev[3];
-    r->args.context_lens = (const int32_t *)dev[4];
-    r->args.out = (void *)dev[5];
-    const size_t need = simpler_hip_pa_decode_workspace_size(&r->args);
-    if (need == 0) {
-        release_staged(r);
-        r->magic = 0;
-        return SIMPLER_HIP_ERR_INVALID;
-    }
-    {
-        std::lock_guard<std::mutex> lk(c->mu);
-        rc = ensure_workspace(c, need);
-    }
-    if (rc != SIMPLER_HIP_OK) {
-        release_staged(r);
-        r->magic = 0;
-        return rc;
+    if (cb.kind == kPagedAttention && r->execution == SIMPLER_HIP_EXEC_FUSED) {
+        r->args.query = dev[0];
+        r->args.key_cache = dev[1];
+        r->args.value_cache = dev[2];
+        r->args.block_table = (const int32_t *)dev[3];
+        r->args.context_lens = (const int32_t *)dev[4];
+        r->args.out = (void *)dev[5];
+        const size_t need = simpler_hip_pa_decode_workspace_size(&r->args);
+        if (need == 0) {
+            release_staged(r);
+            r->magic = 0;
+            return SIMPLER_HIP_ERR_INVALID;
+        }
+        {
+            std::lock_guard<std::mutex> lk(c->mu);
+            rc = ensure_workspace(c, need);
+        }
+        if (rc != SIMPLER_HIP_OK) {
+            release_staged(r);
+            r->magic = 0;
+            return rc;
+        }
     }
     if (hipEventCreateWithFlags(&r->done, hipEventDisableTiming) != hipSuccess) {
         release_staged(r);
@@ -520,7 +637,12 @@ int simpler_launch_run(DeviceContextHandle h, RuntimeHandle runtime) {
     DeviceContext *c = as_ctx(h);
     NativeRun *r = static_cast<NativeRun *>(runtime);
     if (!set_device(c) || !r || r->magic != kRunMagic || r->state != 1) return -1;
-    int rc = simpler_hip_pa_decode(&r->args, c->workspace, c->workspace_bytes, c->stream);
+    int rc;
+    if (r->kind == kPagedAttention && r->execution == SIMPLER_HIP_EXEC_FUSED) {
+        rc = simpler_hip_pa_decode(&r->args, c->workspace, c->workspace_bytes, c->stream);
+    } else {
+        rc = run_task_graph(c, r);
+    }
     if (rc != SIMPLER_HIP_OK) return rc;
     for (int i = 0; i < r->n_staged; ++i) {
         if (r->dir[i] == SIMPLER_ARG_IN) continue;
@@ -549,6 +671,7 @@ int simpler_wait_run(DeviceContextHandle h, RuntimeHandle runtime) {
     NativeRun *r = static_cast<NativeRun *>(runtime);
     if (!set_device(c) || !r || r->magic != kRunMagic || r->state != 2) return -1;
     if (hipEventSynchronize(r->done) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    if (r->kind != kPagedAttention || r->execution != SIMPLER_HIP_EXEC_FUSED) return SIMPLER_HIP_OK;
     return simpler_hip_pa_decode_check(c->workspace, c->workspace_bytes, c->stream);
 }
 
@@ -611,5 +734,13 @@ int comm_barrier(CommHandle) { return PTO_RUNTIME_ERR_UNSUPPORTED; }
 int comm_destroy(CommHandle) { return PTO_RUNTIME_ERR_UNSUPPORTED; }
 
 void *simpler_hip_context_stream(DeviceContextHandle h) { return as_ctx(h) ? (void *)as_ctx(h)->stream : nullptr; }
+
+int simpler_hip_set_execution(DeviceContextHandle h, int32_t execution) {
+    DeviceContext *c = as_ctx(h);
+    if (!c || execution < SIMPLER_HIP_EXEC_FUSED || execution > SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH) return -1;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->execution = execution;
+    return 0;
+}
 
 }  // extern "C"

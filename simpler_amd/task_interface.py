@@ -162,6 +162,33 @@ class ChipTensor(ctypes.Structure):
         t.extent_elem_cache = extent
         return t
 
+    def view(self, shapes: Sequence[int], offsets: Sequence[int], manual_dep: bool = False) -> "ChipTensor":
+        """Sub-box of this tensor (``ChipTensor::view``, ``tensor.h:283-312``): same buffer and strides,
+        ``start_offset`` advanced by ``offsets`` (elements per dim)."""
+        nd = self.ndims
+        if len(shapes) != nd or len(offsets) != nd:
+            raise ValueError(f"view needs {nd} shapes and offsets")
+        for i in range(nd):
+            if int(shapes[i]) and int(offsets[i]) + int(shapes[i]) > self.shapes[i]:
+                raise ValueError(f"view exceeds dim {i}: {offsets[i]} + {shapes[i]} > {self.shapes[i]}")
+        t = ChipTensor()
+        ctypes.memmove(ctypes.addressof(t), ctypes.addressof(self), ctypes.sizeof(ChipTensor))
+        empty = any(int(s) == 0 for s in shapes)
+        for i in range(nd):
+            if not empty:
+                t.start_offset += int(offsets[i]) * int(self.strides[i])
+            t.shapes[i] = int(shapes[i])
+        t.manual_dep = 1 if manual_dep else 0
+        last = sum((int(shapes[i]) - 1) * int(self.strides[i]) for i in range(nd)) if not empty else -1
+        t.extent_elem_cache = last + 1
+        row_major, acc = True, 1
+        for i in range(nd - 1, -1, -1):
+            if int(shapes[i]) != 1 and int(self.strides[i]) != acc:
+                row_major = False
+            acc *= int(shapes[i])
+        t.is_contiguous = 1 if (row_major or empty) else 0
+        return t
+
     @property
     def shape(self) -> tuple[int, ...]:
         return tuple(self.shapes[i] for i in range(self.ndims))
@@ -467,6 +494,19 @@ class ChipWorker:
             self._ctx = None
             self._slots.clear()
             self._handles.clear()
+
+    EXECUTION_MODES = {"fused": 0, "eager": 1, "graph": 2}
+
+    def set_execution(self, mode: str) -> None:
+        """How paged-attention callables run from now on (``simpler_hip_set_execution``):
+        ``"fused"`` (default) the fused decode kernel; ``"eager"`` / ``"graph"`` the
+        reference's QK/SF/PV/UP orchestration on the task-graph backend, launched task by
+        task or as one hipGraph."""
+        if mode not in self.EXECUTION_MODES:
+            raise ValueError(f"execution must be one of {sorted(self.EXECUTION_MODES)}")
+        rc = self._lib.simpler_hip_set_execution(self._require(), self.EXECUTION_MODES[mode])
+        if rc != 0:
+            raise RuntimeError(f"simpler_hip_set_execution failed: {rc}")
 
     @property
     def initialized(self) -> bool:

@@ -106,6 +106,8 @@ class Worker:
             raise RuntimeError("Worker is already initialized")
         chip = ChipWorker()
         chip.init(int(self._config.get("device_id", 0)))
+        if "execution" in self._config:  # "fused" | "eager" | "graph" (ChipWorker.set_execution)
+            chip.set_execution(str(self._config["execution"]))
         self._chip = chip
         return self
 

@@ -1,0 +1,264 @@
+"""GPU parity of the task-graph backend: incore kernels, orchestrations, hipGraph replays.
+
+* Each incore kernel against the oracle's step function (``oracle.pa_oracle``
+  qk_matmul / softmax_prepare / pv_matmul / online_update, pinned in
+  test_task_graph_oracle.py). Matmuls: fp32 sums in another order, so
+  |diff| <= 1e-4 + 1e-5·|x|. Softmax: m exact; p on the bf16 grid and at most one
+  bf16 step from the oracle (device and host exp may differ in the last fp32
+  bit before rounding); l within 1e-5 relative. Online update: exp as above,
+  within 1e-5 relative.
+* The reference paged-attention orchestration (QK -> SF -> PV -> UP per block)
+  end to end, eager and as a hipGraph, through the TaskGraph API and through
+  simpler_run (Worker execution="eager"/"graph"), against the whole-op oracle
+  at the decode tolerance (max-abs 2e-2, rel-L2 1e-3).
+* The vector example: f = (a+b+1)*(a+b+2) + (a+b) is fp32 arithmetic in a fixed
+  order, so it is bit-exact against numpy in the same order (and 47.0 for the
+  reference's a = 2, b = 3).
+* hipGraph execution replays the same instantiated graph; every replay is
+  checked against the eager result, with the program's own eager work and
+  synchronisations in between.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pa_oracle as po
+from simpler_amd import TaskArgs, Worker
+from simpler_amd import paged_attention as pa
+from simpler_amd.task_graph import CoreTaskArgs, IncoreKernel, TaskGraph, TaskGraphError, TensorCreateInfo
+from simpler_amd.task_graph import vector_example_callable
+from simpler_amd.task_interface import ChipTensor, DataType, TensorArgType
+from simpler_amd.workloads import make_case, make_custom_case
+from tests.pa_helpers import assert_close, oracle_numpy
+
+pytestmark = pytest.mark.gpu
+
+_DT = {torch.bfloat16: DataType.BFLOAT16, torch.float32: DataType.FLOAT32, torch.int32: DataType.INT32}
+
+
+def ct(t: torch.Tensor) -> ChipTensor:
+    assert t.is_contiguous()
+    return ChipTensor.make(t.data_ptr(), tuple(t.shape), _DT[t.dtype], child_memory=t.device.type != "cpu")
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def bf16_dev(rng, shape, device, scale=1.0):
+    x = torch.from_numpy((rng.standard_normal(shape) * scale).astype(np.float32))
+    return x.to(torch.bfloat16).to(device)
+
+
+@pytest.fixture
+def graph(device):
+    g = TaskGraph("eager")
+    for k in (IncoreKernel.QK_MATMUL, IncoreKernel.SOFTMAX_PREPARE, IncoreKernel.PV_MATMUL,
+              IncoreKernel.ONLINE_UPDATE):
+        g.bind(int(k), k)
+    yield g
+    g.close()
+
+
+def close_matmul(got, want):
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-5 * np.abs(want)), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("m,n,d", [(16, 128, 128), (64, 64, 64), (20, 48, 96)])
+def test_qk_and_pv_kernels(graph, device, m, n, d):
+    print(f"[case] tg qk/pv m={m} n={n} d={d}", flush=True)
+    rng = np.random.default_rng(m * 7 + n)
+    q = bf16_dev(rng, (m, d), device)
+    cache = bf16_dev(rng, (4 * n, d), device)  # kj is a view at block 2
+    kj = ct(cache).view((n, d), (2 * n, 0))
+    a = CoreTaskArgs()
+    a.add_input(ct(q), kj)
+    a.add_output(TensorCreateInfo((m, n), DataType.FLOAT32))
+    sij = graph.submit_task(0, a).get_ref(0)
+    got_s = graph.read(sij)
+    close_matmul(got_s, po.qk_matmul(to_np(q), to_np(cache)[2 * n: 3 * n]))
+
+    p = torch.from_numpy(po.bf16_round(np.abs(rng.standard_normal((m, n))).astype(np.float32))).to(torch.bfloat16)
+    p = p.to(device)
+    v = bf16_dev(rng, (4 * n, d), device)
+    a = CoreTaskArgs()
+    a.add_input(ct(p), ct(v).view((n, d), (n, 0)))
+    a.add_output(TensorCreateInfo((m, d), DataType.FLOAT32))
+    o = graph.submit_task(2, a).get_ref(0)
+    close_matmul(graph.read(o), po.pv_matmul(to_np(p), to_np(v)[n: 2 * n]))
+
+
+@pytest.mark.parametrize("valid", [1, 57, 128, 0])
+def test_softmax_prepare_kernel(graph, device, valid):
+    print(f"[case] tg softmax valid={valid}", flush=True)
+    rng = np.random.default_rng(100 + valid)
+    m, n = 16, 128
+    s = torch.from_numpy((rng.standard_normal((m, n)) * 6).astype(np.float32)).to(device)
+    scale = 0.0883883
+    a = CoreTaskArgs()
+    a.add_input(ct(s).view((m, valid), (0, 0)) if valid else ct(s).view((m, 0), (0, 0)))
+    a.add_output(TensorCreateInfo((m, n), DataType.BFLOAT16), TensorCreateInfo((m,), DataType.FLOAT32),
+                 TensorCreateInfo((m,), DataType.FLOAT32))
+    a.add_scalar(ctypes.c_float(scale))
+    outs = graph.submit_task(1, a)
+    p = graph.read(outs.get_ref(0))
+    mm, ll = graph.read(outs.get_ref(1)), graph.read(outs.get_ref(2))
+    wp, wm, wl = po.softmax_prepare(to_np(s), valid, scale)
+    np.testing.assert_array_equal(mm, wm)
+    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(wp), 1e-30))) - 7)
+    assert np.all(np.abs(p - wp) <= step * 1.0001)
+    assert np.array_equal(p, po.bf16_round(p))
+    np.testing.assert_allclose(ll, wl, rtol=1e-5, atol=1e-6)
+
+
+def test_online_update_kernel_chain(graph, device):
+    print("[case] tg online_update chain", flush=True)
+    rng = np.random.default_rng(7)
+    m, d = 16, 128
+    blocks = [(rng.standard_normal(m).astype(np.float32) * 3, (rng.random(m) * 50 + 1).astype(np.float32),
+               rng.standard_normal((m, d)).astype(np.float32) * 10) for _ in range(3)]
+    state = graph.alloc_tensors(TensorCreateInfo((m, d), DataType.FLOAT32), TensorCreateInfo((m,), DataType.FLOAT32),
+                                TensorCreateInfo((m,), DataType.FLOAT32))
+    oi, li, mi = state.get_ref(0), state.get_ref(1), state.get_ref(2)
+    dst = torch.zeros((m, d), dtype=torch.float32, device=device)
+    keep = []
+    wm = wl = wo = None
+    for k, (mb, lb, ob) in enumerate(blocks):
+        tens = [torch.from_numpy(x).to(device) for x in (mb, lb, ob)]
+        keep += tens
+        a = CoreTaskArgs()
+        a.add_input(*(ct(t) for t in tens))
+        a.add_inout(mi, li, oi, ct(dst))
+        a.add_scalar(int(k == 0), int(k == len(blocks) - 1))
+        graph.submit_task(3, a)
+        wm, wl, wo, wd = po.online_update(mb, lb, ob, wm, wl, wo, k == 0, k == len(blocks) - 1)
+    torch.cuda.synchronize(device)
+    np.testing.assert_array_equal(graph.read(mi), wm)
+    np.testing.assert_allclose(graph.read(li), wl, rtol=1e-5)
+    np.testing.assert_allclose(dst.cpu().numpy(), wd, rtol=1e-5, atol=1e-6)
+
+
+def _pa_tensors(case, d):
+    return [ct(d.query), ct(d.key_cache), ct(d.value_cache), ct(d.block_table), ct(d.context_lens)]
+
+
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_paged_attention_orchestration(device, mode, out_dtype):
+    print(f"[case] tg paged attention mode={mode} out={out_dtype}", flush=True)
+    case = make_case("cfg1_small")
+    d = case.to(device)
+    out = torch.zeros(case.out_shape(), dtype=out_dtype, device=device)
+    with TaskGraph(mode) as g:
+        g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+        assert g.task_count == 2 * (1 + 4 * 4)
+        g.launch()
+        g.wait()
+    ref = oracle_numpy(case)
+    if out_dtype == torch.bfloat16:
+        ref = torch.tensor(ref).to(torch.bfloat16).float().numpy()
+    assert_close(out.float().cpu().numpy(), ref, what=f"task graph {mode}")
+
+
+def test_paged_attention_ragged_and_multi_tile(device):
+    # 256 heads -> two 128-row q tiles per sequence (paged_attention_orch.cpp:105-106); ragged lengths
+    print("[case] tg paged attention ragged 256 heads", flush=True)
+    case = make_custom_case(batch=3, num_heads=256, kv_heads=1, head_dim=64, block_size=64,
+                            context_lens=[1, 65, 200], seed=5, max_blocks=4)
+    d = case.to(device)
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    with TaskGraph("eager") as g:
+        g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+        g.wait()
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what="task graph ragged")
+
+
+def test_bad_block_is_reported_before_any_launch(device):
+    case = make_case("cfg1_small")
+    d = case.to(device)
+    bt = d.block_table.clone()
+    bt[1, 2] = case.key_cache.shape[0] + 3
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    with TaskGraph("graph") as g:
+        with pytest.raises(TaskGraphError) as e:
+            g.orchestrate_paged_attention([ct(d.query), ct(d.key_cache), ct(d.value_cache), ct(bt),
+                                           ct(d.context_lens), ct(out)], case.scale)
+        assert e.value.rc == -6  # SIMPLER_HIP_ERR_BAD_BLOCK
+
+
+def test_hipgraph_replays_match_eager(device):
+    print("[case] tg hipGraph replays", flush=True)
+    case = make_custom_case(batch=2, num_heads=16, kv_heads=1, head_dim=128, block_size=128,
+                            context_lens=[300, 512], seed=9, max_blocks=4)
+    d = case.to(device)
+    eager_out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    with TaskGraph("eager") as g:
+        g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(eager_out)], case.scale)
+        g.wait()
+    want = eager_out.cpu().numpy()
+    out = torch.zeros_like(eager_out)
+    with TaskGraph("graph") as g:
+        for rep in range(4):
+            g.reset()
+            g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+            g.launch()
+            g.wait()
+            got = out.cpu().numpy()
+            np.testing.assert_array_equal(got, want, err_msg=f"replay {rep}")
+            out.fill_(float("nan"))  # eager work between replays
+            torch.cuda.synchronize(device)
+
+
+def test_vector_example_through_graph_api(device):
+    rng = np.random.default_rng(3)
+    a = torch.from_numpy(rng.standard_normal(128 * 128).astype(np.float32)).to(device)
+    b = torch.from_numpy(rng.standard_normal(128 * 128).astype(np.float32)).to(device)
+    f = torch.zeros_like(a)
+    for mode in ("eager", "graph"):
+        f.zero_()
+        with TaskGraph(mode) as g:
+            g.scope_begin()
+            g.orchestrate_vector_example([ct(a), ct(b), ct(f)])
+            g.scope_end()
+            g.launch()
+            g.wait()
+        an, bn = a.cpu().numpy(), b.cpu().numpy()
+        c = an + bn
+        np.testing.assert_array_equal(f.cpu().numpy(), (c + np.float32(1)) * (c + np.float32(2)) + c)
+
+
+@pytest.mark.parametrize("execution", ["eager", "graph"])
+def test_worker_runs_reference_chain_on_the_task_graph(device, execution):
+    print(f"[case] worker execution={execution}", flush=True)
+    w = Worker(level=2, platform="mi355x", device_id=device.index or 0, execution=execution)
+    w.init()
+    try:
+        case = make_custom_case(batch=4, num_heads=16, kv_heads=1, head_dim=16, block_size=16,
+                                context_lens=[33, 64, 128, 15], seed=42, max_blocks=16)  # CaseVarSeq4
+        h = w.register(pa.reference_chain_callable())
+        out = torch.zeros(case.out_shape(), dtype=torch.float32)
+        args = TaskArgs()
+        for t in (case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens):
+            args.add_tensor(t.contiguous(), TensorArgType.INPUT)
+        args.add_tensor(out, TensorArgType.OUTPUT_EXISTING)
+        args.add_scalar(ctypes.c_float(case.scale))
+        for _ in range(2):  # second run reuses the context's graph (hipGraph: updated in place)
+            out.zero_()
+            w.run(h, args)
+            assert_close(out.numpy(), oracle_numpy(case), what=f"worker {execution}")
+        # the vector example callable (reference golden: a=2, b=3 -> f=47)
+        hv = w.register(vector_example_callable())
+        va = TaskArgs()
+        a, b, f = torch.full((128 * 128,), 2.0), torch.full((128 * 128,), 3.0), torch.zeros(128 * 128)
+        va.add_tensor(a, TensorArgType.INPUT)  # TaskArgs keeps addresses only: a, b, f stay referenced here
+        va.add_tensor(b, TensorArgType.INPUT)
+        va.add_tensor(f, TensorArgType.OUTPUT_EXISTING)
+        w.run(hv, va)
+        assert torch.all(f == 47.0)
+    finally:
+        w.close()
