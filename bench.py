@@ -39,7 +39,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default=DEFAULT_CONFIG)
-    p.add_argument("--op", default="decode", choices=["decode", "kv_append", "prelude"],
+    p.add_argument("--tg-mode", default="graph", choices=["eager", "graph"],
+                   help="--op taskgraph: launch tasks as submitted, or as one hipGraph per step")
+    p.add_argument("--op", default="decode", choices=["decode", "kv_append", "prelude", "taskgraph"],
                    help="decode (the headline path); kv_append / prelude: the cache-write step before it")
     p.add_argument("--tokens", type=int, default=32768,
                    help="--op kv_append: tokens written per call (32 = one decode step of bs=32)")
@@ -185,12 +187,96 @@ def bench_kv(args) -> int:
     return 0
 
 
+def bench_taskgraph(args) -> int:
+    """The reference's unfused paged-attention chain on the task-graph backend.
+
+    A step = one run of the reference orchestration (paged_attention_orch.cpp:
+    one alloc task + QK, SF, PV, UP per KV block and 16-row head tile), from
+    the host-side DAG build (dependency inference, allocation) to the last task
+    finishing; eager launches each task as it is submitted, graph launches one
+    hipGraph with the inferred edges. The workload is the reference's own
+    runnable case (cfg1: B=2, Hq=16, Hkv=1, D=128, BS=128, L=512)."""
+    import torch
+
+    from simpler_amd import paged_attention as pa
+    from simpler_amd.task_graph import TaskGraph
+    from simpler_amd.task_interface import ChipTensor, DataType
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, make_case
+
+    cfg = CONFIGS[args.config if args.config != DEFAULT_CONFIG else "cfg1_small"]
+    dev = torch.device("cuda", 0)
+    case_cpu = make_case(cfg)
+    case = case_cpu.to(dev)
+    out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
+    out = torch.zeros(case.out_shape(), dtype=out_dtype, device=dev)
+    dt = {torch.bfloat16: DataType.BFLOAT16, torch.float32: DataType.FLOAT32, torch.int32: DataType.INT32}
+    tensors = [ChipTensor.make(t.data_ptr(), tuple(t.shape), dt[t.dtype], child_memory=True)
+               for t in (case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out)]
+    stream = torch.cuda.current_stream(dev)
+    g = TaskGraph(args.tg_mode, stream=stream.cuda_stream)
+
+    def step():
+        g.reset()
+        g.orchestrate_paged_attention(tensors, case.scale)
+        g.launch()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    ntasks = g.task_count
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = (time.perf_counter() - t0) / args.steps
+    ev_ms = start.elapsed_time(end) / args.steps
+    ms = max(ev_ms, wall * 1e3)  # the host builds each step's DAG: the wall clock bounds the step
+    # the fused kernel on the same inputs, for comparison
+    pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
+                         case.scale)
+    for _ in range(args.warmup):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    f0 = time.perf_counter()
+    for _ in range(args.steps):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    fused_us = (time.perf_counter() - f0) / args.steps * 1e6
+    g.close()
+    nbytes = algorithmic_bytes(case_cpu, out_bytes=2 if args.out_dtype == "bf16" else 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
+    line = {
+        "metric": f"{METRIC} [{cfg.name}, task graph {args.tg_mode}]",
+        "value": round(gbs, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "event_us_per_step": round(ev_ms * 1e3, 2), "wall_us_per_step": round(wall * 1e6, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.description}; reference orchestration, {ntasks} tasks per step",
+                   "tasks_per_step": ntasks, "tg_mode": args.tg_mode, "out_dtype": args.out_dtype,
+                   "fused_us_per_step": round(fused_us, 2), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                     "kernel": f"task graph step ({ntasks} launches: QK/SF/PV/UP incore kernels)",
+                     "kernel_us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                     "note": "launch-bound: per-kernel durations are in profiles/task_graph_cfg1_small.md"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the path shards by batch / kv head with no exchange, see DESIGN.md", file=sys.stderr)
         return 2
+    if args.op == "taskgraph":
+        return bench_taskgraph(args)
     if args.op != "decode":
         return bench_kv(args)
 

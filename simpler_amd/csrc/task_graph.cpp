@@ -21,14 +21,18 @@
 // tasks (the write-after-read order simpler gets from its ring buffers'
 // fanout reference counts, pto_ring_buffer.h).
 //
-// Execution: EAGER launches each task on the stream at submit; GRAPH adds a
-// kernel node per task with the fanin as its dependencies and launches the
-// instantiated hipGraph (an instantiated graph is kept per segment and
-// updated in place on the next run when the topology is unchanged).
+// Execution: EAGER launches each task on the stream at submit. GRAPH turns the
+// tasks submitted between launches (a segment) into one hipGraph, a kernel
+// node per task with its in-segment fanin as dependencies. The executable
+// graph is cached per segment index: when the next run submits the same
+// kernels, launch shapes and edges (a decode loop over stable buffers), it is
+// replayed, with hipGraphExecKernelNodeSetParams on the nodes whose parameter
+// blocks changed, instead of being rebuilt.
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <deque>
 #include <map>
 #include <new>
@@ -62,10 +66,33 @@ void tg_log(const char *fmt, ...) {
 struct Task {
     int32_t func_id = -1;
     int32_t kernel = -1;  // -1: dependency-only
-    int32_t segment = 0;
     KernelLaunch launch;
     std::vector<int32_t> fanin;
-    hipGraphNode_t node = nullptr;
+};
+
+// One node of a cached executable graph: what must match for a replay.
+struct NodeSig {
+    const void *func = nullptr;
+    size_t param_bytes = 0;
+    unsigned grid = 0, block = 0;
+    std::vector<int32_t> deps;  // producers, as indices within the segment
+};
+
+struct SegmentCache {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<hipGraphNode_t> nodes;
+    std::vector<NodeSig> sigs;
+    std::vector<std::array<unsigned char, simpler_hip::kMaxKernelParamBytes>> params;
+    void clear() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+        nodes.clear();
+        sigs.clear();
+        params.clear();
+    }
 };
 
 // A writer's view of a buffer: its byte range plus the geometry needed for
@@ -217,12 +244,11 @@ struct SimplerHipTaskGraph {
     size_t chunk_cursor = 0;
     uint64_t record_next = kRecordBase;
     std::unordered_map<uint64_t, HostCopy> host_cache;
-    // GRAPH mode
-    hipGraph_t graph = nullptr;
-    int32_t segment = 0;           // current segment index within the run
-    int32_t segment_tasks = 0;     // tasks in the pending graph
-    std::vector<hipGraphExec_t> execs;  // one per segment index, reused across runs
-    bool launched_any = false;
+    // GRAPH mode: tasks [segment_first, end) wait for the next launch; one
+    // cached executable graph per segment index, replayed across runs
+    int32_t segment = 0;
+    size_t segment_first = 0;
+    std::vector<SegmentCache> cache;
 
     SimplerHipTaskGraph() {
         for (int i = 0; i < kMaxFuncIds; ++i) func_kernel[i] = -1;
@@ -290,38 +316,113 @@ void producers_of(const SimplerHipTaskGraph *g, const SimplerChipTensor &t, std:
         if (overlap(r, t) != Overlap::kNone) out->push_back(r.producer);
 }
 
-int launch_segment(SimplerHipTaskGraph *g) {
-    if (g->mode != SIMPLER_HIP_TG_GRAPH || !g->graph) return SIMPLER_HIP_OK;
-    if (g->segment_tasks == 0) {
-        (void)hipGraphDestroy(g->graph);
-        g->graph = nullptr;
-        return SIMPLER_HIP_OK;
+hipKernelNodeParams node_params(const Task &t, void **args) {
+    args[0] = const_cast<unsigned char *>(t.launch.params);
+    hipKernelNodeParams p{};
+    p.func = const_cast<void *>(t.launch.func);
+    p.gridDim = t.launch.grid;
+    p.blockDim = t.launch.block;
+    p.sharedMemBytes = 0;
+    p.kernelParams = args;
+    p.extra = nullptr;
+    return p;
+}
+
+// Same kernel, launch shape and in-segment edges: the cached executable graph
+// can be replayed after patching the parameter blocks that changed.
+bool same_shape(const SegmentCache &c, const SimplerHipTaskGraph *g, size_t first, size_t n) {
+    if (c.sigs.size() != n) return false;
+    for (size_t i = 0; i < n; ++i) {
+        const Task &t = g->tasks[first + i];
+        const NodeSig &s = c.sigs[i];
+        if (s.func != t.launch.func || s.param_bytes != t.launch.param_bytes || s.grid != t.launch.grid.x ||
+            s.block != t.launch.block.x)
+            return false;
+        size_t k = 0;
+        for (int32_t f : t.fanin) {
+            if ((size_t)f < first) continue;  // finished in an earlier segment
+            if (k >= s.deps.size() || s.deps[k] != (int32_t)((size_t)f - first)) return false;
+            ++k;
+        }
+        if (k != s.deps.size()) return false;
     }
-    if ((size_t)g->segment >= g->execs.size()) g->execs.resize(g->segment + 1, nullptr);
-    hipGraphExec_t &exec = g->execs[g->segment];
-    if (exec) {
-        hipGraphExecUpdateResult res;
-        hipGraphNode_t err_node = nullptr;
-        if (hipGraphExecUpdate(exec, g->graph, &err_node, &res) != hipSuccess || res != hipGraphExecUpdateSuccess) {
-            (void)hipGetLastError();
-            (void)hipGraphExecDestroy(exec);
-            exec = nullptr;
+    return true;
+}
+
+int build_segment(SegmentCache &c, SimplerHipTaskGraph *g, size_t first, size_t n) {
+    c.clear();
+    if (hipGraphCreate(&c.graph, 0) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    c.nodes.resize(n);
+    c.sigs.resize(n);
+    c.params.resize(n);
+    std::vector<hipGraphNode_t> deps;
+    for (size_t i = 0; i < n; ++i) {
+        const Task &t = g->tasks[first + i];
+        NodeSig &s = c.sigs[i];
+        s.func = t.launch.func;
+        s.param_bytes = t.launch.param_bytes;
+        s.grid = t.launch.grid.x;
+        s.block = t.launch.block.x;
+        deps.clear();
+        for (int32_t f : t.fanin)
+            if ((size_t)f >= first) {
+                s.deps.push_back((int32_t)((size_t)f - first));
+                deps.push_back(c.nodes[(size_t)f - first]);
+            }
+        hipError_t e;
+        if (t.kernel < 0) {
+            e = hipGraphAddEmptyNode(&c.nodes[i], c.graph, deps.data(), deps.size());
+        } else {
+            void *args[1];
+            const hipKernelNodeParams p = node_params(t, args);
+            e = hipGraphAddKernelNode(&c.nodes[i], c.graph, deps.data(), deps.size(), &p);
+            memcpy(c.params[i].data(), t.launch.params, t.launch.param_bytes);
+        }
+        if (e != hipSuccess) {
+            tg_log("adding graph node failed: %s", hipGetErrorString(e));
+            c.clear();
+            return SIMPLER_HIP_ERR_LAUNCH;
         }
     }
-    if (!exec && hipGraphInstantiate(&exec, g->graph, nullptr, nullptr, 0) != hipSuccess) {
+    if (hipGraphInstantiate(&c.exec, c.graph, nullptr, nullptr, 0) != hipSuccess) {
         tg_log("hipGraphInstantiate failed");
-        exec = nullptr;
+        c.clear();
         return SIMPLER_HIP_ERR_LAUNCH;
     }
-    if (hipGraphLaunch(exec, g->stream) != hipSuccess) {
+    return SIMPLER_HIP_OK;
+}
+
+// GRAPH mode: run the tasks submitted since the last launch as one hipGraph.
+int launch_segment(SimplerHipTaskGraph *g) {
+    if (g->mode != SIMPLER_HIP_TG_GRAPH) return SIMPLER_HIP_OK;
+    const size_t first = g->segment_first, n = g->tasks.size() - first;
+    if (n == 0) return SIMPLER_HIP_OK;
+    if ((size_t)g->segment >= g->cache.size()) g->cache.resize(g->segment + 1);
+    SegmentCache &c = g->cache[g->segment];
+    if (c.exec && same_shape(c, g, first, n)) {
+        for (size_t i = 0; i < n; ++i) {
+            const Task &t = g->tasks[first + i];
+            if (t.kernel < 0 || memcmp(c.params[i].data(), t.launch.params, t.launch.param_bytes) == 0) continue;
+            void *args[1];
+            const hipKernelNodeParams p = node_params(t, args);
+            if (hipGraphExecKernelNodeSetParams(c.exec, c.nodes[i], &p) != hipSuccess) {
+                (void)hipGetLastError();
+                c.clear();
+                break;
+            }
+            memcpy(c.params[i].data(), t.launch.params, t.launch.param_bytes);
+        }
+    }
+    if (!c.exec || !same_shape(c, g, first, n)) {
+        const int rc = build_segment(c, g, first, n);
+        if (rc != SIMPLER_HIP_OK) return rc;
+    }
+    if (hipGraphLaunch(c.exec, g->stream) != hipSuccess) {
         tg_log("hipGraphLaunch failed");
         return SIMPLER_HIP_ERR_LAUNCH;
     }
-    (void)hipGraphDestroy(g->graph);
-    g->graph = nullptr;
-    g->segment_tasks = 0;
+    g->segment_first = g->tasks.size();
     ++g->segment;
-    g->launched_any = true;
     return SIMPLER_HIP_OK;
 }
 
@@ -332,41 +433,14 @@ int drain(SimplerHipTaskGraph *g) {
     return sync_stream(g);
 }
 
+// EAGER: launch now. GRAPH: the task waits in the segment until launch.
 int record_task(SimplerHipTaskGraph *g, Task &t) {
-    if (g->mode == SIMPLER_HIP_TG_RECORD_ONLY) return SIMPLER_HIP_OK;
-    if (g->mode == SIMPLER_HIP_TG_EAGER) {
-        if (t.kernel < 0) return SIMPLER_HIP_OK;
-        void *args[1] = {t.launch.params};
-        if (hipLaunchKernel(t.launch.func, t.launch.grid, t.launch.block, args, 0, g->stream) != hipSuccess) {
-            tg_log("launch of kernel %d failed: %s", t.kernel, hipGetErrorString(hipGetLastError()));
-            return SIMPLER_HIP_ERR_LAUNCH;
-        }
-        return SIMPLER_HIP_OK;
-    }
-    if (!g->graph && hipGraphCreate(&g->graph, 0) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
-    std::vector<hipGraphNode_t> deps;
-    deps.reserve(t.fanin.size());
-    for (int32_t f : t.fanin)
-        if (g->tasks[f].segment == g->segment && g->tasks[f].node) deps.push_back(g->tasks[f].node);
-    hipError_t e;
-    if (t.kernel < 0) {
-        e = hipGraphAddEmptyNode(&t.node, g->graph, deps.data(), deps.size());
-    } else {
-        void *args[1] = {t.launch.params};
-        hipKernelNodeParams p{};
-        p.func = const_cast<void *>(t.launch.func);
-        p.gridDim = t.launch.grid;
-        p.blockDim = t.launch.block;
-        p.sharedMemBytes = 0;
-        p.kernelParams = args;
-        p.extra = nullptr;
-        e = hipGraphAddKernelNode(&t.node, g->graph, deps.data(), deps.size(), &p);
-    }
-    if (e != hipSuccess) {
-        tg_log("adding graph node failed: %s", hipGetErrorString(e));
+    if (g->mode != SIMPLER_HIP_TG_EAGER || t.kernel < 0) return SIMPLER_HIP_OK;
+    void *args[1] = {t.launch.params};
+    if (hipLaunchKernel(t.launch.func, t.launch.grid, t.launch.block, args, 0, g->stream) != hipSuccess) {
+        tg_log("launch of kernel %d failed: %s", t.kernel, hipGetErrorString(hipGetLastError()));
         return SIMPLER_HIP_ERR_LAUNCH;
     }
-    ++g->segment_tasks;
     return SIMPLER_HIP_OK;
 }
 
@@ -412,9 +486,7 @@ void simpler_hip_tg_destroy(SimplerHipTaskGraph *g) {
     if (!g) return;
     if (device_mode(g)) {
         sync_stream(g);
-        if (g->graph) (void)hipGraphDestroy(g->graph);
-        for (hipGraphExec_t e : g->execs)
-            if (e) (void)hipGraphExecDestroy(e);
+        for (SegmentCache &c : g->cache) c.clear();
         for (Chunk &c : g->chunks) (void)hipFree(c.base);
     }
     delete g;
@@ -505,7 +577,6 @@ int64_t simpler_hip_tg_submit(SimplerHipTaskGraph *g, int32_t func_id, const Sim
     Task t;
     t.func_id = func_id;
     t.kernel = kernel;
-    t.segment = g->segment;
     std::vector<int32_t> &fanin = t.fanin;
     for (int i = 0; i < nd; ++i) fanin.push_back((int32_t)(explicit_deps[i] & 0xffffffffu));
 
@@ -674,10 +745,6 @@ int simpler_hip_tg_wait(SimplerHipTaskGraph *g) {
 int simpler_hip_tg_reset(SimplerHipTaskGraph *g) {
     if (!g) return SIMPLER_HIP_ERR_INVALID;
     const int rc = sync_stream(g);
-    if (g->graph) {
-        (void)hipGraphDestroy(g->graph);
-        g->graph = nullptr;
-    }
     g->tasks.clear();
     g->tmap.clear();
     g->buf_of.clear();
@@ -689,7 +756,7 @@ int simpler_hip_tg_reset(SimplerHipTaskGraph *g) {
     g->chunk_cursor = 0;
     g->record_next = kRecordBase;
     g->segment = 0;
-    g->segment_tasks = 0;
+    g->segment_first = 0;
     return rc;
 }
 

@@ -201,16 +201,26 @@ def test_hipgraph_replays_match_eager(device):
         g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(eager_out)], case.scale)
         g.wait()
     want = eager_out.cpu().numpy()
-    out = torch.zeros_like(eager_out)
+    # a second query/out pair: replays alternate between them, so the cached
+    # graph's kernel parameters are patched in place every other run
+    q2 = (d.query.float() * -0.5).to(torch.bfloat16).contiguous()
+    eager2 = torch.zeros_like(eager_out)
+    with TaskGraph("eager") as g:
+        g.orchestrate_paged_attention([ct(q2)] + _pa_tensors(case, d)[1:] + [ct(eager2)], case.scale)
+        g.wait()
+    want2 = eager2.cpu().numpy()
+    out, out2 = torch.zeros_like(eager_out), torch.zeros_like(eager_out)
     with TaskGraph("graph") as g:
-        for rep in range(4):
+        for rep in range(6):
             g.reset()
-            g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+            alt = rep % 2 == 1
+            tensors = ([ct(q2)] + _pa_tensors(case, d)[1:] + [ct(out2)]) if alt else (_pa_tensors(case, d) + [ct(out)])
+            g.orchestrate_paged_attention(tensors, case.scale)
             g.launch()
             g.wait()
-            got = out.cpu().numpy()
-            np.testing.assert_array_equal(got, want, err_msg=f"replay {rep}")
-            out.fill_(float("nan"))  # eager work between replays
+            got = (out2 if alt else out).cpu().numpy()
+            np.testing.assert_array_equal(got, want2 if alt else want, err_msg=f"replay {rep}")
+            (out2 if alt else out).fill_(float("nan"))  # eager work between replays
             torch.cuda.synchronize(device)
 
 
