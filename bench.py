@@ -73,8 +73,13 @@ def cpu_baseline(case, args) -> dict | None:
     def bits(t):
         return t.contiguous().view(__import__("torch").int16).numpy().view(np.uint16)
 
-    q, k = bits(case.query), bits(case.key_cache)
-    v = None if c.mla else bits(case.value_cache)
+    kc, vc = case.key_cache, case.value_cache
+    if case.fp8:  # power-of-two scales: the dequantised caches are exactly bf16
+        from simpler_amd.workloads import dequantize_kv_fp8
+        kc = dequantize_kv_fp8(kc, case.k_scale).to(__import__("torch").bfloat16)
+        vc = dequantize_kv_fp8(vc, case.v_scale).to(__import__("torch").bfloat16)
+    q, k = bits(case.query), bits(kc)
+    v = None if c.mla else bits(vc)
     bt, cl = case.block_table.numpy(), case.context_lens.numpy()
     out = np.zeros((c.batch, c.q_len, c.num_heads, c.head_dim_v), dtype=np.float32)
     runs, t0 = 0, time.perf_counter()
@@ -95,7 +100,8 @@ def cpu_baseline(case, args) -> dict | None:
         "kind": "port",
         "sample": f"full {c.name} decode step (all {c.batch}x{c.kv_heads} sequence/kv-head items), "
                   f"{runs} repetitions in {el:.1f} s, C restatement of the reference QK/SF/PV/UP kernels "
-                  f"(oracle/pa_oracle.c), {threads} pthreads",
+                  f"(oracle/pa_oracle.c), {threads} pthreads"
+                  + ("; fp8 caches given to it dequantised (bf16-exact), bytes counted as fp8" if case.fp8 else ""),
     }
 
 
@@ -296,7 +302,8 @@ def main() -> int:
     out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
     out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
     pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
-                         case.scale, causal=cfg.causal, num_workers=args.workers)
+                         case.scale, causal=cfg.causal, num_workers=args.workers, k_scale=case.k_scale,
+                         v_scale=case.v_scale)
     workers = pa.plan(pargs)
     kernel_name = pa.kernel_name(pargs)
     stream = torch.cuda.current_stream(dev)
@@ -383,6 +390,7 @@ def main() -> int:
             "block_size": cfg.block_size,
             "context_tokens": int(case_cpu.context_lens.sum()),
             "out_dtype": args.out_dtype,
+            "kv_format": "fp8_e4m3fn + fp32 scale per (block, kv head); bf16 MFMA" if case_cpu.fp8 else "bf16",
             "workers": workers,
             "parallelism": "single GPU",
         },

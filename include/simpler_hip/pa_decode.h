@@ -39,11 +39,16 @@ enum {
  * (src/common/task_interface/data_type.h:47-67). */
 enum { SIMPLER_HIP_DT_FLOAT32 = 0, SIMPLER_HIP_DT_FLOAT16 = 1, SIMPLER_HIP_DT_BFLOAT16 = 6 };
 
+/* KV-cache element formats. FP8_E4M3: OCP E4M3FN bytes (the reference's
+ * DataType FP8E4M3FN, data_type.h:63) with one fp32 scale per (physical block,
+ * kv head); head dims 128, block sizes 16/32/64/128, GQA path (not MLA). */
+enum { SIMPLER_HIP_KV_BF16 = 0, SIMPLER_HIP_KV_FP8_E4M3 = 1 };
+
 /*
  * One paged-attention decode call. All pointers are device pointers.
  *
  * query        bf16 [batch, q_len, num_heads, head_dim_k]   (q_len = 1: [batch, num_heads, Dk])
- * key_cache    bf16, element (blk, t, kvh, d) at
+ * key_cache    bf16 (or fp8, see kv_format), element (blk, t, kvh, d) at
  *              blk*k_block_stride + t*k_token_stride + kvh*k_head_stride + d
  *              (contiguous BSND [num_blocks, block_size, kv_heads, Dk]:
  *               strides BS*Hkv*Dk, Hkv*Dk, Dk)
@@ -80,7 +85,13 @@ typedef struct SimplerHipPaDecodeArgs {
     /* 0 = one worker wavefront per wave slot of the device; > 0 forces the
      * number of workers the (tile, KV block) work list is divided among. */
     int32_t num_workers;
-    int32_t reserved;
+    /* SIMPLER_HIP_KV_BF16 (0) or SIMPLER_HIP_KV_FP8_E4M3 (1). */
+    int32_t kv_format;
+    /* kv_format FP8_E4M3 only: fp32 [num_blocks, num_kv_heads] dequantisation
+     * scales; cache element (blk, t, kvh, d) stands for
+     * fp8_e4m3fn(byte) * scale[blk * num_kv_heads + kvh]. NULL otherwise. */
+    const float *k_scale;
+    const float *v_scale;
 } SimplerHipPaDecodeArgs;
 
 /* Bytes of device workspace simpler_hip_pa_decode needs for these args

@@ -256,3 +256,27 @@ def online_update(mij, lij, oi_new, mi, li, oi, is_first: bool, is_last: bool):
     o2 = (oi * alpha[:, None] + oi_new * beta[:, None]).astype(np.float32)
     dst = (o2 / l2[:, None]).astype(np.float32) if is_last else None
     return mn, l2, o2, dst
+
+
+# ---------------------------------------------------------------------------
+# fp8 KV caches (E4M3FN bytes + one fp32 scale per (block, kv head)). There is
+# no reference kernel for this format (the reference defines the dtype code,
+# src/common/task_interface/data_type.h:63); the oracle dequantises and runs
+# the golden above on the fp32 values.
+# ---------------------------------------------------------------------------
+
+
+def fp8_e4m3fn_to_f32(b: np.ndarray) -> np.ndarray:
+    """OCP E4M3FN decode: sign, 4 exponent bits (bias 7), 3 mantissa bits;
+    exponent 0 is subnormal (m · 2^-9); S.1111.111 is NaN; no infinities."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int32)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e, m = (b >> 3) & 0xF, b & 0x7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    val = np.where((e == 0xF) & (m == 0x7), np.nan, val)
+    return (sign * val).astype(np.float32)
+
+
+def dequantize_kv(cache8: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """``[nblk, BS, Hkv, D]`` E4M3FN bytes and ``[nblk, Hkv]`` scales -> fp32 values."""
+    return (fp8_e4m3fn_to_f32(cache8) * np.asarray(scale, np.float32)[:, None, :, None]).astype(np.float32)

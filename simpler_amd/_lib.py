@@ -55,7 +55,9 @@ class PaDecodeArgs(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("causal", ctypes.c_int32),
         ("num_workers", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("kv_format", ctypes.c_int32),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
     ]
 
 

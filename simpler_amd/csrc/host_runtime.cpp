@@ -205,9 +205,27 @@ int decode_pa_args(const SimplerChipStorageTaskArgs *a, SimplerHipPaDecodeArgs &
     const SimplerChipTensor &q = tensor_at(a, 0), &k = tensor_at(a, 1), &v = tensor_at(a, 2);
     const SimplerChipTensor &bt = tensor_at(a, 3), &cl = tensor_at(a, 4), &o = tensor_at(a, 5);
     memset(&pa, 0, sizeof(pa));
-    if (q.dtype != SIMPLER_DT_BFLOAT16 || k.dtype != SIMPLER_DT_BFLOAT16 || v.dtype != SIMPLER_DT_BFLOAT16) {
-        logf("query/key_cache/value_cache must be BFLOAT16");
+    // fp8 caches: FP8E4M3FN key/value caches, then tensors 6 and 7 = fp32
+    // [num_blocks, kv_heads] K and V scales (no reference counterpart)
+    const bool fp8 = k.dtype == SIMPLER_DT_FP8E4M3FN;
+    if (q.dtype != SIMPLER_DT_BFLOAT16 || (!fp8 && k.dtype != SIMPLER_DT_BFLOAT16) || v.dtype != k.dtype) {
+        logf("query must be BFLOAT16 and key_cache/value_cache both BFLOAT16 or both FP8E4M3FN");
         return SIMPLER_HIP_ERR_UNSUPPORTED;
+    }
+    if (fp8) {
+        if (a->tensor_count_ < kPaTensors + 2) {
+            logf("fp8 caches need tensors 6 and 7: k_scale and v_scale, fp32 [num_blocks, kv_heads]");
+            return SIMPLER_HIP_ERR_INVALID;
+        }
+        for (int i = kPaTensors; i < kPaTensors + 2; ++i) {
+            const SimplerChipTensor &sc = tensor_at(a, i);
+            if (sc.dtype != SIMPLER_DT_FLOAT32 || sc.ndims != 2 || !contiguous(sc) || sc.shapes[0] != k.shapes[0] ||
+                sc.shapes[1] != (k.ndims == 4 ? k.shapes[2] : 1)) {
+                logf("k_scale/v_scale must be contiguous fp32 [num_blocks, kv_heads]");
+                return SIMPLER_HIP_ERR_INVALID;
+            }
+        }
+        pa.kv_format = SIMPLER_HIP_KV_FP8_E4M3;
     }
     if (bt.dtype != SIMPLER_DT_INT32 || cl.dtype != SIMPLER_DT_INT32 || bt.ndims != 2 || cl.ndims != 1) {
         logf("block_table must be INT32 [B, max_blocks] and context_lens INT32 [B]");
@@ -544,11 +562,13 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
     if (cb.kind == kPagedAttention) {
         r->n_tensors = kPaTensors;
         rc = decode_pa_args(a, r->args, 1);
+        if (rc == SIMPLER_HIP_OK && r->args.kv_format == SIMPLER_HIP_KV_FP8_E4M3) r->n_tensors = kPaTensors + 2;
         if (rc == SIMPLER_HIP_OK) rc = check_host_tables(a, r->args);
         if (rc == SIMPLER_HIP_OK && r->execution != SIMPLER_HIP_EXEC_FUSED &&
-            (r->args.num_kv_heads != 1 || r->args.q_len != 1 || r->args.head_dim_k != r->args.head_dim_v)) {
+            (r->args.num_kv_heads != 1 || r->args.q_len != 1 || r->args.head_dim_k != r->args.head_dim_v ||
+             r->args.kv_format != SIMPLER_HIP_KV_BF16)) {
             logf("task-graph paged attention runs the reference orchestration: one KV head, one query token, "
-                 "Dk == Dv");
+                 "Dk == Dv, bf16 caches");
             rc = SIMPLER_HIP_ERR_UNSUPPORTED;
         }
         r->scale_bits = a->scalars_[0];
@@ -608,6 +628,10 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
         r->args.block_table = (const int32_t *)dev[3];
         r->args.context_lens = (const int32_t *)dev[4];
         r->args.out = (void *)dev[5];
+        if (r->args.kv_format == SIMPLER_HIP_KV_FP8_E4M3) {
+            r->args.k_scale = (const float *)dev[6];
+            r->args.v_scale = (const float *)dev[7];
+        }
         const size_t need = simpler_hip_pa_decode_workspace_size(&r->args);
         if (need == 0) {
             release_staged(r);

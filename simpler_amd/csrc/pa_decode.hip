@@ -87,6 +87,8 @@ struct KernelParams {
     float *part_ml;  // [workers][2 slots][m[16], l[16]]
     unsigned *error_flag;
     const char *zeros;  // 256 bytes of the workspace that stay zero (LDS fill source)
+    const float *k_scale;  // fp8 caches: [num_blocks][kv_heads] dequantisation scales
+    const float *v_scale;
     int64_t k_block_stride, k_token_stride, k_head_stride;
     int64_t v_block_stride, v_token_stride, v_head_stride;
     int32_t batch, q_len, num_heads, kv_heads, group, rows, row_tiles;
@@ -113,6 +115,20 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
     // fp32 -> bf16 round-to-nearest-even (gfx950: v_cvt_pk_bf16_f32)
     const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
     return __builtin_bit_cast(unsigned, h);
+}
+
+// Four E4M3FN bytes -> four bf16 (two words); exact (every E4M3FN value is a
+// bf16 value). gfx950 v_cvt_scalef32_pk_bf16_fp8 with scale 1.
+__device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
+    const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    return (u32x2_t){__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi)};
+}
+
+// Eight E4M3FN bytes (two words) -> eight bf16 (one 16-byte MFMA operand).
+__device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(unsigned w0, unsigned w1) {
+    const u32x2_t a = fp8x4_to_bf16x4(w0), b = fp8x4_to_bf16x4(w1);
+    return (u32x4_t){a[0], a[1], b[0], b[1]};
 }
 
 __device__ __forceinline__ float bf16lo_to_f32(unsigned w) { return __uint_as_float(w << 16); }
@@ -238,13 +254,24 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // One segment: KV blocks [blk_begin, blk_end) of tile (b, kvh, rt)
 // ---------------------------------------------------------------------------
 
-template <int BS, int DK, int DV, typename OutT, bool V_SHARED>
+// KV8: K and V caches hold E4M3FN bytes with one fp32 scale per (block, kv
+// head). They are widened to bf16 in registers (exact) right before the
+// MFMAs. The K scale folds into the softmax scale. The V scale is carried as
+// the accumulator's frame: A is kept in units of the V scale of the last block
+// it absorbed, and moving to a block with another scale multiplies the
+// rescale factor by old/new. Each K load then reads 16 dims (16 bytes) of a
+// token, so the QK contraction visits dims in a permuted order: k-step kk of
+// lane group qd holds dims 16·qd + 64·(kk/2) + 8·(kk%2) .. +7, and Q is loaded
+// in the same order.
+template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
     constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
     constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
+    constexpr int ESZ = KV8 ? 1 : 2;       // cache element bytes
+    static_assert(!KV8 || (DK % 64 == 0 && DV % 128 == 0), "fp8 caches: head dims multiple of 64 (K), 128 (V)");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -260,10 +287,11 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     if (pc < rows_here) {
         const int r = rt * 16 + pc;
         const int i = r / P.group, hh = r - i * P.group;
-        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK + 8 * qd;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
-            if (DK % 32 == 0 || 32 * kk + 8 * qd < DK) qv[kk] = ld16(qrow + 32 * kk);
+            const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
+            if (DK % 32 == 0 || dim < DK) qv[kk] = ld16(qrow + dim);
         }
         rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
     }
@@ -283,16 +311,19 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     float m_run = kNegClamp, f_run = kNegClamp, l_part = 0.f;
 
-    u32x4_t kreg[NT][KS];
-    u32x4_t vreg[NT][DVS][4];
+    // bf16: the operands themselves; fp8: the raw bytes (half the registers)
+    u32x4_t kreg[NT][KV8 ? KS / 2 : KS];
+    u32x4_t vreg[NT][DVS][KV8 ? 1 : 4];
+    u32x2_t vraw[NT][DVS][KV8 ? 4 : 1];
+    float vs_frame = 1.f;  // KV8: the V scale A is expressed in (this lane's row)
 
     // Addresses: a wave-uniform byte base plus one 32-bit per-lane offset that
     // is the same for every block.
-    const int64_t k_tok_b = P.k_token_stride * 2, v_tok_b = P.v_token_stride * 2;
+    const int64_t k_tok_b = P.k_token_stride * ESZ, v_tok_b = P.v_token_stride * ESZ;
     const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
-    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 16 * pc);
-    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
-    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * 2;
+    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 8 * ESZ * pc);
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * ESZ;
+    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * ESZ;
 
     auto phys_of = [&](int blk, bool &bad) -> int {
         if (blk - bt_base >= kBlockTableWindow) {  // blocks are visited in order
@@ -304,13 +335,13 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         return bad ? 0 : phys;
     };
     auto load_k = [&](int phys) {
-        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * ESZ;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const char *kt = kb + (int64_t)(16 * t) * k_tok_b;
 #pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-                if (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
+            for (int kk = 0; kk < (KV8 ? KS / 2 : KS); ++kk) {
+                if (KV8 || DK % 32 == 0 || 32 * kk + 8 * qd < DK)
                     kreg[t][kk] = *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk);
                 else
                     kreg[t][kk] = (u32x4_t){0u, 0u, 0u, 0u};
@@ -318,7 +349,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         }
     };
     auto load_v = [&](int phys) {
-        const char *vb = v_head + (int64_t)phys * P.v_block_stride * 2;
+        const char *vb = v_head + (int64_t)phys * P.v_block_stride * ESZ;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -326,11 +357,15 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 const char *vt = vb + (int64_t)(16 * t + e) * v_tok_b;
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds) {
-                    if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
+                    if constexpr (KV8) {
+                        const u32x2_t *src = reinterpret_cast<const u32x2_t *>(vt + v_lane + 128 * ds);
+                        vraw[t][ds][e] = V_SHARED ? *src : __builtin_nontemporal_load(src);
+                    } else if (DV % 128 == 0 || 128 * ds + 8 * pc < DV) {
                         vreg[t][ds][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds)
                                                   : stream_ld16(vt + v_lane + 256 * ds);
-                    else
+                    } else {
                         vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                    }
                 }
             }
     };
@@ -348,6 +383,12 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const bool blk_bad = bad;
         if (blk_bad && lane == 0) atomicOr(P.error_flag, 1u);
         load_v(phys);
+        float sc = P.scale, vs = 1.f;
+        if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform)
+            const int64_t si = (int64_t)phys * P.kv_heads + kvh;
+            sc = P.scale * P.k_scale[si];
+            vs = P.v_scale[si];
+        }
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- QK: S^T tiles ----
@@ -356,9 +397,17 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         for (int t = 0; t < NT; ++t) {
             f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[t][kk]),
+            for (int kk = 0; kk < KS; ++kk) {
+                u32x4_t kop;
+                if constexpr (KV8) {
+                    const u32x4_t raw = kreg[t][kk >> 1];
+                    kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
+                } else {
+                    kop = kreg[t][kk];
+                }
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kop),
                                                             __builtin_bit_cast(bf16x8_t, qv[kk]), c, 0, 0, 0);
+            }
             s[t] = c;
         }
 
@@ -379,7 +428,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float x = s[t][e] * P.scale;
+                float x = s[t][e] * sc;
                 if (!full) x = (16 * t + 4 * qd + e < rvalid) ? x : -INFINITY;
                 s[t][e] = x;
                 mx = fmaxf(mx, x);
@@ -393,7 +442,12 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const bool use = first || (mb >= mnew - kFrameGap);
         const float alpha = first ? 0.f : __expf(m_run - mnew);
         const float beta = __expf(mb - mnew);
-        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        const bool v_zero = KV8 && vs == 0.f;  // this block's V is zero: nothing to add
+        if (KV8 && use && !v_zero) {            // move this row's A into the block's V-scale frame
+            cf *= vs_frame / vs;
+            vs_frame = vs;
+        }
 
         // ---- p = bf16(exp(s - m_blk)); l_blk = sum of the rounded p ----
         i16x4_t pa[NT];
@@ -424,23 +478,34 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         }
 
         // ---- PV: A += P * V ----
-        const int vvalid = blk_bad ? 0 : min(BS, ctx - blk0);  // tokens with defined V
+        const int vvalid = (blk_bad || v_zero) ? 0 : min(BS, ctx - blk0);  // tokens with defined V
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
+            if (KV8 && v_zero) break;  // wave-uniform: the block adds nothing
+            u32x4_t vt4[DVS][4];       // 8 bf16 dims of tokens 16t + 4qd + e
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (KV8)
+                        vt4[ds][e] = fp8x8_to_bf16x8(vraw[t][ds][e][0], vraw[t][ds][e][1]);
+                    else
+                        vt4[ds][e] = vreg[t][ds][e];
+                }
             if (vvalid < BS) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (16 * t + 4 * qd + e >= vvalid)
 #pragma unroll
-                        for (int ds = 0; ds < DVS; ++ds) vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                        for (int ds = 0; ds < DVS; ++ds) vt4[ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
                     const int w = jj >> 1;
-                    const unsigned a0 = vreg[t][ds][0][w], a1 = vreg[t][ds][1][w];
-                    const unsigned a2 = vreg[t][ds][2][w], a3 = vreg[t][ds][3][w];
+                    const unsigned a0 = vt4[ds][0][w], a1 = vt4[ds][1][w];
+                    const unsigned a2 = vt4[ds][2][w], a3 = vt4[ds][3][w];
                     unsigned d0, d1;
                     if (jj & 1) {
                         d0 = (a0 >> 16) | (a1 & 0xffff0000u);
@@ -458,7 +523,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     // ---- finish: O = e^{f-m} A, l = sum over the four lane groups ----
     float l_tot = l_part + __shfl_xor(l_part, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
-    const float osc = __expf(f_run - m_run);
+    const float osc = __expf(f_run - m_run) * vs_frame;
     float l_e[4], o_e[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -513,7 +578,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 // four sibling waves, one per row tile, walk the same KV blocks, so V is loaded
 // through the caches (the siblings hit each other's lines) rather than
 // streamed past them.
-template <int BS, int DK, int DV, typename OutT, int MAXW>
+template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
@@ -539,7 +604,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
         float *po = P.part_o + piece * 16 * DV;
         float *pml = P.part_ml + piece * 32;
-        if (rt < P.row_tiles) run_segment<BS, DK, DV, OutT, (MAXW > 1)>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
+        if (rt < P.row_tiles)
+            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -1110,11 +1176,16 @@ int validate(const SimplerHipPaDecodeArgs *a) {
     if (a->block_size < 1 || a->max_blocks_per_seq < 1 || a->num_blocks < 1) return SIMPLER_HIP_ERR_INVALID;
     const int64_t strides[6] = {a->k_block_stride, a->k_token_stride, a->k_head_stride,
                                 a->v_block_stride, a->v_token_stride, a->v_head_stride};
+    if (a->kv_format != SIMPLER_HIP_KV_BF16 && a->kv_format != SIMPLER_HIP_KV_FP8_E4M3) return SIMPLER_HIP_ERR_INVALID;
+    const bool fp8 = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3;
+    const int esz = fp8 ? 1 : 2;
     for (int64_t s : strides)
-        if (s <= 0 || s % 8) return SIMPLER_HIP_ERR_INVALID;  // 16-byte aligned rows
-    if (a->k_token_stride * 2 * a->block_size >= (int64_t)1 << 31 ||
-        a->v_token_stride * 2 * a->block_size >= (int64_t)1 << 31)
+        if (s <= 0 || (s * esz) % 16) return SIMPLER_HIP_ERR_INVALID;  // 16-byte aligned rows
+    if (a->k_token_stride * esz * a->block_size >= (int64_t)1 << 31 ||
+        a->v_token_stride * esz * a->block_size >= (int64_t)1 << 31)
         return SIMPLER_HIP_ERR_INVALID;  // per-lane 32-bit byte offsets within a block
+    if (fp8 && (!a->k_scale || !a->v_scale || ((uintptr_t)a->k_scale & 3) || ((uintptr_t)a->v_scale & 3)))
+        return SIMPLER_HIP_ERR_INVALID;
     if (a->out_dtype != SIMPLER_HIP_DT_FLOAT32 && a->out_dtype != SIMPLER_HIP_DT_BFLOAT16)
         return SIMPLER_HIP_ERR_UNSUPPORTED;
     if (!(a->scale == a->scale)) return SIMPLER_HIP_ERR_INVALID;
@@ -1137,10 +1208,23 @@ struct KernelPair {
     bool mla;
 };
 
-template <int BS, int D, typename OutT>
+template <int BS, int D, typename OutT, bool KV8 = false>
 KernelPair pick_fn() {
-    return {pa_decode_kernel<BS, D, D, OutT, 1>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker>,
+    return {pa_decode_kernel<BS, D, D, OutT, 1, KV8>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, KV8>,
             pa_merge_kernel<D, OutT>, false};
+}
+
+// fp8 caches: head dim 128 (Llama/Qwen GQA), the four block sizes.
+template <typename OutT>
+KernelPair pick_fp8(int bs, int dk, int dv) {
+    if (dk != 128 || dv != 128) return {nullptr, nullptr, nullptr, false};
+    switch (bs) {
+        case 16: return pick_fn<16, 128, OutT, true>();
+        case 32: return pick_fn<32, 128, OutT, true>();
+        case 64: return pick_fn<64, 128, OutT, true>();
+        case 128: return pick_fn<128, 128, OutT, true>();
+        default: return {nullptr, nullptr, nullptr, false};
+    }
 }
 
 template <int BS, typename OutT>
@@ -1189,6 +1273,12 @@ KernelPair pick_mla(int bs) {
 }
 
 KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
+    if (a->kv_format == SIMPLER_HIP_KV_FP8_E4M3) {
+        if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_fp8<float>(a->block_size, a->head_dim_k, a->head_dim_v);
+        if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
+            return pick_fp8<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
+        return {nullptr, nullptr, nullptr, false};
+    }
     if (is_mla_shape(a)) {
         if (!v_is_k_prefix(a)) return {nullptr, nullptr, nullptr, false};
         if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_mla<float>(a->block_size);
@@ -1372,6 +1462,8 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.workers = plan.workers;
     P.scale = a->scale;
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
+    P.k_scale = a->k_scale;
+    P.v_scale = a->v_scale;
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {

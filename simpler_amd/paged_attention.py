@@ -26,6 +26,9 @@ from .task_interface import ArgDirection, ChipCallable, CoreCallable, DataType
 NATIVE_CALLABLE_NAME = "simpler_hip_paged_attention_decode"
 
 _OUT_DTYPES = {torch.float32: int(DataType.FLOAT32), torch.bfloat16: int(DataType.BFLOAT16)}
+# fp8 KV caches (E4M3FN bytes, include/simpler_hip/pa_decode.h SIMPLER_HIP_KV_FP8_E4M3)
+KV_BF16, KV_FP8_E4M3 = 0, 1
+_FP8_DTYPES = (torch.float8_e4m3fn, torch.uint8)
 _ERRORS = {
     -1: "invalid argument (shape, dtype, stride or alignment)",
     -2: "unsupported configuration",
@@ -89,11 +92,30 @@ def make_args(
     *,
     causal: bool = False,
     num_workers: int = 0,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
 ) -> _lib.PaDecodeArgs:
-    """Validate torch tensors and fill the C ``SimplerHipPaDecodeArgs``."""
+    """Validate torch tensors and fill the C ``SimplerHipPaDecodeArgs``.
+
+    fp8 caches: ``key_cache``/``value_cache`` of dtype ``torch.float8_e4m3fn``
+    (or uint8 holding E4M3FN bytes) with ``k_scale``/``v_scale`` fp32
+    ``[num_blocks, num_kv_heads]``: element (blk, t, h, d) stands for
+    ``float(cache[blk, t, h, d]) * scale[blk, h]``.
+    """
+    fp8 = key_cache.dtype in _FP8_DTYPES
+    kv_dtype = key_cache.dtype if fp8 else torch.bfloat16
     _check(query, "query", torch.bfloat16, (3, 4))
-    _check(key_cache, "key_cache", torch.bfloat16, (4,))
-    _check(value_cache, "value_cache", torch.bfloat16, (4,))
+    _check(key_cache, "key_cache", kv_dtype, (4,))
+    _check(value_cache, "value_cache", kv_dtype, (4,))
+    if fp8:
+        if k_scale is None or v_scale is None:
+            raise ValueError("fp8 caches need k_scale and v_scale ([num_blocks, num_kv_heads] float32)")
+        for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+            _check(t, name, torch.float32, (2,))
+            if not t.is_contiguous() or tuple(t.shape) != (key_cache.shape[0], key_cache.shape[2]):
+                raise ValueError(f"{name} must be a contiguous [num_blocks, num_kv_heads] tensor")
+    elif k_scale is not None or v_scale is not None:
+        raise ValueError("k_scale/v_scale apply to fp8 caches only")
     _check(block_table, "block_table", torch.int32, (2,))
     _check(context_lens, "context_lens", torch.int32, (1,))
     if out.dtype not in _OUT_DTYPES:
@@ -132,6 +154,9 @@ def make_args(
     a.scale = float(scale)
     a.causal = 1 if causal else 0
     a.num_workers = int(num_workers)
+    if fp8:
+        a.kv_format = KV_FP8_E4M3
+        a.k_scale, a.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
     return a
 
 
@@ -172,6 +197,8 @@ def paged_attention_decode(
     causal: bool = False,
     out_dtype: torch.dtype = torch.float32,
     num_workers: int = 0,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Fused paged-attention decode; returns ``out`` ``[B, (q_len,) Hq, Dv]``.
 
@@ -186,7 +213,7 @@ def paged_attention_decode(
         out = torch.empty(shape, dtype=out_dtype, device=query.device)
     args = make_args(
         query, key_cache, value_cache, block_table, context_lens, out, scale,
-        causal=causal, num_workers=num_workers,
+        causal=causal, num_workers=num_workers, k_scale=k_scale, v_scale=v_scale,
     )
     launch(args, query.device)
     return out

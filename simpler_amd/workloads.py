@@ -41,6 +41,7 @@ class DecodeConfig:
     max_blocks: int | None = None  # block_table width (defaults to ceil(ctx_max/BS))
     out_dtype: torch.dtype = torch.bfloat16
     description: str = ""
+    kv_format: str = "bf16"  # "fp8": E4M3FN caches with a power-of-two scale per (block, kv head)
 
     @property
     def group(self) -> int:
@@ -62,6 +63,10 @@ CONFIGS: dict[str, DecodeConfig] = {
         DecodeConfig("cfg5_verify", 4, 16, 32, 8, 128, 128, 128, 2048 + 8, 16384 + 8, q_len=8, causal=True,
                      description="speculative verify: B=16, q_len=8 causal, Hq=32, Hkv=8, D=128, BS=128, "
                                  "prefix~U[2048,16384]"),
+        # cfg2's draws (same seed index), K/V quantised to fp8 E4M3FN per (block, kv head)
+        DecodeConfig("cfg2_fp8", 1, 32, 32, 8, 128, 128, 128, 1024, 8192, kv_format="fp8",
+                     description="Qwen3-8B GQA decode, fp8 E4M3FN KV with per-(block, kv head) scales: B=32, Hq=32, "
+                                 "Hkv=8, D=128, BS=128, L~U[1024,8192]"),
     ]
 }
 
@@ -77,12 +82,20 @@ class DecodeCase:
     context_lens: torch.Tensor  # int32 [B]
     scale: float
     extra: dict = field(default_factory=dict)
+    k_scale: torch.Tensor | None = None  # fp8 caches: fp32 [num_blocks, kv_heads]
+    v_scale: torch.Tensor | None = None
 
     def to(self, device) -> "DecodeCase":
         k = self.key_cache.to(device)
         v = k[..., : self.config.head_dim_v] if self.config.mla else self.value_cache.to(device)
+        mv = lambda t: None if t is None else t.to(device)  # noqa: E731
         return DecodeCase(self.config, self.seed, self.query.to(device), k, v, self.block_table.to(device),
-                          self.context_lens.to(device), self.scale, dict(self.extra))
+                          self.context_lens.to(device), self.scale, dict(self.extra), mv(self.k_scale),
+                          mv(self.v_scale))
+
+    @property
+    def fp8(self) -> bool:
+        return self.k_scale is not None
 
     def out_shape(self) -> tuple[int, ...]:
         return (*self.query.shape[:-1], self.config.head_dim_v)
@@ -90,6 +103,30 @@ class DecodeCase:
 
 def _randn_bf16(shape, gen: torch.Generator) -> torch.Tensor:
     return torch.randn(shape, generator=gen, dtype=torch.float32).to(torch.bfloat16)
+
+
+FP8_MAX = 448.0  # largest finite E4M3FN value
+
+
+def quantize_kv_fp8(cache: torch.Tensor, pow2: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """``[nblk, BS, Hkv, D]`` -> (E4M3FN cache, fp32 scale ``[nblk, Hkv]``).
+
+    One scale per (block, kv head): the block's largest magnitude maps to at
+    most 448 (rounded up to a power of two with ``pow2``, so that the
+    dequantised values ``fp8 * scale`` are exactly bf16 values). An all-zero
+    block gets scale 0."""
+    x = cache.float()
+    amax = x.abs().amax(dim=(1, 3))
+    scale = amax / FP8_MAX
+    if pow2:
+        scale = torch.where(amax > 0, torch.exp2(torch.ceil(torch.log2(scale.clamp_min(1e-30)))), scale)
+    q = torch.where(scale[:, None, :, None] > 0, x / scale[:, None, :, None].clamp_min(1e-30), torch.zeros_like(x))
+    return q.to(torch.float8_e4m3fn), scale.contiguous()
+
+
+def dequantize_kv_fp8(cache8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32 values the fp8 cache stands for: ``float(byte) * scale[blk, h]``."""
+    return cache8.float() * scale[:, None, :, None].float()
 
 
 def make_case(cfg: DecodeConfig | str, seed: int | None = None, *, ctx_override: list[int] | None = None,
@@ -135,7 +172,11 @@ def make_case(cfg: DecodeConfig | str, seed: int | None = None, *, ctx_override:
         value = key[..., : cfg.head_dim_v]
     else:
         value = _randn_bf16((pool, bs, cfg.kv_heads, cfg.head_dim_v), gen)
-    return DecodeCase(cfg, seed, query, key, value, table, lens, 1.0 / math.sqrt(cfg.head_dim_k))
+    case = DecodeCase(cfg, seed, query, key, value, table, lens, 1.0 / math.sqrt(cfg.head_dim_k))
+    if cfg.kv_format == "fp8":
+        case.key_cache, case.k_scale = quantize_kv_fp8(key)
+        case.value_cache, case.v_scale = quantize_kv_fp8(value)
+    return case
 
 
 def make_custom_case(*, batch: int, num_heads: int, kv_heads: int, head_dim: int, block_size: int,
@@ -185,7 +226,9 @@ def algorithmic_bytes(case: DecodeCase, out_bytes: int = 2) -> int:
     lens = [int(x) for x in case.context_lens.tolist()]
     tok = sum(lens)
     kv_cols = c.head_dim_k if c.mla else c.head_dim_k + c.head_dim_v
-    kv = tok * c.kv_heads * kv_cols * 2
+    kv = tok * c.kv_heads * kv_cols * (1 if case.fp8 else 2)
+    if case.fp8:  # one K and one V scale per (visited block, kv head)
+        kv += 8 * c.kv_heads * sum((n + c.block_size - 1) // c.block_size for n in lens)
     q = c.batch * c.q_len * c.num_heads * c.head_dim_k * 2
     o = c.batch * c.q_len * c.num_heads * c.head_dim_v * out_bytes
     tables = 4 * sum((n + c.block_size - 1) // c.block_size for n in lens) + 4 * c.batch
@@ -196,7 +239,7 @@ def kv_bytes(case: DecodeCase) -> int:
     c = case.config
     tok = sum(int(x) for x in case.context_lens.tolist())
     kv_cols = c.head_dim_k if c.mla else c.head_dim_k + c.head_dim_v
-    return tok * c.kv_heads * kv_cols * 2
+    return tok * c.kv_heads * kv_cols * (1 if case.fp8 else 2)
 
 
 def algorithmic_flops(case: DecodeCase) -> int:
