@@ -74,6 +74,7 @@ constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
 constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
 constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit
+constexpr int kWorkersPerCuFp8 = 4;    // fp8 caches: one worker per SIMD (see wave_slots)
 constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
 
 struct KernelParams {
@@ -1291,18 +1292,21 @@ KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
     return {nullptr, nullptr, nullptr, false};
 }
 
-// Default worker count: compute units x kWorkersPerCu workgroups, capped by
-// the workgroups per CU the kernel's register footprint allows. Two streaming waves per CU measured fastest on MI355X for every
-// benchmark shape (512 workers: 112.8 us on the Qwen3-8B bs=32 shape, against
-// 119.2 us with four per CU and 137 us with 1.5 per CU): more waves per CU
-// make the K streams of different waves evict each other's L1 lines.
+// Default worker count: compute units x the requested workgroups per CU,
+// capped by what the kernel's register footprint allows. For bf16 caches two
+// streaming waves per CU measured fastest on MI355X for every benchmark shape
+// (512 workers: 112.8 us on the Qwen3-8B bs=32 shape, against 119.2 us with
+// four per CU and 137 us with 1.5 per CU): more waves per CU make the K
+// streams of different waves evict each other's L1 lines. fp8 caches ask for
+// four.
 // Without a device (host-only builds and tests) an MI355X is assumed:
 // 256 CUs.
-int wave_slots(KernelFn fn, int threads) {
+int wave_slots(KernelFn fn, int threads, int want_per_cu) {
     struct Entry {
         KernelFn fn;
         int device;
         int threads;
+        int want;
         int slots;
     };
     static std::mutex mu;
@@ -1311,11 +1315,11 @@ int wave_slots(KernelFn fn, int threads) {
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     std::lock_guard<std::mutex> lk(mu);
     for (const Entry &e : cache)
-        if (e.fn == fn && e.device == dev && e.threads == threads) return e.slots;
+        if (e.fn == fn && e.device == dev && e.threads == threads && e.want == want_per_cu) return e.slots;
     // kWorkersPerCu workgroups per CU, or as many as fit (a 4-wave workgroup
     // fills a CU at one wave per SIMD). Two 2-wave workers per CU measured
     // 195.5 us on the speculative-verify shape against 213.9 us with one.
-    int per_cu = kWorkersPerCu;
+    int per_cu = want_per_cu;
     int cus = 256;
     // Without a device: the kernels use the whole register file of a SIMD
     // (one wave per SIMD, four SIMDs per CU), the MLA kernel most of the LDS.
@@ -1332,7 +1336,7 @@ int wave_slots(KernelFn fn, int threads) {
     }
     (void)hipGetLastError();
     const int slots = cus * per_cu;
-    cache.push_back({fn, dev, threads, slots});
+    cache.push_back({fn, dev, threads, want_per_cu, slots});
     return slots;
 }
 
@@ -1352,7 +1356,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
         if (a->num_workers > 0) {
             p.workers = a->num_workers;
         } else {
-            const int wgs = wave_slots(p.main, p.threads);
+            const int wgs = wave_slots(p.main, p.threads, kWorkersPerCu);
             p.workers = wgs / p.groups > 0 ? wgs / p.groups : 1;
         }
         p.grid = (int64_t)p.workers * p.groups;
@@ -1364,7 +1368,12 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
         p.main = p.tiles_per_worker > 1 ? k.main_multi : k.main;
         p.groups = 1;
         p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
-        p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads);
+        // fp8 halves the bytes per block but not the math, so a wave spends
+        // longer per byte: one worker per SIMD (cfg2: 58.6 us against 87.7 us
+        // with two per CU) keeps enough loads in flight; bf16 prefers two
+        // (their K half-line reads evict each other in L1 at four).
+        const int per_cu = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 ? kWorkersPerCuFp8 : kWorkersPerCu;
+        p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu);
         p.grid = p.workers;
     }
     const int dv = a->head_dim_v;
