@@ -267,7 +267,8 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int nblk, const int blk_begin, const int blk_end,
-                                            float *const part_o, float *const part_ml) {
+                                            float *const part_o, float *const part_ml,
+                                            const bool sync_siblings) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
     constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
     constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
@@ -383,6 +384,9 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const bool first = (blk == blk_begin);
         const bool blk_bad = bad;
         if (blk_bad && lane == 0) atomicOr(P.error_flag, 1u);
+        // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
+        // block's loads together lets the caches serve the second request.
+        if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
         load_v(phys);
         float sc = P.scale, vs = 1.f;
         if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform)
@@ -605,8 +609,12 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
         float *po = P.part_o + piece * 16 * DV;
         float *pml = P.part_ml + piece * 32;
+        // every wave of the group has a row tile: all run the same blocks, so
+        // a per-block barrier among them is matched
+        const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
         if (rt < P.row_tiles)
-            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8>(P, b, kvh, rt, nb, blk, blk + seg, po, pml);
+            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8>(P, b, kvh, rt, nb, blk, blk + seg, po, pml,
+                                                           MAXW > 1 && full_group);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -627,6 +635,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
 // ---------------------------------------------------------------------------
 
 constexpr int kMergeThreads = 256;
+constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weights
 
 template <int DV, typename OutT>
 __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelParams P) {
@@ -660,6 +669,44 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
         const int slot = (w * chunk >= t0) ? 0 : 1;
         return ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
     };
+    const int np = w_last - w_first + 1;
+    if (np <= kMergeLdsPieces) {
+        // Per-(row, piece) weights e^{m_w - M} / L once per workgroup, then the
+        // partial rows stream through with no dependent loads in the way.
+        __shared__ float wgt[16][kMergeLdsPieces];  // m of each (row, piece), then its weight
+        __shared__ float lsum[16][kMergeLdsPieces];
+        for (int e = tid; e < 16 * np; e += kMergeThreads) {  // all (m, l) loads in flight at once
+            const int row = e / np, k = e - row * np;
+            const int64_t pc = piece_of(w_first + k);
+            wgt[row][k] = P.part_ml[pc * 32 + row];
+            lsum[row][k] = P.part_ml[pc * 32 + 16 + row];
+        }
+        __syncthreads();
+        if (tid < 16) {
+            float M = -INFINITY;
+            for (int k = 0; k < np; ++k) M = fmaxf(M, wgt[tid][k]);
+            float L = 0.f;
+            for (int k = 0; k < np; ++k) {
+                const float c = __expf(wgt[tid][k] - M);
+                wgt[tid][k] = c;
+                L += c * lsum[tid][k];
+            }
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            for (int k = 0; k < np; ++k) wgt[tid][k] *= inv;
+        }
+        __syncthreads();
+        for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+            f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+            for (int k = 0; k < np; ++k) {
+                const int64_t piece = piece_of(w_first + k);
+                o += wgt[row][k] * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
+            }
+            OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, o);
+        }
+        return;
+    }
     for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
         const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
         float M = -INFINITY;
