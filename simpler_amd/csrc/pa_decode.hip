@@ -10,8 +10,7 @@
 //   UP  aiv/aiv_online_update.cpp:125-224   -> register-resident online merge
 // plus the cross-split log-sum-exp merge of the reference's SplitKV path
 // (tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention_highperf/
-//  kernels/kernel/pa_kernel.cce:1634-1773), done in-kernel by the last split
-// of each (batch, kv head, row tile) to finish.
+//  kernels/kernel/pa_kernel.cce:1634-1773), done by a second kernel.
 //
 // Numerics follow the reference golden (simpler_setup/goldens/paged_attention.py
 // :145-187) block for block: the softmax max is taken per KV block, p is rounded
@@ -24,10 +23,12 @@
 // than e^-kFrameGap relative and is skipped, which bounds A by e^kFrameGap * |O|.
 //
 // Work decomposition (stream-K): the work is the flattened list of
-// (tile, KV block) pairs, tile = (batch, kv head, row tile), in that order.
+// (tile, KV block) pairs, tile = (batch, kv head, row tile), in that order
+// (optionally as one list per tile of a batch; see lane_tiles).
 // A row is one (query token, head in the GQA group) pair; 16 rows per tile
-// (MFMA N). The main kernel launches exactly one 64-lane wavefront per wave
-// slot of the GPU (CUs x waves per CU at this kernel's occupancy) and gives
+// (MFMA N). The main kernel launches one worker (a wavefront, or sibling
+// wavefronts for several row tiles) per slot of the GPU (CUs x workers per
+// CU at this kernel's occupancy) and gives
 // each an equal contiguous slice of that list, computed on the device from
 // context_lens, so ragged lengths cost no imbalance and no tail. A tile that
 // lies inside one slice is finished (normalised and stored) by that wave; a
@@ -36,7 +37,8 @@
 // the partial writes before the merge; no device-scope fences are used.
 //
 // Lane (qd = lane/16, pc = lane%16):
-//   QK   A operand = K token pc of the tile, dims 32kk+8qd..+7 (one 16-B load)
+//   QK   A operand = K token pc of the tile, dims 32kk+8qd..+7 (one 16-B load,
+//                    or one 16-B LDS read when K is staged through LDS)
 //        B operand = Q row pc, same dims
 //        C         = S[row pc][tokens 4qd..4qd+3]   (S^T tile)
 //   PV   A operand = P[row pc][tokens 4qd..4qd+3]  == the QK C layout (no shuffle)
@@ -73,8 +75,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
 constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
-constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit
-constexpr int kWorkersPerCuFp8 = 4;    // fp8 caches: one worker per SIMD (see wave_slots)
+constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit (half-line K reads)
+constexpr int kWorkersPerSimdCu = 4;   // one worker per SIMD: full-row K reads and fp8 caches (see make_plan)
 constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
 
 struct KernelParams {
@@ -97,6 +99,7 @@ struct KernelParams {
     int32_t row_groups;        // ceil(row_tiles / tiles_per_worker): work-list tiles per kv head
     int32_t block_size, max_blocks, num_pool_blocks;
     int32_t workers;
+    int32_t lanes;  // independent work lists; list u holds tiles [u, u+1) * (tiles per batch / lanes) of each batch
     float scale;
     int32_t causal;
 };
@@ -110,6 +113,24 @@ __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret
 // two halves into one line request (non-temporal K measured 5-10% slower).
 __device__ __forceinline__ u32x4_t stream_ld16(const char *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
+
+__device__ __forceinline__ u32x4_t lds_ld16(const char *base, uint32_t off) {
+    return *reinterpret_cast<const LDS_AS u32x4_t *>((const LDS_AS char *)base + off);
+}
+
+__device__ __forceinline__ void lds_st16(char *base, uint32_t off, u32x4_t v) {
+    *reinterpret_cast<LDS_AS u32x4_t *>((LDS_AS char *)base + off) = v;
+}
+
+// Orders one wave's LDS writes before its later reads of other lanes' data
+// (and those reads before later writes). The LDS executes a wave's
+// instructions in order, so this only has to stop the compiler from moving
+// LDS accesses across it; it emits no instruction.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
@@ -174,8 +195,18 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
     return (ctx + P.block_size - 1) / P.block_size;
 }
 
-// Wave-level scan over the batch. Work of batch b = blocks_of(b) * tiles per
-// batch. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
+// Work lists: the (tile, KV block) pairs of all batches form P.lanes lists of
+// equal length. List u holds, per batch, the tiles u*lt .. u*lt+lt-1 (lt =
+// tiles per batch / lanes), batch-major, then tile, then block; its
+// P.workers / lanes workers (ids u, u + lanes, u + 2*lanes, ...) take equal
+// contiguous slices of it. With lanes = tiles per batch, the workers of every
+// kv head get the same block ranges, so neighbouring workers read the
+// different heads of the same token rows at about the same time (the caches
+// interleave heads within a row).
+__device__ __forceinline__ int lane_tiles(const KernelParams &P) { return P.kv_heads * P.row_groups / P.lanes; }
+
+// Wave-level scan over the batch for one list. Work of batch b = blocks_of(b)
+// * lane_tiles. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
 // before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
 // *prefix_of_pos = the batch whose work range contains pos and the work before
 // it. `pos` may be given as a fraction of the total (pos_num / pos_den of it,
@@ -184,7 +215,7 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
 __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
                          int *prefix_of_pos) {
     const int lane = threadIdx.x & 63;
-    const int tpb = P.kv_heads * P.row_groups;
+    const int tpb = lane_tiles(P);
     int carry = 0;
     for (int base = 0; base < P.batch; base += 64) {
         const int b = base + lane;
@@ -210,20 +241,22 @@ __device__ int scan_work(const KernelParams &P, int want_b, int *prefix_of_want,
     return carry;
 }
 
-// Worker w's slice start in one pass over the batch (the common case of at
-// most 64 sequences): total work, then the batch containing w*chunk.
-__device__ int locate_slice(const KernelParams &P, int w, int *start, int *end, int *b_of_start,
+// Slice c of a list (the list's c-th worker), in one pass over the batch when
+// there are at most 64 sequences: total work, then the batch containing
+// c*chunk.
+__device__ int locate_slice(const KernelParams &P, int c, int *start, int *end, int *b_of_start,
                             int *prefix_of_start) {
     const int lane = threadIdx.x & 63;
+    const int per_list = max(P.workers / P.lanes, 1);
     if (P.batch > 64) {
         const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
-        const int chunk = (total + P.workers - 1) / max(P.workers, 1);
-        *start = w * chunk;
+        const int chunk = (total + per_list - 1) / per_list;
+        *start = c * chunk;
         *end = min(*start + chunk, total);
         if (*start < *end) scan_work(P, -1, nullptr, *start, b_of_start, prefix_of_start);
         return total;
     }
-    const int tpb = P.kv_heads * P.row_groups;
+    const int tpb = lane_tiles(P);
     const int cnt = lane < P.batch ? blocks_of(P, lane) * tpb : 0;
     int incl = cnt;
 #pragma unroll
@@ -232,8 +265,8 @@ __device__ int locate_slice(const KernelParams &P, int w, int *start, int *end, 
         if (lane >= off) incl += y;
     }
     const int total = __shfl(incl, 63, 64);
-    const int chunk = (total + P.workers - 1) / max(P.workers, 1);
-    *start = w * chunk;
+    const int chunk = (total + per_list - 1) / per_list;
+    *start = c * chunk;
     *end = min(*start + chunk, total);
     const int excl = incl - cnt;
     const unsigned long long hit = __ballot(cnt > 0 && *start >= excl && *start < excl + cnt);
@@ -264,16 +297,26 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // token, so the QK contraction visits dims in a permuted order: k-step kk of
 // lane group qd holds dims 16·qd + 64·(kk/2) + 8·(kk%2) .. +7, and Q is loaded
 // in the same order.
-template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8>
+//
+// KLDS (bf16, DK = 128): K is read like V, as whole 256-byte token rows (lane
+// (qd, pc) reads 16-byte chunk pc of token 4qd+e of each 16-token tile, so
+// one instruction covers four full rows), with non-temporal loads, and is
+// rearranged into the QK operand layout through this wave's BS x 256-byte LDS
+// buffer `klds`. Chunk c of token T sits at slot c ^ (T & 15) of the token's
+// LDS row, so the row writes and the operand reads each touch 16 distinct
+// 16-byte slots per 16 lanes. The K registers are free once a block is in
+// LDS, so the next block's K is issued before this block's QK.
+template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
-                                            const bool sync_siblings) {
+                                            const bool sync_siblings, char *const klds = nullptr) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
     constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
     constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
     constexpr int ESZ = KV8 ? 1 : 2;       // cache element bytes
     static_assert(!KV8 || (DK % 64 == 0 && DV % 128 == 0), "fp8 caches: head dims multiple of 64 (K), 128 (V)");
+    static_assert(!KLDS || (!KV8 && DK == 128), "K through LDS: bf16 caches, DK = 128");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -322,7 +365,14 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     // Addresses: a wave-uniform byte base plus one 32-bit per-lane offset that
     // is the same for every block.
     const int64_t k_tok_b = P.k_token_stride * ESZ, v_tok_b = P.v_token_stride * ESZ;
-    const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
+    const uint32_t k_lane = KLDS ? (uint32_t)(4 * qd * k_tok_b + 16 * pc) : (uint32_t)(pc * k_tok_b + 16 * qd);
+    uint32_t kw_off[4], kr_off[KS];  // KLDS: LDS byte offsets of this lane's row writes / operand reads
+    if constexpr (KLDS) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw_off[e] = (4 * qd + e) * 256 + ((pc ^ (4 * qd + e)) << 4);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) kr_off[kk] = pc * 256 + (((4 * kk + qd) ^ pc) << 4);
+    }
     const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 8 * ESZ * pc);
     const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * ESZ;
     const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * ESZ;
@@ -338,6 +388,16 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     };
     auto load_k = [&](int phys) {
         const char *kb = k_head + (int64_t)phys * P.k_block_stride * ESZ;
+        if constexpr (KLDS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const char *kt = kb + (int64_t)(16 * t + e) * k_tok_b + k_lane;
+                    kreg[t][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(kt) : stream_ld16(kt);
+                }
+            return;
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const char *kt = kb + (int64_t)(16 * t) * k_tok_b;
@@ -395,6 +455,21 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             vs = P.v_scale[si];
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (KLDS) {
+            // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
+            wave_lds_sync();
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lds_st16(klds, t * 4096 + kw_off[e], kreg[t][e]);
+            wave_lds_sync();
+            __builtin_amdgcn_sched_barrier(0);
+            if (blk + 1 < blk_end) {
+                phys = phys_of(blk + 1, bad);
+                load_k(phys);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
 
         // ---- QK: S^T tiles ----
         f32x4_t s[NT];
@@ -407,6 +482,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 if constexpr (KV8) {
                     const u32x4_t raw = kreg[t][kk >> 1];
                     kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
+                } else if constexpr (KLDS) {
+                    kop = lds_ld16(klds, t * 4096 + kr_off[kk]);
                 } else {
                     kop = kreg[t][kk];
                 }
@@ -418,7 +495,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 
         // ---- prefetch K of the next block ----
         __builtin_amdgcn_sched_barrier(0);
-        if (blk + 1 < blk_end) {
+        if (!KLDS && blk + 1 < blk_end) {
             phys = phys_of(blk + 1, bad);
             load_k(phys);
         }
@@ -587,11 +664,15 @@ template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
+    // single-tile bf16 workers with 128-dim heads stage K through LDS
+    constexpr bool KLDS = MAXW == 1 && !KV8 && DK == 128;
+    __shared__ __attribute__((aligned(16))) char klds[KLDS ? BS * 256 : 16];
     const int w = blockIdx.x;
     const int wave = MAXW == 1 ? 0 : (int)(threadIdx.x >> 6);
-    const int tpb = P.kv_heads * P.row_groups;
+    const int tpb = lane_tiles(P);
+    const int list = w % P.lanes;
     int start = 0, end = 0, b = 0, prefix = 0;
-    locate_slice(P, w, &start, &end, &b, &prefix);
+    locate_slice(P, w / P.lanes, &start, &end, &b, &prefix);
     if (start >= end) return;
     int nb = blocks_of(P, b);
     if (nb == 0) return;  // not reached: the batch holding `start` has work
@@ -602,7 +683,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        const int kvh = j / P.row_groups, rg = j - kvh * P.row_groups;
+        const int jt = list * tpb + j;  // tile of the batch
+        const int kvh = jt / P.row_groups, rg = jt - kvh * P.row_groups;
         const int rt = rg * P.tiles_per_worker + wave;  // this wave's row tile
         // A worker touches at most two tiles partially: the first and the last
         // of its slice (slots 0 and 1); tiles in between are finished here.
@@ -613,8 +695,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         // a per-block barrier among them is matched
         const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
         if (rt < P.row_tiles)
-            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8>(P, b, kvh, rt, nb, blk, blk + seg, po, pml,
-                                                           MAXW > 1 && full_group);
+            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS>(P, b, kvh, rt, nb, blk, blk + seg, po, pml,
+                                                                 MAXW > 1 && full_group, klds);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -645,7 +727,8 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
     const int b = tile / tpb, jr = tile - b * tpb;
     const int kvh = jr / P.row_tiles, rt = jr - kvh * P.row_tiles;
     const int rg = rt / P.tiles_per_worker, wave = rt - rg * P.tiles_per_worker;
-    const int j = kvh * P.row_groups + rg;  // work-list tile
+    const int jt = kvh * P.row_groups + rg;  // tile of the batch in the work lists
+    const int list = jt / lane_tiles(P), j = jt - list * lane_tiles(P);
     const int rows_here = min(16, P.rows - rt * 16);
     int prefix = 0;
     const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
@@ -658,16 +741,18 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
         }
         return;
     }
-    const int chunk = (total + P.workers - 1) / P.workers;
+    const int per_list = max(P.workers / P.lanes, 1);
+    const int chunk = (total + per_list - 1) / per_list;
     const int t0 = prefix + j * nb;
-    const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;
+    const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;  // slices of the list
     if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
     // Log-sum-exp over the pieces: the row max and total l from the (m, l)
     // pairs first, then O = sum_w e^{m_w - M} O_w / L, whose piece loads do not
     // depend on each other and stay in flight together.
-    auto piece_of = [&](int w) -> int64_t {
-        const int slot = (w * chunk >= t0) ? 0 : 1;
-        return ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
+    auto piece_of = [&](int c) -> int64_t {
+        const int slot = (c * chunk >= t0) ? 0 : 1;
+        const int64_t w = (int64_t)c * P.lanes + list;  // the worker that ran slice c
+        return (w * P.tiles_per_worker + wave) * 2 + slot;
     };
     const int np = w_last - w_first + 1;
     if (np <= kMergeLdsPieces) {
@@ -761,10 +846,6 @@ struct MlaLayout {
     static constexpr int kRowChunks = kChunks + ((10 - kChunks % 16) % 16 + 16) % 16;  // = 10 (mod 16)
     static constexpr int kRowBytes = kRowChunks * 16;
 };
-
-__device__ __forceinline__ u32x4_t lds_ld16(const char *base, uint32_t off) {
-    return *reinterpret_cast<const LDS_AS u32x4_t *>((const LDS_AS char *)base + off);
-}
 
 __device__ __forceinline__ i16x4_t lds_ld_tr(const char *base, uint32_t off) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4_t *)((LDS_AS char *)base + off));
@@ -1205,6 +1286,7 @@ struct Plan {
     int row_groups;
     int threads;  // per worker workgroup
     int groups;   // workgroups per worker (MLA row groups), else 1
+    int lanes;    // work lists (KernelParams::lanes)
     int64_t grid;
     KernelFn main;
     size_t flag_bytes, part_ml_bytes, part_o_bytes;
@@ -1254,30 +1336,31 @@ struct KernelPair {
     KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     KernelFn merge;
     bool mla;
+    bool klds;  // `main` stages K through LDS (full-row K reads)
 };
 
 template <int BS, int D, typename OutT, bool KV8 = false>
 KernelPair pick_fn() {
     return {pa_decode_kernel<BS, D, D, OutT, 1, KV8>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, KV8>,
-            pa_merge_kernel<D, OutT>, false};
+            pa_merge_kernel<D, OutT>, false, !KV8 && D == 128};
 }
 
 // fp8 caches: head dim 128 (Llama/Qwen GQA), the four block sizes.
 template <typename OutT>
 KernelPair pick_fp8(int bs, int dk, int dv) {
-    if (dk != 128 || dv != 128) return {nullptr, nullptr, nullptr, false};
+    if (dk != 128 || dv != 128) return {nullptr, nullptr, nullptr, false, false};
     switch (bs) {
         case 16: return pick_fn<16, 128, OutT, true>();
         case 32: return pick_fn<32, 128, OutT, true>();
         case 64: return pick_fn<64, 128, OutT, true>();
         case 128: return pick_fn<128, 128, OutT, true>();
-        default: return {nullptr, nullptr, nullptr, false};
+        default: return {nullptr, nullptr, nullptr, false, false};
     }
 }
 
 template <int BS, typename OutT>
 KernelPair pick_d(int dk, int dv) {
-    if (dk != dv) return {nullptr, nullptr, nullptr, false};
+    if (dk != dv) return {nullptr, nullptr, nullptr, false, false};
     switch (dk) {
         case 16: return pick_fn<BS, 16, OutT>();
         case 32: return pick_fn<BS, 32, OutT>();
@@ -1285,8 +1368,8 @@ KernelPair pick_d(int dk, int dv) {
         case 128: return pick_fn<BS, 128, OutT>();
         case 256:
             if constexpr (BS <= 64) return pick_fn<BS, 256, OutT>();
-            return {nullptr, nullptr, nullptr, false};
-        default: return {nullptr, nullptr, nullptr, false};
+            return {nullptr, nullptr, nullptr, false, false};
+        default: return {nullptr, nullptr, nullptr, false, false};
     }
 }
 
@@ -1297,7 +1380,7 @@ KernelPair pick_bs(int bs, int dk, int dv) {
         case 32: return pick_d<32, OutT>(dk, dv);
         case 64: return pick_d<64, OutT>(dk, dv);
         case 128: return pick_d<128, OutT>(dk, dv);
-        default: return {nullptr, nullptr, nullptr, false};
+        default: return {nullptr, nullptr, nullptr, false, false};
     }
 }
 
@@ -1314,9 +1397,9 @@ bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
 template <typename OutT>
 KernelPair pick_mla(int bs) {
     switch (bs) {
-        case 32: return {pa_mla_kernel<32, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true};
-        case 64: return {pa_mla_kernel<64, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true};
-        default: return {nullptr, nullptr, nullptr, false};
+        case 32: return {pa_mla_kernel<32, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false};
+        case 64: return {pa_mla_kernel<64, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false};
+        default: return {nullptr, nullptr, nullptr, false, false};
     }
 }
 
@@ -1325,27 +1408,27 @@ KernelPair pick_kernel(const SimplerHipPaDecodeArgs *a) {
         if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_fp8<float>(a->block_size, a->head_dim_k, a->head_dim_v);
         if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
             return pick_fp8<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
-        return {nullptr, nullptr, nullptr, false};
+        return {nullptr, nullptr, nullptr, false, false};
     }
     if (is_mla_shape(a)) {
-        if (!v_is_k_prefix(a)) return {nullptr, nullptr, nullptr, false};
+        if (!v_is_k_prefix(a)) return {nullptr, nullptr, nullptr, false, false};
         if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_mla<float>(a->block_size);
         if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16) return pick_mla<__bf16>(a->block_size);
-        return {nullptr, nullptr, nullptr, false};
+        return {nullptr, nullptr, nullptr, false, false};
     }
     if (a->out_dtype == SIMPLER_HIP_DT_FLOAT32) return pick_bs<float>(a->block_size, a->head_dim_k, a->head_dim_v);
     if (a->out_dtype == SIMPLER_HIP_DT_BFLOAT16)
         return pick_bs<__bf16>(a->block_size, a->head_dim_k, a->head_dim_v);
-    return {nullptr, nullptr, nullptr, false};
+    return {nullptr, nullptr, nullptr, false, false};
 }
 
 // Default worker count: compute units x the requested workgroups per CU,
-// capped by what the kernel's register footprint allows. For bf16 caches two
-// streaming waves per CU measured fastest on MI355X for every benchmark shape
-// (512 workers: 112.8 us on the Qwen3-8B bs=32 shape, against 119.2 us with
-// four per CU and 137 us with 1.5 per CU): more waves per CU make the K
-// streams of different waves evict each other's L1 lines. fp8 caches ask for
-// four.
+// capped by what the kernel's register footprint allows. Kernels that read K
+// in half lines (plain loads that rely on the L1 to merge the two halves)
+// measured fastest at two waves per CU (512 workers: 112.8 us on the Qwen3-8B
+// bs=32 shape, against 119.2 us with four per CU, whose K streams evict each
+// other's L1 lines). Kernels that read K in whole rows and fp8 caches ask for
+// four (one per SIMD).
 // Without a device (host-only builds and tests) an MI355X is assumed:
 // 256 CUs.
 int wave_slots(KernelFn fn, int threads, int want_per_cu) {
@@ -1392,6 +1475,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
     p.row_tiles = (p.rows + 15) / 16;
+    p.lanes = 1;
     if (k.mla) {
         // A work slice runs as `groups` sibling workgroups of 64 rows (4 row
         // tiles) each; `workers` counts slices.
@@ -1415,12 +1499,28 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
         p.main = p.tiles_per_worker > 1 ? k.main_multi : k.main;
         p.groups = 1;
         p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
-        // fp8 halves the bytes per block but not the math, so a wave spends
-        // longer per byte: one worker per SIMD (cfg2: 58.6 us against 87.7 us
-        // with two per CU) keeps enough loads in flight; bf16 prefers two
-        // (their K half-line reads evict each other in L1 at four).
-        const int per_cu = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 ? kWorkersPerCuFp8 : kWorkersPerCu;
+        // One worker per SIMD when K is read in whole rows (through LDS) and for
+        // fp8 caches; two per CU when K is read in half lines, whose plain
+        // loads rely on the L1 merging the two halves and evict each other at
+        // four.
+        const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && p.main == k.main);
+        const int per_cu = one_per_simd ? kWorkersPerSimdCu : kWorkersPerCu;
         p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu);
+        // bf16 caches: one work list per tile of a batch when the worker count
+        // allows it, so the kv heads' workers walk the same blocks side by
+        // side (cfg3-like long contexts: 167.7 us against 173.4 us; the
+        // Qwen3-8B bs=32 shape and the verify shape: within 0.5%). fp8 caches,
+        // whose heads are single 128-byte lines of a 1 KB token row, measured
+        // 4% slower with it and keep one list.
+        const int tpb = a->num_kv_heads * p.row_groups;
+        if (tpb > 1 && a->kv_format != SIMPLER_HIP_KV_FP8_E4M3) {
+            if (a->num_workers > 0) {
+                if (p.workers % tpb == 0) p.lanes = tpb;
+            } else if (p.workers >= 4 * tpb) {
+                p.workers -= p.workers % tpb;
+                p.lanes = tpb;
+            }
+        }
         p.grid = p.workers;
     }
     const int dv = a->head_dim_v;
@@ -1516,6 +1616,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.max_blocks = a->max_blocks_per_seq;
     P.num_pool_blocks = a->num_blocks;
     P.workers = plan.workers;
+    P.lanes = plan.lanes;
     P.scale = a->scale;
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
     P.k_scale = a->k_scale;

@@ -198,8 +198,13 @@ def test_mla_dispatch_and_plan():
 
 
 def test_worker_plan():
-    # without a device the launcher assumes an MI355X: 256 CUs x 2 worker waves each
-    assert pa.plan(_args()) == 512
+    # without a device the launcher assumes an MI355X (256 CUs). 128-dim bf16 heads
+    # read K in whole rows through LDS: one worker per SIMD
+    assert pa.plan(_args()) == 1024
+    # other head dims read K in half lines: two workers per CU
+    assert pa.plan(_args(head_dim_k=64, head_dim_v=64, k_head_stride=64, v_head_stride=64)) == 512
+    # the default count is rounded down to whole work lists (one per kv head)
+    assert pa.plan(_args(num_heads=24, num_kv_heads=6)) == 1020
     assert pa.plan(_args(num_workers=7)) == 7
     ws = lambda **kw: _lib.lib().simpler_hip_pa_decode_workspace_size(ctypes.byref(_args(**kw)))
     # error word + two (m, l) and two O partial slots per worker, 256-byte aligned sections
@@ -209,8 +214,8 @@ def test_worker_plan():
     # and keeps two partial slots per wave
     assert pa.plan(_args(q_len=8, causal=1)) == 512
     assert ws(q_len=8, causal=1, num_workers=7) == 256 + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
-    # 25 row tiles: 4-wave workgroups, one per CU
-    assert pa.plan(_args(num_heads=80, num_kv_heads=1, q_len=5, causal=1)) == 256
+    # 25 row tiles: 4-wave workgroups, one per CU, in 7 work lists (row groups)
+    assert pa.plan(_args(num_heads=80, num_kv_heads=1, q_len=5, causal=1)) == 252
 
 
 def test_work_list_must_fit_32_bit_indices():
