@@ -270,3 +270,38 @@ def test_workspace_reused_across_plans(device):
     big = make_case("cfg3_long")
     got = run_gpu(big, device, num_workers=1024)
     assert_close(got, oracle_c(big, n_threads=16), what="workspace reuse")
+
+
+def test_workspace_shared_by_every_kernel(device):
+    # Calls of different kernels, shapes and worker counts (GQA, MLA, few or many
+    # tiles, cut at different places) share the one per-device workspace: no call
+    # may pick up another's partial results.
+    gqa = make_custom_case(batch=5, num_heads=32, kv_heads=8, head_dim=128, block_size=64,
+                           context_lens=[1, 700, 2100, 333, 64], seed=901)
+    ref = oracle_numpy(gqa)
+    mla = _mla_case(heads=128, lens=[1, 69, 700, 2100], seed=902)
+    mla_ref = oracle_numpy(mla)
+    few = make_custom_case(batch=2, num_heads=16, kv_heads=1, head_dim=64, block_size=16,
+                           context_lens=[300, 45], seed=903)
+    few_ref = oracle_numpy(few)
+    for workers in (64, 7, 0, 333):
+        print(f"[case] shared workspace workers={workers}", flush=True)
+        assert_close(run_gpu(mla, device, num_workers=workers), mla_ref, what=f"mla w{workers}")
+        assert_close(run_gpu(gqa, device, num_workers=workers), ref, what=f"gqa after mla w{workers}")
+        assert_close(run_gpu(few, device, num_workers=workers), few_ref, what=f"few tiles w{workers}")
+        assert_close(run_gpu(gqa, device, num_workers=workers), ref, what=f"gqa after few w{workers}")
+
+
+@pytest.mark.parametrize("workers", [0, 5000])
+def test_many_short_tiles(workers, device):
+    # 520 sequences x 32 kv heads = 16640 tiles of 0..3 blocks each, with 1024
+    # (per-kv-head work lists) or 5000 workers: many tiles cut into pieces, and
+    # empty contexts zero-filled by the merge kernel
+    print(f"[case] 16640 tiles workers={workers}", flush=True)
+    lens = torch.randint(0, 49, (520,), generator=torch.Generator().manual_seed(904)).tolist()
+    lens[3] = 0
+    case = make_custom_case(batch=520, num_heads=64, kv_heads=32, head_dim=32, block_size=16,
+                            context_lens=lens, seed=905)
+    got = run_gpu(case, device, num_workers=workers)
+    assert np.all(got[3] == 0)
+    assert_close(got, oracle_numpy(case), what=f"16640 tiles w{workers}")
