@@ -55,6 +55,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "simpler_hip/pa_decode.h"
@@ -74,7 +75,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
-constexpr int kBlockTableWindow = 64;  // block-table entries held one per lane
 constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit (half-line K reads)
 constexpr int kWorkersPerSimdCu = 4;   // one worker per SIMD: full-row K reads and fp8 caches (see make_plan)
 constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
@@ -344,10 +344,12 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     // blocks that end at or before it need no masking.
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
 
-    // Block-table entries of this segment, a window of 64 held one per lane.
-    const int32_t *bt_row = P.block_table + (int64_t)b * P.max_blocks;
-    int bt_base = blk_begin;
-    int bt_val = (blk_begin + lane < blk_end) ? bt_row[blk_begin + lane] : 0;
+    // Block-table entries are read through the scalar cache (constant address
+    // space): the load is counted by lgkmcnt, so waiting for it never waits for
+    // the K/V loads in flight. (A vector load issued after V(i) and needed for
+    // K(i+1) would make the K(i+1) loads wait for all of V(i).)
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
 
     f32x4_t acc[DVS][8];
 #pragma unroll
@@ -377,16 +379,11 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * ESZ;
     const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * ESZ;
 
-    auto phys_of = [&](int blk, bool &bad) -> int {
-        if (blk - bt_base >= kBlockTableWindow) {  // blocks are visited in order
-            bt_base += kBlockTableWindow;
-            bt_val = (bt_base + lane < blk_end) ? bt_row[bt_base + lane] : 0;
-        }
-        const int phys = __builtin_amdgcn_readlane(bt_val, blk - bt_base);
+    auto checked = [&](int phys, bool &bad) -> int {
         bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
         return bad ? 0 : phys;
     };
-    auto load_k = [&](int phys) {
+    auto load_k = [&](auto &kdst, int phys) {
         const char *kb = k_head + (int64_t)phys * P.k_block_stride * ESZ;
         if constexpr (KLDS) {
 #pragma unroll
@@ -394,7 +391,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const char *kt = kb + (int64_t)(16 * t + e) * k_tok_b + k_lane;
-                    kreg[t][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(kt) : stream_ld16(kt);
+                    kdst[t][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(kt) : stream_ld16(kt);
                 }
             return;
         }
@@ -404,13 +401,13 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 #pragma unroll
             for (int kk = 0; kk < (KV8 ? KS / 2 : KS); ++kk) {
                 if (KV8 || DK % 32 == 0 || 32 * kk + 8 * qd < DK)
-                    kreg[t][kk] = *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk);
+                    kdst[t][kk] = *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk);
                 else
-                    kreg[t][kk] = (u32x4_t){0u, 0u, 0u, 0u};
+                    kdst[t][kk] = (u32x4_t){0u, 0u, 0u, 0u};
             }
         }
     };
-    auto load_v = [&](int phys) {
+    auto load_v = [&](auto &vdst, auto &vrawdst, int phys) {
         const char *vb = v_head + (int64_t)phys * P.v_block_stride * ESZ;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -421,55 +418,33 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 for (int ds = 0; ds < DVS; ++ds) {
                     if constexpr (KV8) {
                         const u32x2_t *src = reinterpret_cast<const u32x2_t *>(vt + v_lane + 128 * ds);
-                        vraw[t][ds][e] = V_SHARED ? *src : __builtin_nontemporal_load(src);
+                        vrawdst[t][ds][e] = V_SHARED ? *src : __builtin_nontemporal_load(src);
                     } else if (DV % 128 == 0 || 128 * ds + 8 * pc < DV) {
-                        vreg[t][ds][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds)
+                        vdst[t][ds][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds)
                                                   : stream_ld16(vt + v_lane + 256 * ds);
                     } else {
-                        vreg[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                        vdst[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                     }
                 }
             }
     };
 
-    // Pipeline per block i: V(i) is issued first, then QK(i) consumes K(i)
-    // (issued during block i-1), then K(i+1) is issued, then softmax and PV(i).
-    // The scheduling barriers keep the compiler from sinking loads past the
-    // math, which would serialise the memory latency.
-    bool bad = false;
-    int phys = phys_of(blk_begin, bad);
-    load_k(phys);
-
-    for (int blk = blk_begin; blk < blk_end; ++blk) {
+    // One KV block: QK on kr (or the LDS copy), softmax, PV on vr / vrw.
+    // before_qk and after_qk place the single-buffer pipeline's loads of the
+    // next block's K.
+    auto compute_block = [&](const int blk, const int phys_b, const bool blk_bad, auto &kr, auto &vr, auto &vrw,
+                             auto &&before_qk, auto &&after_qk) {
         const bool first = (blk == blk_begin);
-        const bool blk_bad = bad;
         if (blk_bad && lane == 0) atomicOr(P.error_flag, 1u);
-        // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
-        // block's loads together lets the caches serve the second request.
-        if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
-        load_v(phys);
         float sc = P.scale, vs = 1.f;
-        if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform)
-            const int64_t si = (int64_t)phys * P.kv_heads + kvh;
-            sc = P.scale * P.k_scale[si];
-            vs = P.v_scale[si];
+        if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform, scalar loads)
+            typedef const __attribute__((address_space(4))) float *cfloat_p;
+            const int64_t si = (int64_t)phys_b * P.kv_heads + kvh;
+            sc = P.scale * ((cfloat_p)P.k_scale)[si];
+            vs = ((cfloat_p)P.v_scale)[si];
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (KLDS) {
-            // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
-            wave_lds_sync();
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) lds_st16(klds, t * 4096 + kw_off[e], kreg[t][e]);
-            wave_lds_sync();
-            __builtin_amdgcn_sched_barrier(0);
-            if (blk + 1 < blk_end) {
-                phys = phys_of(blk + 1, bad);
-                load_k(phys);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        before_qk();
 
         // ---- QK: S^T tiles ----
         f32x4_t s[NT];
@@ -480,12 +455,12 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             for (int kk = 0; kk < KS; ++kk) {
                 u32x4_t kop;
                 if constexpr (KV8) {
-                    const u32x4_t raw = kreg[t][kk >> 1];
+                    const u32x4_t raw = kr[t][kk >> 1];
                     kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
                 } else if constexpr (KLDS) {
                     kop = lds_ld16(klds, t * 4096 + kr_off[kk]);
                 } else {
-                    kop = kreg[t][kk];
+                    kop = kr[t][kk];
                 }
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kop),
                                                             __builtin_bit_cast(bf16x8_t, qv[kk]), c, 0, 0, 0);
@@ -493,12 +468,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             s[t] = c;
         }
 
-        // ---- prefetch K of the next block ----
         __builtin_amdgcn_sched_barrier(0);
-        if (!KLDS && blk + 1 < blk_end) {
-            phys = phys_of(blk + 1, bad);
-            load_k(phys);
-        }
+        after_qk();
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- softmax prepare: mask, scale, block max (golden :145-165) ----
@@ -570,9 +541,9 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (KV8)
-                        vt4[ds][e] = fp8x8_to_bf16x8(vraw[t][ds][e][0], vraw[t][ds][e][1]);
+                        vt4[ds][e] = fp8x8_to_bf16x8(vrw[t][ds][e][0], vrw[t][ds][e][1]);
                     else
-                        vt4[ds][e] = vreg[t][ds][e];
+                        vt4[ds][e] = vr[t][ds][e];
                 }
             if (vvalid < BS) {
 #pragma unroll
@@ -600,7 +571,56 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                         pa[t], __builtin_bit_cast(i16x4_t, (u32x2_t){d0, d1}), acc[ds][jj], 0, 0, 0);
                 }
         }
-    }
+    };
+
+    // Per block i: V(i) is issued first, then QK(i) consumes K(i) (issued
+    // during block i-1), then K(i+1) is issued (with K staged through LDS: as
+    // soon as K(i) is in LDS, before QK(i)), then softmax and PV(i). The
+    // scheduling barriers keep the compiler from sinking loads past the math,
+    // which would serialise the memory latency. The segment's last block is
+    // peeled off (no K(i+1)): with the prefetch under a run-time condition the
+    // compiler's wait counts would have to cover the path without it, so PV(i)
+    // would wait for K(i+1) as well.
+    bool bad = false;
+    int phys = checked(bt_row[blk_begin], bad);
+    load_k(kreg, phys);
+    auto step = [&](const int blk, auto has_next) {
+        constexpr bool NEXT = decltype(has_next)::value;
+        const bool blk_bad = bad;
+        const int phys_b = phys;
+        const int raw_next = NEXT ? bt_row[blk + 1] : 0;  // in flight during this block's loads
+        __builtin_amdgcn_sched_barrier(0);
+        // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
+        // block's loads together lets the caches serve the second request.
+        if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
+        load_v(vreg, vraw, phys_b);
+        auto stage_k_and_prefetch = [&] {
+            if constexpr (KLDS) {
+                // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
+                wave_lds_sync();
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) lds_st16(klds, t * 4096 + kw_off[e], kreg[t][e]);
+                wave_lds_sync();
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (NEXT) {
+                    phys = checked(raw_next, bad);
+                    load_k(kreg, phys);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        auto prefetch_k = [&] {
+            if constexpr (!KLDS && NEXT) {
+                phys = checked(raw_next, bad);
+                load_k(kreg, phys);
+            }
+        };
+        compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k);
+    };
+    for (int blk = blk_begin; blk + 1 < blk_end; ++blk) step(blk, std::true_type{});
+    step(blk_end - 1, std::false_type{});
 
     // ---- finish: O = e^{f-m} A, l = sum over the four lane groups ----
     float l_tot = l_part + __shfl_xor(l_part, 16, 64);
@@ -673,8 +693,14 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     const int list = w % P.lanes;
     int start = 0, end = 0, b = 0, prefix = 0;
     locate_slice(P, w / P.lanes, &start, &end, &b, &prefix);
+    // wave-uniform values (cross-lane results), kept in scalar registers so that
+    // block-table and scale reads derived from them are scalar loads
+    start = __builtin_amdgcn_readfirstlane(start);
+    end = __builtin_amdgcn_readfirstlane(end);
+    b = __builtin_amdgcn_readfirstlane(b);
+    prefix = __builtin_amdgcn_readfirstlane(prefix);
     if (start >= end) return;
-    int nb = blocks_of(P, b);
+    int nb = __builtin_amdgcn_readfirstlane(blocks_of(P, b));
     if (nb == 0) return;  // not reached: the batch holding `start` has work
     const int rel = start - prefix;
     int j = rel / nb;
@@ -705,7 +731,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
             j = 0;
             do {
                 ++b;
-                nb = blocks_of(P, b);
+                nb = __builtin_amdgcn_readfirstlane(blocks_of(P, b));
             } while (nb == 0 && b + 1 < P.batch);
         }
     }
