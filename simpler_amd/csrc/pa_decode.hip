@@ -879,6 +879,30 @@ __device__ __forceinline__ i16x4_t lds_ld_tr(const char *base, uint32_t off) {
 
 constexpr int kMlaRowsPerGroup = 64;  // four waves x 16 rows
 
+// LDS exchange area of the MLA workgroup: P^T operands of the four waves'
+// rows ([wave][k-step][lane] x 16 B), then 2 x 64 per-row floats.
+template <int BS>
+struct MlaExchange {
+    static constexpr int kPBytes = 4 * (BS / 32) * 64 * 16;
+    static constexpr int kBytes = kPBytes + 2 * 64 * 4;
+};
+
+__device__ __forceinline__ void lds_stf(char *base, uint32_t off, float v) {
+    *reinterpret_cast<LDS_AS float *>((LDS_AS char *)base + off) = v;
+}
+
+__device__ __forceinline__ float lds_ldf(const char *base, uint32_t off) {
+    return *reinterpret_cast<const LDS_AS float *>((const LDS_AS char *)base + off);
+}
+
+// Workgroup barrier that orders LDS accesses only: the block fill and L2
+// prefetch loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Work slice and row group of workgroup w. Row groups of a slice are
 // w, w+8, w+16, ...: the same XCD under round-robin workgroup dispatch.
 __device__ __forceinline__ void mla_worker(int w, int slices, int groups, int *slice, int *group) {
@@ -940,7 +964,8 @@ template <int BS, int DK, int DV, typename OutT>
 __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
                                                 const int groups, const int b, const int kvh, const int nblk,
                                                 const int blk_begin, const int blk_end, const int slot,
-                                                char *const smem0, char *const smem1, char *const sink) {
+                                                char *const smem0, char *const smem1, char *const sink,
+                                                char *const pexch) {
     using L = MlaLayout<DK>;
     constexpr int RB = L::kRowBytes;
     constexpr int RC = L::kRowChunks;
@@ -1045,9 +1070,16 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 
     // O^T accumulators and the row-sum tile (ones x P^T: every lane holds its
     // row's sum), both in the frame of the latest used block max f.
-    f32x4_t acc[NC];
+    // PV's output dims are split across the four waves: wave w accumulates
+    // O^T column tiles NCW*w .. NCW*w + NCW-1 (dims 16 c ..) for the four row
+    // tiles of the workgroup (acc[cl][r]), so each wave reads a quarter of V^T
+    // from LDS; the P^T operands of all four row tiles come through pexch.
+    constexpr int NCW = NC / 4;
+    f32x4_t acc[NCW][4];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NCW; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[c][r] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     float m_run = kNegClamp, f_run = kNegClamp;
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
@@ -1091,13 +1123,12 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 
         // ---- PV operand reads for the first two stages go out before the
         // softmax math (they do not depend on it) ----
-        constexpr int NSC = NC / 2;  // PV stages of two O^T column tiles
+        constexpr int NSC = NCW / 2;  // PV stages of two of this wave's O^T column tiles
         i16x4_t vf[3][2][PS][2];
         auto load_v = [&](int sc, i16x4_t (&dst)[2][PS][2]) {
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                const int c = 2 * sc + cc;
-                const uint32_t co = (cc ? vofs_odd : vofs_even) + 64 * (c >> 1);
+                const uint32_t co = (cc ? vofs_odd : vofs_even) + 64 * (NSC * wave + sc);
 #pragma unroll
                 for (int u = 0; u < PS; ++u) {
                     dst[cc][u][0] = lds_ld_tr(kb, co + u * 32 * RB);
@@ -1163,18 +1194,39 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 #pragma unroll
         for (int u = 0; u < PS; ++u)
             lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8_t, pk[u]), lacc, 0, 0, 0);
-        acc[0] *= cf;
-        acc[1] *= cf;
+
+        // ---- hand this wave's P^T and per-row factor to the other waves ----
+#pragma unroll
+        for (int u = 0; u < PS; ++u) lds_st16(pexch, ((wave * PS + u) * 64 + lane) * 16, pk[u]);
+        if (q == 0) lds_stf(pexch, MlaExchange<BS>::kPBytes + (wave * 16 + pc) * 4, cf);
+        lds_barrier();
+        u32x4_t pb[4][PS];  // P^T of row tile r (wave r's rows), k-step u
+        float cfr[4];       // e^{f - m_blk} of row pc of row tile r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int u = 0; u < PS; ++u) pb[r][u] = lds_ld16(pexch, ((r * PS + u) * 64 + lane) * 16);
+            cfr[r] = lds_ldf(pexch, MlaExchange<BS>::kPBytes + (r * 16 + pc) * 4);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[0][r] *= cfr[r];
+            acc[1][r] *= cfr[r];
+        }
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- A' = e^{f - m_blk} A + P V: stage sc = column tiles 2sc, 2sc+1;
-        // the next stage's tiles are rescaled between this stage's MFMAs ----
+        // ---- A' = e^{f - m_blk} A + P V: stage sc = this wave's column tiles
+        // 2sc, 2sc+1 for the four row tiles; the next stage's tiles are rescaled
+        // between this stage's MFMAs ----
 #pragma unroll
         for (int sc = 0; sc < NSC; ++sc) {
             if (sc + 2 < NSC) load_v(sc + 2, vf[(sc + 2) % 3]);
             if (sc + 1 < NSC) {
-                acc[2 * sc + 2] *= cf;
-                acc[2 * sc + 3] *= cf;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[2 * sc + 2][r] *= cfr[r];
+                    acc[2 * sc + 3][r] *= cfr[r];
+                }
             }
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
@@ -1183,14 +1235,16 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
                     const bf16x8_t va = __builtin_bit_cast(
                         bf16x8_t,
                         __builtin_shufflevector(vf[sc % 3][cc][u][0], vf[sc % 3][cc][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
-                    acc[2 * sc + cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        va, __builtin_bit_cast(bf16x8_t, pk[u]), acc[2 * sc + cc], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[2 * sc + cc][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            va, __builtin_bit_cast(bf16x8_t, pb[r][u]), acc[2 * sc + cc][r], 0, 0, 0);
                 }
             if (sc + 2 < NSC) __builtin_amdgcn_sched_group_barrier(kDsRead, 4 * PS, 0);
 #pragma unroll
-            for (int g2 = 0; g2 < 2 * PS; ++g2) {
+            for (int g2 = 0; g2 < 8 * PS; ++g2) {
                 __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-                if (sc + 1 < NSC) __builtin_amdgcn_sched_group_barrier(kValu, 8 / (2 * PS), 0);
+                if (sc + 1 < NSC) __builtin_amdgcn_sched_group_barrier(kValu, 32 / (8 * PS), 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1222,29 +1276,44 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
         if (blk + 2 < blk_end) prefetch(blk + 2);
         if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, 1u);
-        if (active) compute(even ? smem0 : smem1, blk, bad_cur);
+        compute(even ? smem0 : smem1, blk, bad_cur);
         bad_cur = bad_next;
     }
-    __syncthreads();  // the buffers are refilled by the next segment
-    if (!active) return;
+    __syncthreads();  // the buffers are refilled by the next segment; pexch is free
 
-    // ---- finish: O = e^{f-m} A, l = e^{f-m} L ----
+    // ---- finish: O = e^{f-m} A, l = e^{f-m} L. The row factors live with the
+    // row's wave; every wave holds a quarter of every row's dims ----
     const float osc = __expf(f_run - m_run);
     const float l_tot = lacc[0] * osc;
-    if (pc >= rows_here) return;
-    if (blk_begin == 0 && blk_end == nblk) {
-        const float inv = lacc[0] > 0.f ? 1.f / lacc[0] : 0.f;  // the frame factor cancels
-        const int64_t off = out_row_offset(P, b, kvh, r0 + pc, DV) + 4 * q;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) OutStore<OutT>::store4(P.out, off + 16 * c, acc[c] * inv);
-        return;
-    }
-    const int rt = rgrp * 4 + wave;  // row tile within the slice's tile
-    const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rt) * 2 + slot;
-    float *dst = P.part_o + (piece * 16 + pc) * DV + 4 * q;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4_t *>(dst + 16 * c) = acc[c] * osc;
     if (q == 0) {
+        lds_stf(pexch, (wave * 16 + pc) * 4, osc);
+        lds_stf(pexch, 256 + (wave * 16 + pc) * 4, lacc[0]);
+    }
+    lds_barrier();
+    const bool whole = blk_begin == 0 && blk_end == nblk;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rows_r = min(16, P.rows - (rgrp * kMlaRowsPerGroup + 16 * r));
+        if (pc >= rows_r) continue;
+        const int row = rgrp * kMlaRowsPerGroup + 16 * r + pc;
+        if (whole) {
+            const float lr = lds_ldf(pexch, 256 + (r * 16 + pc) * 4);
+            const float inv = lr > 0.f ? 1.f / lr : 0.f;  // the frame factor cancels
+            const int64_t off = out_row_offset(P, b, kvh, row, DV) + 4 * q;
+#pragma unroll
+            for (int cl = 0; cl < NCW; ++cl)
+                OutStore<OutT>::store4(P.out, off + 16 * (NCW * wave + cl), acc[cl][r] * inv);
+        } else {
+            const float oscr = lds_ldf(pexch, (r * 16 + pc) * 4);
+            const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + r) * 2 + slot;
+            float *dst = P.part_o + (piece * 16 + pc) * DV + 4 * q;
+#pragma unroll
+            for (int cl = 0; cl < NCW; ++cl)
+                *reinterpret_cast<f32x4_t *>(dst + 16 * (NCW * wave + cl)) = acc[cl][r] * oscr;
+        }
+    }
+    if (!whole && active && pc < rows_here && q == 0) {
+        const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + wave) * 2 + slot;
         P.part_ml[piece * 32 + pc] = m_run;
         P.part_ml[piece * 32 + 16 + pc] = l_tot;
     }
@@ -1259,6 +1328,8 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
+    // P^T of every wave's rows and per-row factors, handed between the waves
+    __shared__ __attribute__((aligned(16))) char pexch[MlaExchange<BS>::kBytes];
     const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
     int slice = 0, rgrp = 0;
     mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
@@ -1281,7 +1352,7 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
         run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0, smem1,
-                                          sink);
+                                          sink, pexch);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
