@@ -744,6 +744,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
 
 constexpr int kMergeThreads = 256;
 constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weights
+constexpr int kMergePrefetch = 8;    // partial rows per thread read before the weights are known
 
 template <int DV, typename OutT>
 __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelParams P) {
@@ -783,9 +784,21 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
     const int np = w_last - w_first + 1;
     if (np <= kMergeLdsPieces) {
         // Per-(row, piece) weights e^{m_w - M} / L once per workgroup, then the
-        // partial rows stream through with no dependent loads in the way.
+        // partial rows stream through with no dependent loads in the way. The
+        // thread's first unit reads its first kMergePrefetch partial rows
+        // together with the (m, l) loads: they do not depend on the weights.
         __shared__ float wgt[16][kMergeLdsPieces];  // m of each (row, piece), then its weight
         __shared__ float lsum[16][kMergeLdsPieces];
+        const int units = rows_here * (DV / 4);
+        f32x4_t pre[kMergePrefetch];
+        {
+            const int row = tid / (DV / 4), c4 = tid - row * (DV / 4);
+#pragma unroll
+            for (int k = 0; k < kMergePrefetch; ++k)
+                pre[k] = (tid < units && k < np)
+                             ? *reinterpret_cast<const f32x4_t *>(P.part_o + (piece_of(w_first + k) * 16 + row) * DV + 4 * c4)
+                             : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
         for (int e = tid; e < 16 * np; e += kMergeThreads) {  // all (m, l) loads in flight at once
             const int row = e / np, k = e - row * np;
             const int64_t pc = piece_of(w_first + k);
@@ -806,11 +819,18 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
             for (int k = 0; k < np; ++k) wgt[tid][k] *= inv;
         }
         __syncthreads();
-        for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
+        for (int idx = tid; idx < units; idx += kMergeThreads) {
             const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
             f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+            int k = 0;
+            if (idx == tid) {  // the prefetched rows first
+#pragma unroll
+                for (int kp = 0; kp < kMergePrefetch; ++kp)
+                    if (kp < np) o += wgt[row][kp] * pre[kp];
+                k = kMergePrefetch;
+            }
 #pragma unroll 4
-            for (int k = 0; k < np; ++k) {
+            for (; k < np; ++k) {
                 const int64_t piece = piece_of(w_first + k);
                 o += wgt[row][k] * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
             }
