@@ -189,10 +189,13 @@ struct OutStore<__bf16> {
 // Work partition shared by both kernels
 // ---------------------------------------------------------------------------
 
+// Context length of sequence b, clamped to what its block-table row can hold.
+__device__ __forceinline__ int ctx_of(const KernelParams &P, int b) {
+    return min(max(P.context_lens[b], 0), P.max_blocks * P.block_size);
+}
+
 __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
-    int ctx = P.context_lens[b];
-    ctx = min(max(ctx, 0), P.max_blocks * P.block_size);
-    return (ctx + P.block_size - 1) / P.block_size;
+    return (ctx_of(P, b) + P.block_size - 1) / P.block_size;
 }
 
 // Work lists: the (tile, KV block) pairs of all batches form P.lanes lists of
@@ -308,7 +311,7 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // LDS, so the next block's K is issued before this block's QK.
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
-                                            const int nblk, const int blk_begin, const int blk_end,
+                                            const int ctx, const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
                                             const bool sync_siblings, char *const klds = nullptr) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
@@ -321,8 +324,6 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     const int qd = lane >> 4;
     const int pc = lane & 15;
     const int rows_here = min(16, P.rows - rt * 16);
-    int ctx = P.context_lens[b];
-    ctx = min(max(ctx, 0), P.max_blocks * BS);
 
     // ---- Q^T operand (row pc, dims 32kk+8qd..) and this row's visible length ----
     int rowlen = 0;
@@ -700,7 +701,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     b = __builtin_amdgcn_readfirstlane(b);
     prefix = __builtin_amdgcn_readfirstlane(prefix);
     if (start >= end) return;
-    int nb = __builtin_amdgcn_readfirstlane(blocks_of(P, b));
+    int ctx = __builtin_amdgcn_readfirstlane(ctx_of(P, b));  // the segment's sequence, read once
+    int nb = (ctx + BS - 1) / BS;
     if (nb == 0) return;  // not reached: the batch holding `start` has work
     const int rel = start - prefix;
     int j = rel / nb;
@@ -721,7 +723,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         // a per-block barrier among them is matched
         const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
         if (rt < P.row_tiles)
-            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS>(P, b, kvh, rt, nb, blk, blk + seg, po, pml,
+            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml,
                                                                  MAXW > 1 && full_group, klds);
         pos += seg;
         slot = 1;
@@ -731,7 +733,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
             j = 0;
             do {
                 ++b;
-                nb = __builtin_amdgcn_readfirstlane(blocks_of(P, b));
+                ctx = __builtin_amdgcn_readfirstlane(ctx_of(P, b));
+                nb = (ctx + BS - 1) / BS;
             } while (nb == 0 && b + 1 < P.batch);
         }
     }
