@@ -27,10 +27,10 @@
 // (optionally as one list per tile of a batch; see lane_tiles).
 // A row is one (query token, head in the GQA group) pair; 16 rows per tile
 // (MFMA N). The main kernel launches one worker (a wavefront, or sibling
-// wavefronts for several row tiles) per slot of the GPU (CUs x workers per
-// CU at this kernel's occupancy) and gives
-// each an equal contiguous slice of that list, computed on the device from
-// context_lens, so ragged lengths cost no imbalance and no tail. A tile that
+// wavefronts for several row tiles) per slot of the GPU (CUs x workers per CU
+// at this kernel's occupancy) and gives each an equal contiguous slice of that
+// list, computed on the device from context_lens, so ragged lengths cost no
+// imbalance and no tail. A tile that
 // lies inside one slice is finished (normalised and stored) by that wave; a
 // tile cut by slice boundaries leaves one partial (O, m, l) per piece, and a
 // second small kernel merges those by log-sum-exp. The kernel boundary orders
@@ -45,8 +45,9 @@
 //        B operand = V[tokens 4qd..4qd+3][dim 8pc+jj], built from four 16-B row
 //                    loads by an in-register 4x8 bf16 transpose
 //        C         = O[rows 4qd..4qd+3][dim 8pc+jj]
-// Within a segment, V of block i is issued before its QK and K of block i+1
-// is issued right after it, so both streams are in flight during the math.
+// Within a segment, V of block i is issued first and K of block i+1 as soon
+// as K of block i is consumed (after QK(i), or once K(i) is staged in LDS), so
+// both streams are in flight during the math.
 
 #include <hip/hip_runtime.h>
 
@@ -309,6 +310,8 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // LDS row, so the row writes and the operand reads each touch 16 distinct
 // 16-byte slots per 16 lanes. The K registers are free once a block is in
 // LDS, so the next block's K is issued before this block's QK.
+//
+// ctx and nblk are sequence b's (clamped) context length and block count.
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int ctx, const int nblk, const int blk_begin, const int blk_end,
