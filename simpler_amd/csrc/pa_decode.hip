@@ -55,6 +55,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -91,6 +92,7 @@ struct KernelParams {
     float *part_ml;  // [workers][2 slots][m[16], l[16]]
     unsigned *error_flag;
     const char *zeros;  // 256 bytes of the workspace that stay zero (LDS fill source)
+    const char *zero_page;  // zero bytes standing in for the 16-token tiles past a context's end, or null
     const float *k_scale;  // fp8 caches: [num_blocks][kv_heads] dequantisation scales
     const float *v_scale;
     int64_t k_block_stride, k_token_stride, k_head_stride;
@@ -387,21 +389,32 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
         return bad ? 0 : phys;
     };
-    auto load_k = [&](auto &kdst, int phys) {
+    // Base of 16-token tile t of block blk: tiles wholly past the context's end
+    // read the zero page instead (the same lane offsets, L2-resident zeros), so
+    // a sequence's last block costs only its valid tiles of HBM traffic while
+    // the loads stay unconditional (their wait counts stay exact). Scores of
+    // those tokens are masked and their V rows zeroed as before.
+    auto tile_base = [&](const char *blk_base, int blk, int t, int64_t tok_b) -> const char * {
+        const bool past = P.zero_page && 16 * t >= ctx - blk * BS;
+        return past ? P.zero_page : blk_base + (int64_t)(16 * t) * tok_b;
+    };
+    auto load_k = [&](auto &kdst, int phys, int blk) {
         const char *kb = k_head + (int64_t)phys * P.k_block_stride * ESZ;
         if constexpr (KLDS) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+            for (int t = 0; t < NT; ++t) {
+                const char *tb = tile_base(kb, blk, t, k_tok_b);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const char *kt = kb + (int64_t)(16 * t + e) * k_tok_b + k_lane;
+                    const char *kt = tb + (int64_t)e * k_tok_b + k_lane;
                     kdst[t][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(kt) : stream_ld16(kt);
                 }
+            }
             return;
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const char *kt = kb + (int64_t)(16 * t) * k_tok_b;
+            const char *kt = tile_base(kb, blk, t, k_tok_b);
 #pragma unroll
             for (int kk = 0; kk < (KV8 ? KS / 2 : KS); ++kk) {
                 if (KV8 || DK % 32 == 0 || 32 * kk + 8 * qd < DK)
@@ -411,13 +424,13 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             }
         }
     };
-    auto load_v = [&](auto &vdst, auto &vrawdst, int phys) {
+    auto load_v = [&](auto &vdst, auto &vrawdst, int phys, int blk) {
         const char *vb = v_head + (int64_t)phys * P.v_block_stride * ESZ;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const char *vt = vb + (int64_t)(16 * t + e) * v_tok_b;
+                const char *vt = tile_base(vb, blk, t, v_tok_b) + (int64_t)e * v_tok_b;
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds) {
                     if constexpr (KV8) {
@@ -587,7 +600,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     // would wait for K(i+1) as well.
     bool bad = false;
     int phys = checked(bt_row[blk_begin], bad);
-    load_k(kreg, phys);
+    load_k(kreg, phys, blk_begin);
     auto step = [&](const int blk, auto has_next) {
         constexpr bool NEXT = decltype(has_next)::value;
         const bool blk_bad = bad;
@@ -597,7 +610,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
         // block's loads together lets the caches serve the second request.
         if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
-        load_v(vreg, vraw, phys_b);
+        load_v(vreg, vraw, phys_b, blk);
         auto stage_k_and_prefetch = [&] {
             if constexpr (KLDS) {
                 // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
@@ -610,7 +623,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (NEXT) {
                     phys = checked(raw_next, bad);
-                    load_k(kreg, phys);
+                    load_k(kreg, phys, blk + 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -618,7 +631,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         auto prefetch_k = [&] {
             if constexpr (!KLDS && NEXT) {
                 phys = checked(raw_next, bad);
-                load_k(kreg, phys);
+                load_k(kreg, phys, blk + 1);
             }
         };
         compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k);
@@ -1400,6 +1413,7 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
 typedef void (*KernelFn)(KernelParams);
 
 constexpr int kZeroOffset = 128;  // workspace bytes [128, 256) are never written after init
+constexpr size_t kMaxZeroPageBytes = 1 << 20;  // larger token strides read the padding tiles as they are
 
 struct Plan {
     int workers;
@@ -1412,7 +1426,7 @@ struct Plan {
     int lanes;    // work lists (KernelParams::lanes)
     int64_t grid;
     KernelFn main;
-    size_t flag_bytes, part_ml_bytes, part_o_bytes;
+    size_t flag_bytes, zero_bytes, part_ml_bytes, part_o_bytes;
     size_t total;
 };
 
@@ -1647,13 +1661,21 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {
         p.grid = p.workers;
     }
     const int dv = a->head_dim_v;
-    // Layout: [error word] [m,l partials] [O partials]; two partial slots per
-    // worker wave.
+    // Layout: [error word] [zero page] [m,l partials] [O partials]; two
+    // partial slots per worker wave. The zero page covers the lane offsets of
+    // one 16-token tile (16 token strides of K or V, plus the dims): tiles past
+    // a context's end read it instead of the cache. Its contents do not affect
+    // results (those tokens are masked and their V rows zeroed), so calls of
+    // other shapes may overwrite it.
+    const int esz = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 ? 1 : 2;
+    const size_t tok_bytes = (size_t)std::max(a->k_token_stride, a->v_token_stride) * esz;
+    const size_t zero_bytes = align_up(16 * tok_bytes + 512, 256);
+    p.zero_bytes = (!k.mla && zero_bytes <= kMaxZeroPageBytes) ? zero_bytes : 0;
     const size_t pieces = (size_t)p.workers * p.tiles_per_worker * 2;
     p.flag_bytes = 256;  // error word at 0, zeros at [kZeroOffset, 256)
     p.part_ml_bytes = align_up(pieces * 32 * sizeof(float), 256);
     p.part_o_bytes = align_up(pieces * 16 * dv * sizeof(float), 256);
-    p.total = p.flag_bytes + p.part_ml_bytes + p.part_o_bytes;
+    p.total = p.flag_bytes + p.zero_bytes + p.part_ml_bytes + p.part_o_bytes;
     return p;
 }
 
@@ -1718,8 +1740,9 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     char *ws = (char *)workspace;
     P.error_flag = (unsigned *)ws;
     P.zeros = ws + kZeroOffset;
-    P.part_ml = (float *)(ws + plan.flag_bytes);
-    P.part_o = (float *)(ws + plan.flag_bytes + plan.part_ml_bytes);
+    P.zero_page = plan.zero_bytes ? ws + plan.flag_bytes : nullptr;
+    P.part_ml = (float *)(ws + plan.flag_bytes + plan.zero_bytes);
+    P.part_o = (float *)(ws + plan.flag_bytes + plan.zero_bytes + plan.part_ml_bytes);
     P.k_block_stride = a->k_block_stride;
     P.k_token_stride = a->k_token_stride;
     P.k_head_stride = a->k_head_stride;

@@ -207,13 +207,19 @@ def test_worker_plan():
     assert pa.plan(_args(num_heads=24, num_kv_heads=6)) == 1020
     assert pa.plan(_args(num_workers=7)) == 7
     ws = lambda **kw: _lib.lib().simpler_hip_pa_decode_workspace_size(ctypes.byref(_args(**kw)))
-    # error word + two (m, l) and two O partial slots per worker, 256-byte aligned sections
-    assert ws(num_workers=7) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
-    assert ws(num_workers=1) == 256 + 256 + 2 * 16 * 128 * 4
+    # error word, the zero page (16 token strides of 2 KB + 512 B: what one 16-token
+    # tile's lane offsets span), two (m, l) and two O partial slots per worker,
+    # 256-byte aligned sections
+    zero_page = 16 * 2048 + 512
+    assert ws(num_workers=7) == 256 + zero_page + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
+    assert ws(num_workers=1) == 256 + zero_page + 256 + 2 * 16 * 128 * 4
     # q_len 8 x group 4 = 32 rows = 2 row tiles: a worker is a 2-wave workgroup
     # and keeps two partial slots per wave
     assert pa.plan(_args(q_len=8, causal=1)) == 512
-    assert ws(q_len=8, causal=1, num_workers=7) == 256 + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
+    assert ws(q_len=8, causal=1, num_workers=7) == 256 + zero_page + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
+    # token strides too large for a 1 MB zero page: padding tiles are read as they are
+    assert ws(num_workers=7, k_token_stride=1 << 15, v_token_stride=1 << 15, k_block_stride=1 << 22,
+              v_block_stride=1 << 22) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
     # 25 row tiles: 4-wave workgroups, one per CU, in 7 work lists (row groups)
     assert pa.plan(_args(num_heads=80, num_kv_heads=1, q_len=5, causal=1)) == 252
 
