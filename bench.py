@@ -58,6 +58,48 @@ def parse() -> argparse.Namespace:
     return p.parse_args()
 
 
+def api_time(case, out, cfg, steps: int, warmup: int) -> dict | None:
+    """µs per `Worker(level=2).run` of the reference paged-attention callable on
+    the same device-resident inputs: the API time of a call, i.e. the
+    simpler_run host path through libsimpler_hip.so, its argument checks and
+    both kernels, up to the stream synchronisation it ends with."""
+    import ctypes
+
+    from simpler_amd import Worker
+    from simpler_amd import paged_attention as pa
+    from simpler_amd.task_interface import ChipStorageTaskArgs, ChipTensor
+    from simpler_amd.torch_interop import torch_dtype_to_datatype
+
+    def chip(t):
+        return ChipTensor.make(t.data_ptr(), tuple(int(x) for x in t.shape), torch_dtype_to_datatype(t.dtype),
+                               child_memory=True, strides=tuple(int(x) for x in t.stride()))
+
+    w = Worker(level=2, platform="mi355x", device_id=out.device.index or 0)
+    w.init()
+    try:
+        handle = w.register(pa.reference_chain_callable())
+        targs = ChipStorageTaskArgs()
+        for t in (case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out):
+            targs.add_tensor(chip(t))
+        if case.fp8:
+            targs.add_tensor(chip(case.k_scale))
+            targs.add_tensor(chip(case.v_scale))
+        targs.add_scalar(ctypes.c_float(case.scale))
+        if cfg.causal:
+            targs.add_scalar(1)
+        for _ in range(warmup):
+            w.chip_worker.run(handle, targs)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            w.chip_worker.run(handle, targs)
+        us = (time.perf_counter() - t0) / steps * 1e6
+    finally:
+        w.close()
+    return {"us_per_call": round(us, 2), "calls": steps,
+            "path": "Worker(level=2).run -> simpler_run (libsimpler_hip.so), device-resident tensors, "
+                    "reference QK/SF/PV/UP callable"}
+
+
 def cpu_baseline(case, args) -> dict | None:
     """Time the C restatement of the reference kernels on this host (kind "port")."""
     try:
@@ -363,6 +405,11 @@ def main() -> int:
         except Exception:
             traffic = None
 
+    try:
+        api = api_time(case, out, cfg, steps=min(args.steps, 100), warmup=min(args.warmup, 5))
+    except Exception as exc:  # reported, not fatal: the kernel figures above stand on their own
+        print(f"[bench] API timing skipped: {exc}", file=sys.stderr, flush=True)
+        api = None
     cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
     line = {
         "metric": METRIC if cfg.name == DEFAULT_CONFIG else f"{METRIC} [{cfg.name}]",
@@ -409,6 +456,7 @@ def main() -> int:
             "tflops": round(flops / (main_ms * 1e-3) / 1e12, 3),
             "mfma_frac": round(flops / (main_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         },
+        "api": api,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
