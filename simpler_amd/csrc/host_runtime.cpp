@@ -78,6 +78,14 @@ struct DeviceContext {
     size_t runs = 0;
     int32_t execution = SIMPLER_HIP_EXEC_FUSED;
     SimplerHipTaskGraph *graphs[2] = {nullptr, nullptr};  // eager, hipGraph
+    // Completion event of the runs on `stream`, recorded anew by every launch.
+    // Runs launched back to back share it, so waiting on an earlier one waits
+    // for the later ones too: later, never too early.
+    hipEvent_t done = nullptr;
+    // Pinned copy of the decode workspace's error word, written by an async
+    // copy queued behind each fused decode, so the wait reads it from host
+    // memory instead of a stream synchronisation and a blocking copy.
+    unsigned *err_host = nullptr;
 };
 
 // Native-run state lives in caller-owned storage of get_runtime_size() bytes
@@ -90,7 +98,7 @@ struct NativeRun {
     int32_t execution;  // SIMPLER_HIP_EXEC_* chosen at prepare
     int32_t n_tensors;
     int32_t n_staged;
-    hipEvent_t done;
+    hipEvent_t done;  // the context's completion event (not owned by the run)
     void *staged_dev[kMaxRunTensors];
     void *host_ptr[kMaxRunTensors];
     size_t staged_bytes[kMaxRunTensors];
@@ -423,8 +431,22 @@ int simpler_init(DeviceContextHandle h, int device_id, const uint8_t *, size_t, 
     if (hipSetDevice(device_id) != hipSuccess) return -1;
     hipStream_t s = nullptr;
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return -1;
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        hipStreamDestroy(s);
+        return -1;
+    }
+    void *pinned = nullptr;
+    if (hipHostMalloc(&pinned, 64, hipHostMallocDefault) != hipSuccess) {
+        hipEventDestroy(ev);
+        hipStreamDestroy(s);
+        return -1;
+    }
+    *static_cast<unsigned *>(pinned) = 0;
     c->device_id = device_id;
     c->stream = s;
+    c->done = ev;
+    c->err_host = static_cast<unsigned *>(pinned);
     if (const char *e = getenv("SIMPLER_HIP_EXECUTION")) {
         if (strcmp(e, "eager") == 0) c->execution = SIMPLER_HIP_EXEC_TASK_GRAPH;
         else if (strcmp(e, "graph") == 0) c->execution = SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH;
@@ -449,6 +471,10 @@ int finalize_device(DeviceContextHandle h) {
     if (c->workspace) hipFree(c->workspace);
     c->workspace = nullptr;
     c->workspace_bytes = 0;
+    if (c->done) hipEventDestroy(c->done);
+    c->done = nullptr;
+    if (c->err_host) hipHostFree(c->err_host);
+    c->err_host = nullptr;
     if (c->stream) hipStreamDestroy(c->stream);
     c->stream = nullptr;
     c->device_id = -1;
@@ -648,11 +674,7 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
             return rc;
         }
     }
-    if (hipEventCreateWithFlags(&r->done, hipEventDisableTiming) != hipSuccess) {
-        release_staged(r);
-        r->magic = 0;
-        return SIMPLER_HIP_ERR_LAUNCH;
-    }
+    r->done = c->done;
     r->state = 1;
     return 0;
 }
@@ -668,6 +690,9 @@ int simpler_launch_run(DeviceContextHandle h, RuntimeHandle runtime) {
         rc = run_task_graph(c, r);
     }
     if (rc != SIMPLER_HIP_OK) return rc;
+    if (r->kind == kPagedAttention && r->execution == SIMPLER_HIP_EXEC_FUSED &&
+        hipMemcpyAsync(c->err_host, c->workspace, sizeof(unsigned), hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+        return SIMPLER_HIP_ERR_LAUNCH;
     for (int i = 0; i < r->n_staged; ++i) {
         if (r->dir[i] == SIMPLER_ARG_IN) continue;
         if (hipMemcpyAsync(r->host_ptr[i], r->staged_dev[i], r->staged_bytes[i], hipMemcpyDeviceToHost,
@@ -696,6 +721,8 @@ int simpler_wait_run(DeviceContextHandle h, RuntimeHandle runtime) {
     if (!set_device(c) || !r || r->magic != kRunMagic || r->state != 2) return -1;
     if (hipEventSynchronize(r->done) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     if (r->kind != kPagedAttention || r->execution != SIMPLER_HIP_EXEC_FUSED) return SIMPLER_HIP_OK;
+    if (__atomic_load_n(c->err_host, __ATOMIC_ACQUIRE) == 0) return SIMPLER_HIP_OK;
+    // A bad block id was seen: the check re-reads the device word and clears it.
     return simpler_hip_pa_decode_check(c->workspace, c->workspace_bytes, c->stream);
 }
 
@@ -706,7 +733,6 @@ int simpler_finalize_run(DeviceContextHandle h, RuntimeHandle runtime) {
     if (r->magic != kRunMagic) return 0;
     if (r->state == 2) hipEventSynchronize(r->done);
     release_staged(r);
-    if (r->done) hipEventDestroy(r->done);
     memset(r, 0, sizeof(*r));
     return 0;
 }

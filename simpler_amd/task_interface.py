@@ -464,6 +464,7 @@ class ChipWorker:
         self._next_handle = 0
         size = int(self._lib.get_runtime_size())
         align = int(self._lib.get_runtime_alignment())
+        self._runtime_size = size
         self._runtime_raw = ctypes.create_string_buffer(size + align)
         base = ctypes.addressof(self._runtime_raw)
         self._runtime = base + (-base) % align
@@ -558,7 +559,7 @@ class ChipWorker:
         if slot is None:
             raise KeyError("unknown callable handle")
         with self._lock:
-            ctypes.memset(self._runtime, 0, int(self._lib.get_runtime_size()))
+            ctypes.memset(self._runtime, 0, self._runtime_size)
             rc = self._lib.simpler_run(ctx, self._runtime, slot, ctypes.addressof(args), ctypes.byref(cfg), None)
         if rc != 0:
             raise RuntimeError(f"simpler_run failed: {rc}")

@@ -72,6 +72,43 @@ def test_worker_run_with_device_tensors_and_bf16_out(worker, device):
     assert_close(out.float().cpu().numpy(), ref, what="worker/device")
 
 
+def device_args(d, out):
+    args = ChipStorageTaskArgs()
+    for t in (d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out):
+        args.add_tensor(ChipTensor.make(t.data_ptr(), tuple(t.shape), {
+            torch.bfloat16: DataType.BFLOAT16, torch.int32: DataType.INT32,
+            torch.float32: DataType.FLOAT32}[t.dtype], child_memory=True))
+    args.add_scalar(ctypes.c_float(d.scale))
+    return args
+
+
+def test_worker_reports_device_bad_block_then_recovers(worker, device):
+    """A device-resident table with an out-of-pool id is only seen by the kernel:
+    the run fails with SIMPLER_HIP_ERR_BAD_BLOCK (-6), the error word is cleared,
+    and the runs after it on the same context succeed and match the oracle."""
+    print("[case] worker device bad block, then three good runs", flush=True)
+    case = make_custom_case(batch=3, num_heads=16, kv_heads=2, head_dim=64, block_size=16,
+                            context_lens=[40, 17, 64], seed=11, max_blocks=8)
+    d = case.to(device)
+    handle = worker.register(pa.reference_chain_callable())
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    bad_table = d.block_table.clone()
+    bad_table[1, 1] = case.key_cache.shape[0] + 5
+    good_table = d.block_table
+    d.block_table = bad_table
+    torch.cuda.synchronize(device)
+    with pytest.raises(RuntimeError, match="-6"):
+        worker.chip_worker.run(handle, device_args(d, out))
+    d.block_table = good_table
+    ref = oracle_numpy(case)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize(device)
+        worker.chip_worker.run(handle, device_args(d, out))
+        assert_close(out.cpu().numpy(), ref, what=f"worker/device run {i} after a bad block")
+    worker.unregister(handle)
+
+
 def test_worker_malloc_copy_roundtrip(worker):
     buf = worker.malloc(4096)
     src = torch.arange(1024, dtype=torch.int32)
