@@ -339,8 +339,8 @@ int check_host_tables(const SimplerChipStorageTaskArgs *a, const SimplerHipPaDec
 int ensure_workspace(DeviceContext *c, size_t need) {
     if (need <= c->workspace_bytes) return SIMPLER_HIP_OK;
     if (c->workspace) {
-        hipStreamSynchronize(c->stream);
-        hipFree(c->workspace);
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->workspace);
         c->workspace = nullptr;
         c->workspace_bytes = 0;
     }
@@ -394,7 +394,7 @@ int run_task_graph(DeviceContext *c, NativeRun *r) {
 
 void release_staged(NativeRun *r) {
     for (int i = 0; i < r->n_staged; ++i) {
-        if (r->staged_dev[i]) hipFree(r->staged_dev[i]);
+        if (r->staged_dev[i]) (void)hipFree(r->staged_dev[i]);
         r->staged_dev[i] = nullptr;
     }
     r->n_staged = 0;
@@ -433,13 +433,13 @@ int simpler_init(DeviceContextHandle h, int device_id, const uint8_t *, size_t, 
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return -1;
     hipEvent_t ev = nullptr;
     if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
-        hipStreamDestroy(s);
+        (void)hipStreamDestroy(s);
         return -1;
     }
     void *pinned = nullptr;
     if (hipHostMalloc(&pinned, 64, hipHostMallocDefault) != hipSuccess) {
-        hipEventDestroy(ev);
-        hipStreamDestroy(s);
+        (void)hipEventDestroy(ev);
+        (void)hipStreamDestroy(s);
         return -1;
     }
     *static_cast<unsigned *>(pinned) = 0;
@@ -459,23 +459,23 @@ int finalize_device(DeviceContextHandle h) {
     if (!c) return -1;
     std::lock_guard<std::mutex> lk(c->mu);
     if (c->device_id < 0) return 0;
-    hipSetDevice(c->device_id);
-    if (c->stream) hipStreamSynchronize(c->stream);
+    (void)hipSetDevice(c->device_id);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (SimplerHipTaskGraph *&g : c->graphs) {
         simpler_hip_tg_destroy(g);
         g = nullptr;
     }
-    for (auto &kv : c->allocs) hipFree(kv.first);
+    for (auto &kv : c->allocs) (void)hipFree(kv.first);
     c->allocs.clear();
     c->committed = 0;
-    if (c->workspace) hipFree(c->workspace);
+    if (c->workspace) (void)hipFree(c->workspace);
     c->workspace = nullptr;
     c->workspace_bytes = 0;
-    if (c->done) hipEventDestroy(c->done);
+    if (c->done) (void)hipEventDestroy(c->done);
     c->done = nullptr;
-    if (c->err_host) hipHostFree(c->err_host);
+    if (c->err_host) (void)hipHostFree(c->err_host);
     c->err_host = nullptr;
-    if (c->stream) hipStreamDestroy(c->stream);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
     c->stream = nullptr;
     c->device_id = -1;
     return 0;
@@ -498,10 +498,10 @@ void device_free_ctx(DeviceContextHandle h, void *p) {
     std::lock_guard<std::mutex> lk(c->mu);
     auto it = c->allocs.find(p);
     if (it == c->allocs.end()) return;
-    hipStreamSynchronize(c->stream);
+    (void)hipStreamSynchronize(c->stream);
     c->committed -= it->second;
     c->allocs.erase(it);
-    hipFree(p);
+    (void)hipFree(p);
 }
 
 size_t committed_device_memory_ctx(DeviceContextHandle h) {
@@ -731,7 +731,7 @@ int simpler_finalize_run(DeviceContextHandle h, RuntimeHandle runtime) {
     NativeRun *r = static_cast<NativeRun *>(runtime);
     if (!set_device(c) || !r) return -1;
     if (r->magic != kRunMagic) return 0;
-    if (r->state == 2) hipEventSynchronize(r->done);
+    if (r->state == 2) (void)hipEventSynchronize(r->done);
     release_staged(r);
     memset(r, 0, sizeof(*r));
     return 0;

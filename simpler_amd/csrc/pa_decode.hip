@@ -757,16 +757,21 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
 }
 
 // ---------------------------------------------------------------------------
-// Merge kernel: one 256-thread workgroup per tile; log-sum-exp merge of the pieces
+// Merge kernel: one workgroup per tile; log-sum-exp merge of the pieces
 // (pa_kernel.cce:1666-1773 CombineScale), and zeros for empty contexts.
 // ---------------------------------------------------------------------------
 
-constexpr int kMergeThreads = 256;
+// Threads per merge workgroup: one 16-byte unit of a tile's 16 x DV output per
+// thread up to DV = 128 (512 threads), four per thread for MLA's DV = 512.
+template <int DV> constexpr int merge_threads() { return DV * 4 < 512 ? (DV * 4 < 64 ? 64 : DV * 4) : 512; }
 constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weights
-constexpr int kMergePrefetch = 8;    // partial rows per thread read before the weights are known
 
 template <int DV, typename OutT>
-__global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelParams P) {
+__global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const KernelParams P) {
+    constexpr int MT = merge_threads<DV>();
+    constexpr int UNITS = 16 * (DV / 4);            // 16-byte units of a full tile
+    constexpr int UPT = (UNITS + MT - 1) / MT;      // units per thread
+    constexpr int PRE = UPT == 1 ? 8 : 4;           // pieces per unit read before the weights are known
     const int tid = threadIdx.x;
     const int tpb = P.kv_heads * P.row_tiles;
     const int tile = blockIdx.x;  // (batch, kv head, row tile)
@@ -780,7 +785,7 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
     const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
     const int nb = blocks_of(P, b);
     if (nb == 0) {  // empty context: defined as a zero output
-        for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
+        for (int idx = tid; idx < rows_here * (DV / 4); idx += MT) {
             const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
             OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4,
                                    (f32x4_t){0.f, 0.f, 0.f, 0.f});
@@ -803,22 +808,26 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
     const int np = w_last - w_first + 1;
     if (np <= kMergeLdsPieces) {
         // Per-(row, piece) weights e^{m_w - M} / L once per workgroup, then the
-        // partial rows stream through with no dependent loads in the way. The
-        // thread's first unit reads its first kMergePrefetch partial rows
-        // together with the (m, l) loads: they do not depend on the weights.
+        // partial rows stream through with no dependent loads in the way. Every
+        // unit of the thread has its first PRE pieces read together with the
+        // (m, l) loads: they do not depend on the weights, so the merge is one
+        // memory round trip after the work scan, not one per unit.
         __shared__ float wgt[16][kMergeLdsPieces];  // m of each (row, piece), then its weight
         __shared__ float lsum[16][kMergeLdsPieces];
         const int units = rows_here * (DV / 4);
-        f32x4_t pre[kMergePrefetch];
-        {
-            const int row = tid / (DV / 4), c4 = tid - row * (DV / 4);
+        f32x4_t pre[UPT][PRE];
 #pragma unroll
-            for (int k = 0; k < kMergePrefetch; ++k)
-                pre[k] = (tid < units && k < np)
-                             ? *reinterpret_cast<const f32x4_t *>(P.part_o + (piece_of(w_first + k) * 16 + row) * DV + 4 * c4)
-                             : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < UPT; ++u) {
+            const int idx = tid + u * MT;
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+#pragma unroll
+            for (int k = 0; k < PRE; ++k)
+                pre[u][k] = (idx < units && k < np)
+                                ? *reinterpret_cast<const f32x4_t *>(P.part_o + (piece_of(w_first + k) * 16 + row) * DV +
+                                                                     4 * c4)
+                                : (f32x4_t){0.f, 0.f, 0.f, 0.f};
         }
-        for (int e = tid; e < 16 * np; e += kMergeThreads) {  // all (m, l) loads in flight at once
+        for (int e = tid; e < 16 * np; e += MT) {  // all (m, l) loads in flight at once
             const int row = e / np, k = e - row * np;
             const int64_t pc = piece_of(w_first + k);
             wgt[row][k] = P.part_ml[pc * 32 + row];
@@ -838,18 +847,17 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
             for (int k = 0; k < np; ++k) wgt[tid][k] *= inv;
         }
         __syncthreads();
-        for (int idx = tid; idx < units; idx += kMergeThreads) {
+#pragma unroll
+        for (int u = 0; u < UPT; ++u) {
+            const int idx = tid + u * MT;
+            if (idx >= units) break;
             const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
             f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-            int k = 0;
-            if (idx == tid) {  // the prefetched rows first
 #pragma unroll
-                for (int kp = 0; kp < kMergePrefetch; ++kp)
-                    if (kp < np) o += wgt[row][kp] * pre[kp];
-                k = kMergePrefetch;
-            }
+            for (int k = 0; k < PRE; ++k)
+                if (k < np) o += wgt[row][k] * pre[u][k];
 #pragma unroll 4
-            for (; k < np; ++k) {
+            for (int k = PRE; k < np; ++k) {
                 const int64_t piece = piece_of(w_first + k);
                 o += wgt[row][k] * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
             }
@@ -857,7 +865,7 @@ __global__ void __launch_bounds__(kMergeThreads) pa_merge_kernel(const KernelPar
         }
         return;
     }
-    for (int idx = tid; idx < rows_here * (DV / 4); idx += kMergeThreads) {
+    for (int idx = tid; idx < rows_here * (DV / 4); idx += MT) {
         const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
         float M = -INFINITY;
         for (int w = w_first; w <= w_last; ++w) M = fmaxf(M, P.part_ml[piece_of(w) * 32 + row]);
@@ -1473,13 +1481,14 @@ struct KernelPair {
     KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     KernelFn merge;
     bool mla;
-    bool klds;  // `main` stages K through LDS (full-row K reads)
+    bool klds;          // `main` stages K through LDS (full-row K reads)
+    int merge_threads;  // workgroup size of `merge`
 };
 
 template <int BS, int D, typename OutT, bool KV8 = false>
 KernelPair pick_fn() {
     return {pa_decode_kernel<BS, D, D, OutT, 1, KV8>, pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, KV8>,
-            pa_merge_kernel<D, OutT>, false, !KV8 && D == 128};
+            pa_merge_kernel<D, OutT>, false, !KV8 && D == 128, merge_threads<D>()};
 }
 
 // fp8 caches: head dim 128 (Llama/Qwen GQA), the four block sizes.
@@ -1534,8 +1543,10 @@ bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
 template <typename OutT>
 KernelPair pick_mla(int bs) {
     switch (bs) {
-        case 32: return {pa_mla_kernel<32, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false};
-        case 64: return {pa_mla_kernel<64, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false};
+        case 32: return {pa_mla_kernel<32, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false,
+                         merge_threads<kMlaDv>()};
+        case 64: return {pa_mla_kernel<64, kMlaDk, kMlaDv, OutT>, nullptr, pa_merge_kernel<kMlaDv, OutT>, true, false,
+                         merge_threads<kMlaDv>()};
         default: return {nullptr, nullptr, nullptr, false, false};
     }
 }
@@ -1775,7 +1786,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     if (phases & SIMPLER_HIP_PHASE_MERGE) {
-        hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3(kMergeThreads), 0, (hipStream_t)stream, P);
+        hipLaunchKernelGGL(k.merge, dim3((unsigned)tiles), dim3((unsigned)k.merge_threads), 0, (hipStream_t)stream, P);
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     return SIMPLER_HIP_OK;
