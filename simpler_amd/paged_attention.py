@@ -56,6 +56,8 @@ class _Workspace:
         with self._mu:
             buf = self._buf.get(idx)
             if buf is None or buf.numel() < nbytes:
+                if buf is not None:  # launches on any stream may still use the old buffer
+                    torch.cuda.synchronize(device)
                 size = max(nbytes, 1 << 20)
                 buf = torch.empty(size + 256, dtype=torch.uint8, device=device)
                 off = (-buf.data_ptr()) % 256

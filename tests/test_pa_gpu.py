@@ -292,6 +292,39 @@ def test_workspace_shared_by_every_kernel(device):
         assert_close(run_gpu(gqa, device, num_workers=workers), ref, what=f"gqa after few w{workers}")
 
 
+def _poison_workspace(device):
+    """Fill the workspace's partial slots and zero page with 0xFF bytes (NaN as
+    fp32), keeping the first 256 bytes (error word, zeros): a piece the merge
+    reads but no segment wrote turns the output into NaN."""
+    torch.cuda.synchronize(device)
+    buf = pa._WORKSPACE._buf[device.index or 0]
+    buf[256:].fill_(255)
+    torch.cuda.synchronize(device)
+
+
+@pytest.mark.parametrize("shape", ["d128_bs128", "d64_bs16"])
+@pytest.mark.parametrize("workers", [0, 7, 333])
+def test_every_piece_the_merge_reads_is_written(shape, workers, device):
+    # The merge kernel reads the partial pieces of every cut tile. On a workspace
+    # whose partial slots hold NaN, three launches must match the oracle and each
+    # other bit for bit: no piece is read that this launch did not write.
+    print(f"[case] poisoned workspace {shape} workers={workers}", flush=True)
+    if shape == "d128_bs128":
+        case = make_custom_case(batch=12, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                context_lens=[1, 5000, 129, 2048, 7000, 300, 0, 4097, 128, 6500, 50, 3333], seed=911)
+    else:
+        case = make_custom_case(batch=9, num_heads=16, kv_heads=4, head_dim=64, block_size=16,
+                                context_lens=[17, 900, 1, 1600, 333, 16, 1200, 0, 777], seed=912)
+    ref = oracle_numpy(case)
+    run_gpu(case, device, num_workers=workers)  # sizes the workspace for this plan
+    _poison_workspace(device)
+    runs = [run_gpu(case, device, num_workers=workers) for _ in range(3)]
+    for i, got in enumerate(runs):
+        assert np.isfinite(got).all(), f"launch {i}: a piece was read that no segment wrote"
+        assert_close(got, ref, what=f"poisoned workspace {shape} w{workers} launch {i}")
+    assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[1], runs[2])
+
+
 @pytest.mark.parametrize("workers", [0, 5000])
 def test_many_short_tiles(workers, device):
     # 520 sequences x 32 kv heads = 16640 tiles of 0..3 blocks each, with 1024
