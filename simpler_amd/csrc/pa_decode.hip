@@ -156,8 +156,6 @@ __device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(unsigned w0, unsigned w1) {
     return (u32x4_t){a[0], a[1], b[0], b[1]};
 }
 
-__device__ __forceinline__ float bf16lo_to_f32(unsigned w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16hi_to_f32(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
 
 template <typename OutT>
 struct OutStore;
@@ -362,7 +360,12 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegClamp, f_run = kNegClamp, l_part = 0.f;
+    // Row sums of the rounded p on the matrix unit (P x ones), kept in A's
+    // frame: every lane holds rows 4qd+e like A's columns.
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const i16x4_t ones4 = __builtin_bit_cast(i16x4_t, (u32x2_t){0x3f803f80u, 0x3f803f80u});  // bf16 1.0
+    constexpr float kLog2e = 1.4426950408889634f;
+    float m_run = kNegClamp, f_run = kNegClamp;
 
     // bf16: the operands themselves; fp8: the raw bytes (half the registers)
     u32x4_t kreg[NT][KV8 ? KS / 2 : KS];
@@ -489,7 +492,14 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         after_qk();
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- softmax prepare: mask, scale, block max (golden :145-165) ----
+        // ---- softmax prepare: mask, block max of s*scale (golden :145-165).
+        // For scale > 0 the max of the scaled scores is the scaled max, so the
+        // scale folds into the exponent below; otherwise scale first ----
+        if (!(sc > 0.f)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
         const int blk0 = blk * BS;
         const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
         const int rvalid = blk_bad ? 0 : rowlen - blk0;  // tokens of this block visible to row pc
@@ -498,54 +508,60 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float x = s[t][e] * sc;
+                float x = s[t][e];
                 if (!full) x = (16 * t + 4 * qd + e < rvalid) ? x : -INFINITY;
                 s[t][e] = x;
                 mx = fmaxf(mx, x);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mb = fmaxf(mx, kNegClamp);
+        const float mb = fmaxf(mx * sc, kNegClamp);
 
         // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
         const float mnew = first ? mb : fmaxf(m_run, mb);
         const bool use = first || (mb >= mnew - kFrameGap);
-        const float alpha = first ? 0.f : __expf(m_run - mnew);
-        const float beta = __expf(mb - mnew);
-        float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        const float cfe = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);  // e^{f - m_blk}
+        float cf = cfe;
         const bool v_zero = KV8 && vs == 0.f;  // this block's V is zero: nothing to add
         if (KV8 && use && !v_zero) {            // move this row's A into the block's V-scale frame
             cf *= vs_frame / vs;
             vs_frame = vs;
         }
 
-        // ---- p = bf16(exp(s - m_blk)); l_blk = sum of the rounded p ----
+        // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e -
+        // m_blk*log2e)); a skipped block (use false) gives p = 0 ----
+        const float mb2 = use ? mb * kLog2e : INFINITY;
+        const float sc2 = sc * kLog2e;
         i16x4_t pa[NT];
-        float lb = 0.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             float p[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = use ? __expf(s[t][e] - mb) : 0.f;
-            const unsigned w0 = pack_bf16x2(p[0], p[1]);
-            const unsigned w1 = pack_bf16x2(p[2], p[3]);
-            lb += (bf16lo_to_f32(w0) + bf16hi_to_f32(w0)) + (bf16lo_to_f32(w1) + bf16hi_to_f32(w1));
-            pa[t] = __builtin_bit_cast(i16x4_t, (u32x2_t){w0, w1});
+            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
+            pa[t] = __builtin_bit_cast(i16x4_t, (u32x2_t){pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
         }
-        l_part = first ? lb : alpha * l_part + beta * lb;
         m_run = mnew;
         if (use) f_run = mb;
 
-        // ---- rescale A to the new frame (rows 4qd+e live in lane 4qd+e's cf) ----
+        // ---- rescale A (and its row sums) to the new frame (rows 4qd+e live
+        // in lane 4qd+e's factors) ----
         {
-            f32x4_t cv;
+            f32x4_t cv, cl;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
+            for (int e = 0; e < 4; ++e) {
+                cv[e] = __shfl(cf, 4 * qd + e, 64);
+                cl[e] = KV8 ? __shfl(cfe, 4 * qd + e, 64) : cv[e];
+            }
 #pragma unroll
             for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
+            lacc *= cl;
         }
+        // row sums of the rounded p (every column of P x ones is the sum),
+        // also for a block whose V adds nothing
+#pragma unroll
+        for (int t = 0; t < NT; ++t) lacc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[t], ones4, lacc, 0, 0, 0);
 
         // ---- PV: A += P * V ----
         const int vvalid = (blk_bad || v_zero) ? 0 : min(BS, ctx - blk0);  // tokens with defined V
@@ -576,14 +592,14 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                     const int w = jj >> 1;
                     const unsigned a0 = vt4[ds][0][w], a1 = vt4[ds][1][w];
                     const unsigned a2 = vt4[ds][2][w], a3 = vt4[ds][3][w];
-                    unsigned d0, d1;
-                    if (jj & 1) {
-                        d0 = (a0 >> 16) | (a1 & 0xffff0000u);
-                        d1 = (a2 >> 16) | (a3 & 0xffff0000u);
-                    } else {
-                        d0 = (a0 & 0xffffu) | (a1 << 16);
-                        d1 = (a2 & 0xffffu) | (a3 << 16);
-                    }
+                    // the bf16 of dim 2w + (jj & 1) of tokens (0, 1) and (2, 3):
+                    // low halves (bytes 0-1 of each) or high halves (bytes 2-3),
+                    // one v_perm_b32 each (bytes 0-3 from the second operand,
+                    // 4-7 from the first)
+                    constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                    const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                    const unsigned d0 = __builtin_amdgcn_perm(a1, a0, sel);
+                    const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
                     acc[ds][jj] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
                         pa[t], __builtin_bit_cast(i16x4_t, (u32x2_t){d0, d1}), acc[ds][jj], 0, 0, 0);
                 }
@@ -639,15 +655,23 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     for (int blk = blk_begin; blk + 1 < blk_end; ++blk) step(blk, std::true_type{});
     step(blk_end - 1, std::false_type{});
 
-    // ---- finish: O = e^{f-m} A, l = sum over the four lane groups ----
-    float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
-    const float osc = __expf(f_run - m_run) * vs_frame;
-    float l_e[4], o_e[4];
+    // ---- finish: O = e^{f-m} A and l = e^{f-m} L, in the frame of m ----
+    const float oscl = __expf(f_run - m_run);  // row pc's
+    const float osc = oscl * vs_frame;
+    float l_e[4], o_e[4];  // rows 4qd+e
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        l_e[e] = __shfl(l_tot, 4 * qd + e, 64);
+        l_e[e] = lacc[e] * __shfl(oscl, 4 * qd + e, 64);
         o_e[e] = __shfl(osc, 4 * qd + e, 64);
+    }
+    // row pc's l: element pc % 4 of the lanes of group pc / 4
+    float l_tot;
+    {
+        float lr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lr[e] = __shfl(l_e[e], 16 * (pc >> 2) + pc, 64);
+        const int ep = pc & 3;
+        l_tot = ep == 0 ? lr[0] : ep == 1 ? lr[1] : ep == 2 ? lr[2] : lr[3];
     }
 
     if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
