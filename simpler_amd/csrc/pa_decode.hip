@@ -503,16 +503,20 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const int blk0 = blk * BS;
         const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
         const int rvalid = blk_bad ? 0 : rowlen - blk0;  // tokens of this block visible to row pc
+        // one wave-uniform branch around the masking (per-element selects
+        // would run on every block)
+        if (!full) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x = s[t][e];
-                if (!full) x = (16 * t + 4 * qd + e < rvalid) ? x : -INFINITY;
-                s[t][e] = x;
-                mx = fmaxf(mx, x);
-            }
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mb = fmaxf(mx * sc, kNegClamp);
