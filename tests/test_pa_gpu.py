@@ -292,6 +292,45 @@ def test_workspace_shared_by_every_kernel(device):
         assert_close(run_gpu(gqa, device, num_workers=workers), ref, what=f"gqa after few w{workers}")
 
 
+def _visible_v_mean(case) -> np.ndarray:
+    """Closed form for scale 0: every visible token weighs exactly 1 (p =
+    bf16(e^0)), so each output row is the mean of its visible V rows."""
+    c = case.config
+    bs = case.key_cache.shape[1]
+    v_all = case.value_cache.float().numpy() if not c.mla else case.key_cache.float().numpy()[..., : c.head_dim_v]
+    out = np.zeros(case.out_shape(), dtype=np.float64)
+    for b in range(case.query.shape[0]):
+        L = int(case.context_lens[b])
+        rows = v_all[case.block_table[b, : (L + bs - 1) // bs].long().numpy()].reshape(-1, *v_all.shape[2:])[:L]
+        g = c.num_heads // c.kv_heads
+        for h in range(c.num_heads):
+            out[b, h] = rows[:, h // g].mean(axis=0)
+    return out
+
+
+@pytest.mark.parametrize("shape", ["gqa_d128_bs128", "gqa_d64_bs16", "mla"])
+def test_scale_zero_and_negative(shape, device):
+    # The kernels fold a positive scale into the exponent and scale the scores
+    # first otherwise. Scale 0 must give the plain mean of the visible V rows;
+    # a negative scale must match the oracle.
+    print(f"[case] scale 0 / negative {shape}", flush=True)
+    lens = [1, 130, 333, 700]
+    if shape == "gqa_d128_bs128":
+        case = make_custom_case(batch=4, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                context_lens=lens, seed=921)
+    elif shape == "gqa_d64_bs16":
+        case = make_custom_case(batch=4, num_heads=16, kv_heads=2, head_dim=64, block_size=16,
+                                context_lens=lens, seed=922)
+    else:
+        case = _mla_case(heads=128, lens=lens, seed=923)
+    case.scale = 0.0
+    got = run_gpu(case, device)
+    assert_close(got, _visible_v_mean(case), what=f"{shape} scale 0 vs the mean of V")
+    assert_close(got, oracle_numpy(case), what=f"{shape} scale 0 vs oracle")
+    case.scale = -0.088
+    assert_close(run_gpu(case, device), oracle_numpy(case), what=f"{shape} scale -0.088")
+
+
 def _poison_workspace(device):
     """Fill the workspace's partial slots and zero page with 0xFF bytes (NaN as
     fp32), keeping the first 256 bytes (error word, zeros): a piece the merge
