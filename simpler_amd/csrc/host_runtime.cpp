@@ -39,6 +39,7 @@
 #include "simpler_hip/pa_decode.h"
 #include "simpler_hip/pto_runtime_c_api.h"
 #include "simpler_hip/task_graph.h"
+#include "pa_decode_internal.h"
 
 namespace {
 
@@ -82,9 +83,9 @@ struct DeviceContext {
     // Runs launched back to back share it, so waiting on an earlier one waits
     // for the later ones too: later, never too early.
     hipEvent_t done = nullptr;
-    // Pinned copy of the decode workspace's error word, written by an async
-    // copy queued behind each fused decode, so the wait reads it from host
-    // memory instead of a stream synchronisation and a blocking copy.
+    // Host copy of the decode workspace's error word in coherent pinned
+    // memory, stored by each fused decode's merge kernel, so the wait reads it
+    // from host memory instead of a stream synchronisation and a blocking copy.
     unsigned *err_host = nullptr;
 };
 
@@ -437,7 +438,7 @@ int simpler_init(DeviceContextHandle h, int device_id, const uint8_t *, size_t, 
         return -1;
     }
     void *pinned = nullptr;
-    if (hipHostMalloc(&pinned, 64, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc(&pinned, 64, hipHostMallocCoherent) != hipSuccess) {
         (void)hipEventDestroy(ev);
         (void)hipStreamDestroy(s);
         return -1;
@@ -685,14 +686,13 @@ int simpler_launch_run(DeviceContextHandle h, RuntimeHandle runtime) {
     if (!set_device(c) || !r || r->magic != kRunMagic || r->state != 1) return -1;
     int rc;
     if (r->kind == kPagedAttention && r->execution == SIMPLER_HIP_EXEC_FUSED) {
-        rc = simpler_hip_pa_decode(&r->args, c->workspace, c->workspace_bytes, c->stream);
+        // the merge kernel overwrites it; a batch of 0 launches nothing
+        __atomic_store_n(c->err_host, 0u, __ATOMIC_RELEASE);
+        rc = simpler_hip::pa_decode_with_mirror(&r->args, c->workspace, c->workspace_bytes, c->stream, c->err_host);
     } else {
         rc = run_task_graph(c, r);
     }
     if (rc != SIMPLER_HIP_OK) return rc;
-    if (r->kind == kPagedAttention && r->execution == SIMPLER_HIP_EXEC_FUSED &&
-        hipMemcpyAsync(c->err_host, c->workspace, sizeof(unsigned), hipMemcpyDeviceToHost, c->stream) != hipSuccess)
-        return SIMPLER_HIP_ERR_LAUNCH;
     for (int i = 0; i < r->n_staged; ++i) {
         if (r->dir[i] == SIMPLER_ARG_IN) continue;
         if (hipMemcpyAsync(r->host_ptr[i], r->staged_dev[i], r->staged_bytes[i], hipMemcpyDeviceToHost,

@@ -61,6 +61,7 @@
 #include <vector>
 
 #include "simpler_hip/pa_decode.h"
+#include "pa_decode_internal.h"
 
 namespace simpler_hip {
 namespace {
@@ -105,6 +106,7 @@ struct KernelParams {
     int32_t lanes;  // independent work lists; list u holds tiles [u, u+1) * (tiles per batch / lanes) of each batch
     float scale;
     int32_t causal;
+    unsigned *err_mirror;  // host-visible copy of *error_flag written by the merge kernel, or null
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
@@ -801,6 +803,11 @@ __global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const Ker
     constexpr int UPT = (UNITS + MT - 1) / MT;      // units per thread
     constexpr int PRE = UPT == 1 ? 8 : 4;           // pieces per unit read before the weights are known
     const int tid = threadIdx.x;
+    // The main kernel is done: hand its error word to the host through
+    // pinned memory (a run's wait then needs no device-to-host copy).
+    if (P.err_mirror && blockIdx.x == 0 && tid == 0)
+        __hip_atomic_store(P.err_mirror, __hip_atomic_load(P.error_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int tpb = P.kv_heads * P.row_tiles;
     const int tile = blockIdx.x;  // (batch, kv head, row tile)
     const int b = tile / tpb, jr = tile - b * tpb;
@@ -1758,8 +1765,10 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
                                        SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE);
 }
 
-extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
-                                           void *stream, int phases) {
+namespace simpler_hip {
+namespace {
+int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes, void *stream,
+                     int phases, unsigned *err_mirror) {
     if (phases & ~(SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE)) return SIMPLER_HIP_ERR_INVALID;
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
@@ -1806,6 +1815,7 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
     P.k_scale = a->k_scale;
     P.v_scale = a->v_scale;
+    P.err_mirror = (phases & SIMPLER_HIP_PHASE_MERGE) ? err_mirror : nullptr;
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
@@ -1818,6 +1828,19 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }
     return SIMPLER_HIP_OK;
+}
+}  // namespace
+
+int pa_decode_with_mirror(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes, void *stream,
+                          unsigned *err_mirror) {
+    return pa_decode_launch(a, workspace, workspace_bytes, stream, SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE,
+                            err_mirror);
+}
+}  // namespace simpler_hip
+
+extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
+                                           void *stream, int phases) {
+    return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream, phases, nullptr);
 }
 
 extern "C" int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream) {
