@@ -571,6 +571,26 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 
         // ---- PV: A += P * V ----
         const int vvalid = (blk_bad || v_zero) ? 0 : min(BS, ctx - blk0);  // tokens with defined V
+        // V rows past the context's end (and of an out-of-pool block) are
+        // zeroed once, under one wave-uniform branch ahead of PV, where the
+        // selects would run on every block. The K-through-LDS kernel keeps
+        // them in PV, which measured faster there (cfg2: 112.5 against
+        // 113.2 us per step; fp8 63.1 against 62.8 the other way).
+        constexpr bool kZeroAhead = !KLDS;
+        if (kZeroAhead && vvalid < BS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= vvalid)
+#pragma unroll
+                        for (int ds = 0; ds < DVS; ++ds) {
+                            if constexpr (KV8)
+                                vrw[t][ds][e] = (u32x2_t){0u, 0u};
+                            else
+                                vr[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                        }
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if (KV8 && v_zero) break;  // wave-uniform: the block adds nothing
@@ -584,7 +604,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                     else
                         vt4[ds][e] = vr[t][ds][e];
                 }
-            if (vvalid < BS) {
+            if (!kZeroAhead && vvalid < BS) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (16 * t + 4 * qd + e >= vvalid)
