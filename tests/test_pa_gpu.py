@@ -331,6 +331,49 @@ def test_scale_zero_and_negative(shape, device):
     assert_close(run_gpu(case, device), oracle_numpy(case), what=f"{shape} scale -0.088")
 
 
+@pytest.mark.parametrize("shape", ["gqa_d128", "verify_q8", "mla"])
+def test_decode_replays_from_a_hip_graph(shape, device):
+    # The decode launches no memset and allocates nothing once its workspace is
+    # sized, so a caller can capture it. Replays after eager work that changes
+    # the query must each match the oracle for the query of that moment.
+    print(f"[case] hip graph replays {shape}", flush=True)
+    if shape == "gqa_d128":
+        case = make_custom_case(batch=6, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                                context_lens=[1, 700, 2048, 129, 3000, 64], seed=931)
+    elif shape == "verify_q8":
+        case = make_custom_case(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, q_len=8,
+                                causal=True, context_lens=[8, 900, 2500], seed=932)
+    else:
+        case = _mla_case(heads=128, lens=[1, 69, 700, 2100], seed=933)
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    queries = [d.query.clone(), (d.query.float() * -0.5).to(d.query.dtype)]
+
+    def decode():
+        pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out,
+                                  case.scale, causal=case.config.causal)
+
+    decode()  # sizes and zeroes the workspace outside the capture
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode()
+    torch.cuda.synchronize(device)
+    expected = []
+    for q in queries:
+        case.query = q.cpu()
+        expected.append(oracle_numpy(case))
+    for i in range(3):
+        k = i % 2
+        d.query.copy_(queries[k])  # eager work between replays
+        out.fill_(float("nan"))
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert_close(out.cpu().numpy(), expected[k], what=f"{shape} graph replay {i}")
+    pa.check_errors(device)
+
+
 def _poison_workspace(device):
     """Fill the workspace's partial slots and zero page with 0xFF bytes (NaN as
     fp32), keeping the first 256 bytes (error word, zeros): a piece the merge
