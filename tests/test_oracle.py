@@ -85,6 +85,36 @@ def test_constant_keys_give_mean_of_values():
         np.testing.assert_allclose(out[b], np.broadcast_to(rows.mean(axis=0), out[b].shape), atol=1e-6)
 
 
+@pytest.mark.parametrize("shape", ["gqa", "gqa_causal_q4", "mla"])
+def test_scale_zero_gives_mean_of_visible_values(shape):
+    # scale 0: every visible score is 0, p = bf16(e^0) = 1 exactly, so row r of
+    # query token i is the plain mean of the V rows it sees. With a causal
+    # multi-token query, token i sees ctx - (q_len - 1 - i) tokens: an
+    # off-by-one in that window, or a wrong kv head (h // g), fails here.
+    lens = [5, 37, 50]
+    if shape == "gqa":
+        case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=32, block_size=16, context_lens=lens,
+                                seed=31, scale=0.0)
+    elif shape == "gqa_causal_q4":
+        case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=32, block_size=16, context_lens=lens,
+                                seed=32, scale=0.0, q_len=4, causal=True)
+    else:
+        case = make_custom_case(batch=3, num_heads=4, kv_heads=1, head_dim=64, head_dim_v=48, block_size=16,
+                                context_lens=lens, seed=33, scale=0.0, mla=True)
+    c = case.config
+    out = oracle_numpy(case)
+    v_all = (case.key_cache.float().numpy()[..., : c.head_dim_v] if c.mla else case.value_cache.float().numpy())
+    g = c.num_heads // c.kv_heads
+    for b, n in enumerate(lens):
+        rows = np.concatenate([v_all[int(case.block_table[b, j])] for j in range((n + 15) // 16)])[:n]
+        for i in range(c.q_len):
+            seen = n - (c.q_len - 1 - i) if c.causal else n
+            for h in range(c.num_heads):
+                want = rows[:seen, h // g].astype(np.float64).mean(axis=0)
+                got = out[b, i, h] if c.q_len > 1 else out[b, h]
+                np.testing.assert_allclose(got, want, atol=1e-6, err_msg=f"{shape} b{b} token{i} head{h}")
+
+
 def test_one_hot_scores_select_one_value():
     case = make_custom_case(batch=1, num_heads=2, kv_heads=1, head_dim=16, block_size=16, context_lens=[40], seed=9,
                             scale=1.0)
