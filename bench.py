@@ -49,7 +49,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample duration")
-    p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="0 = every CPU this process may use, capped at OMP_NUM_THREADS when set (the box's share)")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                    help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     p.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -100,8 +101,32 @@ def api_time(case, out, cfg, steps: int, warmup: int) -> dict | None:
                     "reference QK/SF/PV/UP callable"}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads(requested: int) -> tuple[int, int]:
+    """(threads to use, CPUs this process may run on). The GPU box grants one
+    GPU's share of its host, 16 CPUs, and says so in OMP_NUM_THREADS; the
+    baseline uses every CPU of that share (all of nproc where no share is set)."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    if requested > 0:
+        return requested, nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(nproc, share) if share > 0 else nproc), nproc
+
+
 def cpu_baseline(case, args) -> dict | None:
-    """Time the C restatement of the reference kernels on this host (kind "port")."""
+    """Time the C restatement of the reference kernels on this host (kind "port"):
+    2 warm-up steps, then at least 10 timed steps and at least --cpu-seconds of
+    work; the median step time is the figure."""
     try:
         import numpy as np
 
@@ -109,7 +134,7 @@ def cpu_baseline(case, args) -> dict | None:
         from simpler_amd.workloads import algorithmic_bytes
     except Exception as e:  # pragma: no cover - reported, never fatal
         return {"value": None, "error": f"oracle unavailable: {e}"}
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads, nproc = cpu_threads(args.cpu_threads)
     c = case.config
 
     def bits(t):
@@ -124,25 +149,37 @@ def cpu_baseline(case, args) -> dict | None:
     v = None if c.mla else bits(vc)
     bt, cl = case.block_table.numpy(), case.context_lens.numpy()
     out = np.zeros((c.batch, c.q_len, c.num_heads, c.head_dim_v), dtype=np.float32)
-    runs, t0 = 0, time.perf_counter()
-    while True:
+
+    def step():
         pa_oracle_c.decode(q, k, v, bt, cl, case.scale, causal=c.causal, v_dim=c.head_dim_v if c.mla else None,
                            n_threads=threads, out=out)
-        runs += 1
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or runs >= 1000:
-            break
-    per_step = el / runs
+
+    for _ in range(2):
+        step()
+    times, t0 = [], time.perf_counter()
+    while len(times) < 10 or (time.perf_counter() - t0 < args.cpu_seconds and len(times) < 1000):
+        s0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - s0)
+    el = time.perf_counter() - t0
+    times.sort()
+    median = times[len(times) // 2] if len(times) % 2 else 0.5 * (times[len(times) // 2 - 1] + times[len(times) // 2])
     nbytes = algorithmic_bytes(case, out_bytes=2 if args.out_dtype == "bf16" else 4)
     return {
-        "value": round(nbytes / per_step / 1e9, 3),
+        "value": round(nbytes / median / 1e9, 3),
         "unit": "GB/s",
-        "us_per_step": round(per_step * 1e6, 1),
+        "us_per_step": round(median * 1e6, 1),
+        "median_us": round(median * 1e6, 1),
+        "mean_us": round(sum(times) / len(times) * 1e6, 1),
+        "runs": len(times),
+        "warmup": 2,
         "cores": threads,
+        "nproc": nproc,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"full {c.name} decode step (all {c.batch}x{c.kv_heads} sequence/kv-head items), "
-                  f"{runs} repetitions in {el:.1f} s, C restatement of the reference QK/SF/PV/UP kernels "
-                  f"(oracle/pa_oracle.c), {threads} pthreads"
+        "sample": f"full {c.name} decode step (all {c.batch}x{c.kv_heads} sequence/kv-head items), median of "
+                  f"{len(times)} steps after 2 warm-ups ({el:.1f} s), C restatement of the reference QK/SF/PV/UP "
+                  f"kernels (oracle/pa_oracle.c), {threads} pthreads on {nproc} CPUs available"
                   + ("; fp8 caches given to it dequantised (bf16-exact), bytes counted as fp8" if case.fp8 else ""),
     }
 

@@ -33,6 +33,8 @@ enum {
     SIMPLER_HIP_ERR_WORKSPACE = -4,   /* workspace missing or too small         */
     SIMPLER_HIP_ERR_LAUNCH = -5,      /* HIP launch / runtime failure           */
     SIMPLER_HIP_ERR_BAD_BLOCK = -6,   /* block_table entry outside the KV pool  */
+    SIMPLER_HIP_ERR_BAD_LENGTH = -7,  /* context_lens entry outside [0, max_blocks_per_seq*block_size],
+                                         or (causal) shorter than q_len           */
 };
 
 /* Output dtypes, using the reference's DataType codes
@@ -124,7 +126,10 @@ int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *args, void *worksp
 
 /* After the stream has completed: returns SIMPLER_HIP_ERR_BAD_BLOCK if any
  * launch since the last check met an out-of-pool block_table entry (such
- * blocks are skipped, never dereferenced), else 0. Clears the flag. Synchronous. */
+ * blocks are skipped, never dereferenced), else SIMPLER_HIP_ERR_BAD_LENGTH if
+ * one read a context_lens entry below 0, above max_blocks_per_seq*block_size,
+ * or (causal) below q_len (the kernels then use the length clamped into
+ * [0, max_blocks_per_seq*block_size]), else 0. Clears the flags. Synchronous. */
 int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream);
 
 /* Measurement helpers: name of the main kernel the args select, and the

@@ -158,6 +158,23 @@ void *simpler_hip_context_stream(DeviceContextHandle ctx);
 enum { SIMPLER_HIP_EXEC_FUSED = 0, SIMPLER_HIP_EXEC_TASK_GRAPH = 1, SIMPLER_HIP_EXEC_TASK_GRAPH_HIPGRAPH = 2 };
 int simpler_hip_set_execution(DeviceContextHandle ctx, int32_t execution);
 
+/* simpler_hip extension (no reference counterpart): which paged-attention
+ * callable family registration id `callable_id` matched, or -1 (not
+ * registered, or not paged attention). CHAIN: the per-block QK/SF/PV/UP
+ * chain (examples/a2a3/tensormap_and_ringbuffer/paged_attention and its
+ * manual_scope / ringbuffer / batch / multi_round variants); UNROLL: the
+ * grouped split-K chain whose QK and PV take three inputs (paged_attention_unroll,
+ * *_unroll_manual_scope, *_unroll_4dims); SPMD: the cooperative AIC/AIV task
+ * (spmd_paged_attention); NATIVE: the callable named
+ * simpler_hip_paged_attention_decode. All run on the fused decode kernel. */
+enum {
+    SIMPLER_HIP_PA_CHAIN = 0,
+    SIMPLER_HIP_PA_UNROLL = 1,
+    SIMPLER_HIP_PA_SPMD = 2,
+    SIMPLER_HIP_PA_NATIVE = 3
+};
+int simpler_hip_callable_family(DeviceContextHandle ctx, int32_t callable_id);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

@@ -78,6 +78,9 @@ typedef enum SimplerHipTensorArgType {
  *                   <- .../vector_example/kernels/aiv/kernel_add_scalar.cpp
  *   VEC_MUL         a, b, c (out), f32: c = a * b
  *                   <- .../vector_example/kernels/aiv/kernel_mul.cpp
+ *   ZERO_FILL       dst [M,D] f32 or bf16 (out): dst = 0. No reference counterpart: the
+ *                   paged-attention orchestration writes it for an empty context, whose
+ *                   output the fused decode defines as zeros.
  * Matrix operands need unit stride in their last dimension. */
 typedef enum SimplerHipIncoreKernel {
     SIMPLER_HIP_K_QK_MATMUL = 0,
@@ -86,7 +89,8 @@ typedef enum SimplerHipIncoreKernel {
     SIMPLER_HIP_K_ONLINE_UPDATE = 3,
     SIMPLER_HIP_K_VEC_ADD = 16,
     SIMPLER_HIP_K_VEC_ADD_SCALAR = 17,
-    SIMPLER_HIP_K_VEC_MUL = 18
+    SIMPLER_HIP_K_VEC_MUL = 18,
+    SIMPLER_HIP_K_ZERO_FILL = 19
 } SimplerHipIncoreKernel;
 
 typedef enum SimplerHipTaskGraphMode {

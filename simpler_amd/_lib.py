@@ -161,6 +161,7 @@ SIGNATURES: dict[str, tuple] = {
     "comm_destroy": (_I, [_VP]),
     "simpler_hip_context_stream": (_VP, [_VP]),
     "simpler_hip_set_execution": (_I, [_VP, _I32]),
+    "simpler_hip_callable_family": (_I, [_VP, _I32]),
     # include/simpler_hip/task_graph.h (tensor arrays are SimplerChipTensor[], passed as void*)
     "simpler_hip_tg_create": (_VP, [_I32, _VP]),
     "simpler_hip_tg_destroy": (None, [_VP]),

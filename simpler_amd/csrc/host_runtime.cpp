@@ -61,8 +61,23 @@ void logf(const char *fmt, ...) {
 
 enum CallableKind { kNone = 0, kPagedAttention = 1, kVectorExample = 2 };
 
+// Which of the reference's paged-attention callables a registration matched.
+// All of them take the same orchestration arguments (query, key_cache,
+// value_cache, block_table, context_lens, out; scalar 0 = scale) and compute
+// the same golden, so the fused kernel serves every one; only kPaChain's
+// orchestration is also available on the task-graph backend.
+enum PaFamily {
+    kPaChain = SIMPLER_HIP_PA_CHAIN,    // QK/SF/PV/UP per block: paged_attention, *_manual_scope, *_ringbuffer,
+                                        // batch_*, multi_round_*
+    kPaUnroll = SIMPLER_HIP_PA_UNROLL,  // grouped QK/SF/PV over <= 64 blocks + UP: paged_attention_unroll,
+                                        // *_unroll_manual_scope, *_unroll_4dims
+    kPaSpmd = SIMPLER_HIP_PA_SPMD,      // one cooperative AIC/AIV mix task: spmd_paged_attention
+    kPaNative = SIMPLER_HIP_PA_NATIVE,  // the name simpler_hip_paged_attention_decode
+};
+
 struct Callable {
     CallableKind kind = kNone;
+    int32_t family = kPaChain;
     int32_t sig[SIMPLER_CHIP_MAX_TENSOR_ARGS] = {};
     int32_t sig_count = 0;
 };
@@ -128,6 +143,30 @@ const int32_t kSfSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_OUT, SIMPLER_ARG_OUT, SIMP
 const int32_t kPvSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_OUT};
 const int32_t kUpSig[] = {SIMPLER_ARG_IN,    SIMPLER_ARG_IN,    SIMPLER_ARG_IN,   SIMPLER_ARG_INOUT,
                           SIMPLER_ARG_INOUT, SIMPLER_ARG_INOUT, SIMPLER_ARG_INOUT};
+// Grouped split-K chain (tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll/
+// test_paged_attention_unroll.py:25-61, the same in paged_attention_unroll_4dims and
+// examples/.../paged_attention_unroll_manual_scope): QK and PV take a third input.
+const int32_t kQkUnrollSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_OUT};
+const int32_t kPvUnrollSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_OUT};
+// Cooperative AIC/AIV task (tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention/
+// test_spmd_paged_attention.py:28-54): func ids 0 and 1 share one 9-tensor payload.
+const int32_t kSpmdMixSig[] = {SIMPLER_ARG_IN,    SIMPLER_ARG_IN,  SIMPLER_ARG_IN,  SIMPLER_ARG_IN, SIMPLER_ARG_IN,
+                               SIMPLER_ARG_INOUT, SIMPLER_ARG_OUT, SIMPLER_ARG_OUT, SIMPLER_ARG_OUT};
+
+struct ChildSig {
+    const int32_t *sig;
+    int32_t n;
+};
+struct PaFamilySpec {
+    PaFamily family;
+    int32_t children;       // func ids 0 .. children-1, each exactly once
+    ChildSig by_fid[4];
+};
+const PaFamilySpec kPaFamilies[] = {
+    {kPaChain, 4, {{kQkSig, 3}, {kSfSig, 4}, {kPvSig, 3}, {kUpSig, 7}}},
+    {kPaUnroll, 4, {{kQkUnrollSig, 4}, {kSfSig, 4}, {kPvUnrollSig, 4}, {kUpSig, 7}}},
+    {kPaSpmd, 2, {{kSpmdMixSig, 9}, {kSpmdMixSig, 9}, {nullptr, 0}, {nullptr, 0}}},
+};
 
 bool sig_equals(const int32_t *a, int32_t na, const int32_t *b, int32_t nb) {
     if (na != nb) return false;
@@ -167,22 +206,36 @@ CallableKind classify(const uint8_t *blob, Callable &out) {
     memcpy(out.sig, h.signature_, sizeof(int32_t) * h.sig_count_);
     char name[SIMPLER_CALLABLE_FUNC_NAME_MAX + 1] = {};
     memcpy(name, h.func_name_, SIMPLER_CALLABLE_FUNC_NAME_MAX);
-    if (strcmp(name, kNativePaName) == 0 && h.sig_count_ >= kPaTensors) return kPagedAttention;
-    if (sig_equals(h.signature_, h.sig_count_, kVecOrchSig, 3) && h.child_count_ == 3) return classify_vector(h, blob);
-    if (!sig_equals(h.signature_, h.sig_count_, kOrchSig, 6) || h.child_count_ != 4) return kNone;
-    const uint8_t *storage = blob + SIMPLER_CHIP_CALLABLE_STORAGE_OFFSET;
-    bool seen[4] = {false, false, false, false};
-    for (int i = 0; i < 4; ++i) {
-        const int fid = h.child_func_ids_[i];
-        if (fid < 0 || fid > 3 || seen[fid]) return kNone;
-        seen[fid] = true;
-        SimplerCoreCallableHeader ch;
-        memcpy(&ch, storage + h.child_offsets_[i], sizeof(ch));
-        const int32_t *want = fid == 0 ? kQkSig : fid == 1 ? kSfSig : fid == 2 ? kPvSig : kUpSig;
-        const int32_t nwant = fid == 3 ? 7 : fid == 1 ? 4 : 3;
-        if (!sig_equals(ch.signature_, ch.sig_count_, want, nwant)) return kNone;
+    if (strcmp(name, kNativePaName) == 0 && h.sig_count_ >= kPaTensors) {
+        out.family = kPaNative;
+        return kPagedAttention;
     }
-    return kPagedAttention;
+    if (sig_equals(h.signature_, h.sig_count_, kVecOrchSig, 3) && h.child_count_ == 3) return classify_vector(h, blob);
+    if (!sig_equals(h.signature_, h.sig_count_, kOrchSig, 6)) return kNone;
+    // The paged-attention orchestrations: the children (in any order) must be
+    // exactly one family's func ids with that family's signatures.
+    const uint8_t *storage = blob + SIMPLER_CHIP_CALLABLE_STORAGE_OFFSET;
+    for (const PaFamilySpec &f : kPaFamilies) {
+        if (h.child_count_ != f.children) continue;
+        bool seen[4] = {false, false, false, false};
+        bool ok = true;
+        for (int i = 0; i < f.children && ok; ++i) {
+            const int fid = h.child_func_ids_[i];
+            if (fid < 0 || fid >= f.children || seen[fid]) {
+                ok = false;
+                break;
+            }
+            seen[fid] = true;
+            SimplerCoreCallableHeader ch;
+            memcpy(&ch, storage + h.child_offsets_[i], sizeof(ch));
+            ok = sig_equals(ch.signature_, ch.sig_count_, f.by_fid[fid].sig, f.by_fid[fid].n);
+        }
+        if (ok) {
+            out.family = f.family;
+            return kPagedAttention;
+        }
+    }
+    return kNone;
 }
 
 // --- argument decoding -----------------------------------------------------------
@@ -598,6 +651,12 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
                  "Dk == Dv, bf16 caches");
             rc = SIMPLER_HIP_ERR_UNSUPPORTED;
         }
+        if (rc == SIMPLER_HIP_OK && r->execution != SIMPLER_HIP_EXEC_FUSED && cb.family != kPaChain &&
+            cb.family != kPaNative) {
+            logf("the task-graph backend runs the per-block QK/SF/PV/UP orchestration only; the grouped and "
+                 "SPMD paged-attention callables run on the fused kernel");
+            rc = SIMPLER_HIP_ERR_UNSUPPORTED;
+        }
         r->scale_bits = a->scalars_[0];
     } else {
         r->n_tensors = kVecTensors;
@@ -784,6 +843,13 @@ int comm_barrier(CommHandle) { return PTO_RUNTIME_ERR_UNSUPPORTED; }
 int comm_destroy(CommHandle) { return PTO_RUNTIME_ERR_UNSUPPORTED; }
 
 void *simpler_hip_context_stream(DeviceContextHandle h) { return as_ctx(h) ? (void *)as_ctx(h)->stream : nullptr; }
+
+int simpler_hip_callable_family(DeviceContextHandle h, int32_t id) {
+    DeviceContext *c = as_ctx(h);
+    if (!c || id < 0 || id >= kMaxCallables) return -1;
+    std::lock_guard<std::mutex> lk(c->mu);
+    return c->callables[id].kind == kPagedAttention ? c->callables[id].family : -1;
+}
 
 int simpler_hip_set_execution(DeviceContextHandle h, int32_t execution) {
     DeviceContext *c = as_ctx(h);

@@ -225,6 +225,24 @@ __global__ void __launch_bounds__(256) tg_vector_kernel(const VecParams P) {
     }
 }
 
+// ---------------------------------------------------------------- zero fill
+
+struct FillParams {
+    char *base;
+    int64_t ld_bytes;   // row stride in bytes
+    int64_t row_bytes;  // bytes per row (a multiple of 2)
+    int32_t rows;
+};
+
+__global__ void __launch_bounds__(256) tg_zero_fill_kernel(const FillParams P) {
+    const int64_t halves = P.row_bytes / 2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)P.rows * halves;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / halves, c = i - r * halves;
+        reinterpret_cast<uint16_t *>(P.base + r * P.ld_bytes)[c] = 0;
+    }
+}
+
 // ---------------------------------------------------------------- host side
 
 int fail(char *why, size_t len, int code, const char *fmt, ...) __attribute__((format(printf, 4, 5)));
@@ -330,6 +348,7 @@ int incore_tensor_count(int32_t kernel) {
         case SIMPLER_HIP_K_VEC_ADD: return 3;
         case SIMPLER_HIP_K_VEC_ADD_SCALAR: return 2;
         case SIMPLER_HIP_K_VEC_MUL: return 3;
+        case SIMPLER_HIP_K_ZERO_FILL: return 1;
         default: return -1;
     }
 }
@@ -463,6 +482,18 @@ int make_incore_launch(int32_t kernel, const SimplerChipTensor *t, int32_t nt, c
             const uint64_t blocks = (n + 255) / 256;
             set_launch(out, reinterpret_cast<const void *>(tg_vector_kernel), (unsigned)(blocks < 2048 ? blocks : 2048),
                        256, P);
+            return SIMPLER_HIP_OK;
+        }
+        case SIMPLER_HIP_K_ZERO_FILL: {
+            Mat d;
+            if ((t[0].dtype != SIMPLER_DT_FLOAT32 && t[0].dtype != SIMPLER_DT_BFLOAT16) || !as_matrix(t[0], d))
+                return fail(why, wl, SIMPLER_HIP_ERR_INVALID, "zero_fill: dst must be an fp32 or bf16 matrix");
+            const int64_t esz = (int64_t)simpler_dtype_size(t[0].dtype);
+            FillParams P{d.base, d.ld * esz, d.cols * esz, (int32_t)d.rows};
+            const int64_t n = d.rows * d.cols * esz / 2;
+            const int64_t blocks = (n + 255) / 256;
+            set_launch(out, reinterpret_cast<const void *>(tg_zero_fill_kernel),
+                       (unsigned)(blocks < 1024 ? blocks : 1024), 256, P);
             return SIMPLER_HIP_OK;
         }
         default: break;

@@ -109,6 +109,8 @@ uint64_t f32_bits(float f) {
 }
 
 constexpr int32_t FUNC_QK_MATMUL = 0, FUNC_SOFTMAX_PREPARE = 1, FUNC_PV_MATMUL = 2, FUNC_ONLINE_UPDATE = 3;
+// Not a reference func id: the zero output of an empty context (see below).
+constexpr int32_t FUNC_ZERO_FILL = 4;
 
 }  // namespace
 
@@ -143,6 +145,7 @@ int simpler_hip_tg_orchestrate_paged_attention(SimplerHipTaskGraph *g, const Sim
         return SIMPLER_HIP_ERR_INVALID;
     }
     for (int32_t f = 0; f < 4; ++f) simpler_hip_tg_bind(g, f, f);  // FUNC_* ids equal the kernel codes
+    simpler_hip_tg_bind(g, FUNC_ZERO_FILL, SIMPLER_HIP_K_ZERO_FILL);
 
     const uint32_t q_tile = std::min<uint32_t>(num_heads, 128);  // :105
     const uint32_t q_loop = (num_heads + q_tile - 1) / q_tile;
@@ -188,6 +191,15 @@ int simpler_hip_tg_orchestrate_paged_attention(SimplerHipTaskGraph *g, const Sim
             const Submitted st = submit(g, -1, alloc);  // alloc_tensors (:160-163)
             if (st.task < 0) return (int)st.task;
             const SimplerChipTensor oi = st.out[0], li_update = st.out[1], mi_update = st.out[2];
+            if (bn_this_batch == 0) {
+                // An empty context submits no block task, so nothing would
+                // write these rows; the fused decode defines them as zeros and
+                // so does this path (the reference leaves them untouched).
+                Args fill;
+                fill.add_output_existing(out_view);
+                const Submitted zf = submit(g, FUNC_ZERO_FILL, fill);
+                if (zf.task < 0) return (int)zf.task;
+            }
 
             for (uint64_t bn = 0; bn < bn_this_batch; ++bn) {
                 simpler_hip_tg_scope_begin(g);

@@ -201,6 +201,27 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
     return (ctx_of(P, b) + P.block_size - 1) / P.block_size;
 }
 
+// Error word bits (workspace offset 0), read back by simpler_hip_pa_decode_check.
+constexpr unsigned kErrBadBlock = 1u;   // a block_table entry outside the pool (that block is skipped)
+constexpr unsigned kErrBadLength = 2u;  // a context_lens entry the kernels had to clamp
+
+// One wave of the grid (wave 0 of workgroup 0) checks every raw length: below
+// 0, above what the block-table row holds, or (causal) shorter than the query.
+// The kernels run such a sequence with its length clamped by ctx_of; the flag
+// turns that into an error for the caller, as the host-side table check does.
+__device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
+    if (blockIdx.x != 0 || threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const int64_t cap = (int64_t)P.max_blocks * P.block_size;
+    const int lo = P.causal ? P.q_len : 0;
+    bool bad = false;
+    for (int b = lane; b < P.batch; b += 64) {
+        const int len = P.context_lens[b];
+        bad |= len < lo || (int64_t)len > cap;
+    }
+    if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
+}
+
 // Work lists: the (tile, KV block) pairs of all batches form P.lanes lists of
 // equal length. List u holds, per batch, the tiles u*lt .. u*lt+lt-1 (lt =
 // tiles per batch / lanes), batch-major, then tile, then block; its
@@ -457,7 +478,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     auto compute_block = [&](const int blk, const int phys_b, const bool blk_bad, auto &kr, auto &vr, auto &vrw,
                              auto &&before_qk, auto &&after_qk) {
         const bool first = (blk == blk_begin);
-        if (blk_bad && lane == 0) atomicOr(P.error_flag, 1u);
+        if (blk_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
         float sc = P.scale, vs = 1.f;
         if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform, scalar loads)
             typedef const __attribute__((address_space(4))) float *cfloat_p;
@@ -754,6 +775,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     // single-tile bf16 workers with 128-dim heads stage K through LDS
     constexpr bool KLDS = MAXW == 1 && !KV8 && DK == 128;
     __shared__ __attribute__((aligned(16))) char klds[KLDS ? BS * 256 : 16];
+    flag_bad_lengths(P);
     const int w = blockIdx.x;
     const int wave = MAXW == 1 ? 0 : (int)(threadIdx.x >> 6);
     const int tpb = lane_tiles(P);
@@ -1377,7 +1399,7 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         bool bad_next = false;
         if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
         if (blk + 2 < blk_end) prefetch(blk + 2);
-        if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, 1u);
+        if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, kErrBadBlock);
         compute(even ? smem0 : smem1, blk, bad_cur);
         bad_cur = bad_next;
     }
@@ -1432,6 +1454,7 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
     // P^T of every wave's rows and per-row factors, handed between the waves
     __shared__ __attribute__((aligned(16))) char pexch[MlaExchange<BS>::kBytes];
+    flag_bad_lengths(P);
     const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
     int slice = 0, rgrp = 0;
     mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
@@ -1757,10 +1780,32 @@ extern "C" size_t simpler_hip_pa_decode_workspace_size(const SimplerHipPaDecodeA
     return make_plan(args, k).total;
 }
 
+namespace simpler_hip {
+namespace {
+// Zeroes [p, p + bytes): 16-byte stores over the aligned body, byte stores for
+// the tail. A kernel rather than hipMemsetAsync, so that callers may enqueue it
+// inside a HIP graph capture (memset nodes are avoided in captured work).
+__global__ void __launch_bounds__(256) zero_fill_kernel(char *p, size_t bytes) {
+    const size_t n16 = bytes / 16;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        reinterpret_cast<u32x4_t *>(p)[i] = (u32x4_t){0u, 0u, 0u, 0u};
+    if (blockIdx.x == 0 && threadIdx.x < bytes % 16) p[n16 * 16 + threadIdx.x] = 0;
+}
+}  // namespace
+
+int zero_fill(void *p, size_t bytes, void *stream) {
+    if (bytes == 0) return SIMPLER_HIP_OK;
+    const size_t units = (bytes + 15) / 16;
+    const unsigned grid = (unsigned)std::min<size_t>((units + 255) / 256, 2048);
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (char *)p, bytes);
+    return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
+}
+}  // namespace simpler_hip
+
 extern "C" int simpler_hip_pa_decode_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
     if (!workspace) return SIMPLER_HIP_ERR_WORKSPACE;
-    if (hipMemsetAsync(workspace, 0, workspace_bytes, (hipStream_t)stream) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
-    return SIMPLER_HIP_OK;
+    return simpler_hip::zero_fill(workspace, workspace_bytes, stream);
 }
 
 extern "C" int simpler_hip_pa_decode_plan(const SimplerHipPaDecodeArgs *args, int32_t *num_workers) {
@@ -1871,5 +1916,5 @@ extern "C" int simpler_hip_pa_decode_check(void *workspace, size_t workspace_byt
     if (flag == 0) return SIMPLER_HIP_OK;
     const unsigned zero = 0;
     if (hipMemcpy(workspace, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
-    return SIMPLER_HIP_ERR_BAD_BLOCK;
+    return (flag & kErrBadBlock) ? SIMPLER_HIP_ERR_BAD_BLOCK : SIMPLER_HIP_ERR_BAD_LENGTH;
 }

@@ -7,6 +7,10 @@
 
 namespace simpler_hip {
 
+// Enqueues a kernel that zeroes `bytes` bytes at device pointer `p` on
+// `stream` (no memset node, so it may run under graph capture).
+int zero_fill(void *p, size_t bytes, void *stream);
+
 // simpler_hip_pa_decode with the merge kernel also storing the final error
 // word into *err_mirror, host-visible pinned memory, so a caller that waits on
 // the stream can read it without a device-to-host copy. Returns what

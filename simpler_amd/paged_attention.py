@@ -35,6 +35,7 @@ _ERRORS = {
     -4: "workspace missing or too small",
     -5: "HIP launch failure",
     -6: "block_table entry outside the KV pool",
+    -7: "context_lens entry outside [0, max_blocks_per_seq * block_size] (or, causal, shorter than q_len)",
 }
 
 
@@ -45,27 +46,42 @@ class PagedAttentionError(RuntimeError):
 
 
 class _Workspace:
-    """Grow-only per-device workspace (error word + per-worker partial slots)."""
+    """Workspace (error word + per-worker partial slots) per (device, stream).
+
+    Launches on one stream run in order, so they may share a buffer; launches
+    on different streams get different buffers, so concurrent decodes never
+    share partial slots. A buffer only grows (to at least twice its old size),
+    and a buffer it replaces is kept alive rather than freed: a HIP graph
+    captured earlier holds its address and keeps using it on replay. The
+    initialisation is a kernel, not a memset, so a buffer may also be created
+    inside a graph capture (the capture then records its zeroing, which runs
+    again on every replay). Graphs captured on one stream share that stream's
+    buffer: do not replay them concurrently on different streams.
+    """
 
     def __init__(self) -> None:
         self._mu = threading.Lock()
-        self._buf: dict[int, torch.Tensor] = {}
+        self._buf: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int, stream: int) -> torch.Tensor:
         idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, int(stream or 0))
         with self._mu:
-            buf = self._buf.get(idx)
+            buf = self._buf.get(key)
             if buf is None or buf.numel() < nbytes:
-                if buf is not None:  # launches on any stream may still use the old buffer
-                    torch.cuda.synchronize(device)
-                size = max(nbytes, 1 << 20)
-                buf = torch.empty(size + 256, dtype=torch.uint8, device=device)
-                off = (-buf.data_ptr()) % 256
-                buf = buf[off : off + size]
-                rc = _lib.lib().simpler_hip_pa_decode_workspace_init(buf.data_ptr(), buf.numel(), stream)
+                size = max(nbytes, 1 << 20, 2 * buf.numel() if buf is not None else 0)
+                with torch.cuda.device(idx):
+                    raw = torch.empty(size + 256, dtype=torch.uint8, device=torch.device("cuda", idx))
+                off = (-raw.data_ptr()) % 256
+                new = raw[off : off + size]
+                rc = _lib.lib().simpler_hip_pa_decode_workspace_init(new.data_ptr(), new.numel(), stream)
                 if rc != 0:
                     raise PagedAttentionError(rc, "simpler_hip_pa_decode_workspace_init")
-                self._buf[idx] = buf
+                if buf is not None:
+                    self._retired.append(buf)  # a captured graph may still use it
+                self._buf[key] = new
+                buf = new
             return buf
 
 
@@ -222,7 +238,8 @@ def paged_attention_decode(
 
 
 def check_errors(device: torch.device | None = None) -> None:
-    """Synchronise and raise if a launch met an out-of-pool block_table entry."""
+    """Synchronise and raise if a launch on the current stream met an out-of-pool
+    block_table entry (rc -6) or a context length it had to clamp (rc -7)."""
     device = device or torch.device("cuda", torch.cuda.current_device())
     stream = torch.cuda.current_stream(device).cuda_stream
     ws = _WORKSPACE.get(device, 1, stream)
@@ -287,3 +304,70 @@ def reference_chain_callable(orch_binary: bytes = b"", incore_binaries: dict[int
 def native_callable() -> ChipCallable:
     """A callable that names the fused decode directly."""
     return ChipCallable.build(signature=ORCH_SIGNATURE, func_name=NATIVE_CALLABLE_NAME, binary=b"", children=[])
+
+
+# Incore signatures of the grouped split-K ("unroll") chain: QK and PV take a
+# third input (tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll/
+# test_paged_attention_unroll.py:25-61).
+UNROLL_INCORE_SIGNATURES = {
+    0: [D.IN, D.IN, D.IN, D.OUT],  # QK   grouped aic_qk_matmul
+    1: [D.IN, D.OUT, D.OUT, D.OUT],  # SF   two-pass aiv_softmax_prepare
+    2: [D.IN, D.IN, D.IN, D.OUT],  # PV   grouped aic_pv_matmul
+    3: [D.IN, D.IN, D.IN, D.INOUT, D.INOUT, D.INOUT, D.INOUT],  # UP
+}
+# The cooperative AIC/AIV task of spmd_paged_attention: both halves declare the
+# shared 9-tensor payload (tests/st/a2a3/tensormap_and_ringbuffer/
+# spmd_paged_attention/test_spmd_paged_attention.py:28-54).
+SPMD_INCORE_SIGNATURES = {
+    0: [D.IN, D.IN, D.IN, D.IN, D.IN, D.INOUT, D.OUT, D.OUT, D.OUT],  # PA_AIC
+    1: [D.IN, D.IN, D.IN, D.IN, D.IN, D.INOUT, D.OUT, D.OUT, D.OUT],  # PA_AIV
+}
+
+# Every paged-attention CALLABLE the reference defines, as (incore signatures,
+# child order by func id). All share the orchestration signature and the
+# 7-argument contract, so each registers and runs on the fused kernel.
+REFERENCE_CALLABLES = {
+    # examples/a2a3/tensormap_and_ringbuffer/paged_attention/test_paged_attention.py:25-61
+    "paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # examples/a2a3/tensormap_and_ringbuffer/paged_attention_manual_scope/test_paged_attention_manual_scope.py:25-61
+    "paged_attention_manual_scope": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # examples/a2a3/tensormap_and_ringbuffer/paged_attention_ringbuffer/test_paged_attention_ringbuffer.py:34-66
+    # (children listed as func ids 0, 2, 1, 3)
+    "paged_attention_ringbuffer": (INCORE_SIGNATURES, [0, 2, 1, 3]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/batch_paged_attention/test_batch_paged_attention.py:25-61
+    "batch_paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/multi_round_paged_attention/test_multi_round_paged_attention.py:30-66
+    "multi_round_paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll/test_paged_attention_unroll.py:25-61
+    "paged_attention_unroll": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # examples/a2a3/tensormap_and_ringbuffer/paged_attention_unroll_manual_scope/
+    # test_paged_attention_unroll_manual_scope.py:25-61
+    "paged_attention_unroll_manual_scope": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll_4dims/test_paged_attention_unroll_4dims.py:32-64
+    # (query and out as [B, 1, H, D], :120-122)
+    "paged_attention_unroll_4dims": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention/test_spmd_paged_attention.py:28-54
+    "spmd_paged_attention": (SPMD_INCORE_SIGNATURES, [0, 1]),
+}
+
+# The family simpler_hip_callable_family reports for each
+REFERENCE_FAMILIES = {
+    name: ("unroll" if sigs is UNROLL_INCORE_SIGNATURES else "spmd" if sigs is SPMD_INCORE_SIGNATURES else "chain")
+    for name, (sigs, _) in REFERENCE_CALLABLES.items()
+}
+
+
+def reference_callable(name: str, orch_binary: bytes = b"",
+                       incore_binaries: dict[int, bytes] | None = None) -> ChipCallable:
+    """The reference's CALLABLE ``name`` (a key of ``REFERENCE_CALLABLES``), with
+    its incore signatures and child order. Binaries are carried, not executed."""
+    sigs, order = REFERENCE_CALLABLES[name]
+    incore_binaries = incore_binaries or {}
+    children = [(fid, CoreCallable.build(signature=sigs[fid], binary=incore_binaries.get(fid, b""))) for fid in order]
+    return ChipCallable.build(
+        signature=ORCH_SIGNATURE,
+        func_name="aicpu_orchestration_entry",
+        binary=orch_binary,
+        children=children,
+        config_name="aicpu_orchestration_config",
+    )

@@ -50,6 +50,7 @@ class IncoreKernel(IntEnum):
     VEC_ADD = 16
     VEC_ADD_SCALAR = 17
     VEC_MUL = 18
+    ZERO_FILL = 19
 
 
 _MODES = {"eager": 0, "graph": 1, "record": 2}

@@ -538,6 +538,17 @@ class ChipWorker:
             self._handles[hid] = slot
             return CallableHandle(hid, slot)
 
+    PA_FAMILIES = {0: "chain", 1: "unroll", 2: "spmd", 3: "native"}
+
+    def callable_family(self, handle: CallableHandle) -> str | None:
+        """Which paged-attention callable family a registration matched
+        (``simpler_hip_callable_family``): ``"chain"``, ``"unroll"``, ``"spmd"``,
+        ``"native"``, or ``None`` for a callable that is not paged attention."""
+        slot = self._handles.get(handle._handle_id)
+        if slot is None:
+            raise KeyError("unknown callable handle")
+        return self.PA_FAMILIES.get(int(self._lib.simpler_hip_callable_family(self._require(), slot)))
+
     def unregister_callable(self, handle: CallableHandle) -> None:
         ctx = self._require()
         with self._lock:

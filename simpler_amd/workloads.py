@@ -210,6 +210,45 @@ def make_custom_case(*, batch: int, num_heads: int, kv_heads: int, head_dim: int
                       scale if scale is not None else 1.0 / math.sqrt(head_dim))
 
 
+def make_reference_case(params: dict, seed: int) -> DecodeCase:
+    """Inputs drawn the way the reference's scene tests draw them
+    (``simpler_setup/goldens/paged_attention.py:30-88``), seeded:
+
+    * ``context_lens``: ``context_len`` for every sequence, or
+      ``context_lens_list`` cycled to the batch;
+    * ``block_table [B, max_model_len // block_size]``: uniform block ids in
+      ``[0, B * ceil(max_len / block_size))``, drawn with replacement (sequences
+      may share blocks; entries past a sequence's length are never read);
+    * query, key ~ U(-0.5, 0.5), value ~ U(-1, 1), rounded to ``dtype``
+      (bfloat16 here); scale 1.0, as the reference's inputs and golden use.
+
+    ``params`` takes the reference's case keys (``batch``, ``num_heads``,
+    ``kv_head_num``, ``head_dim``, ``block_size``, ``context_len``,
+    ``max_model_len``, optional ``context_lens_list``)."""
+    batch, hq, hkv = params["batch"], params["num_heads"], params["kv_head_num"]
+    d, bs = params["head_dim"], params["block_size"]
+    gen = torch.Generator("cpu").manual_seed(seed)
+    lst = params.get("context_lens_list")
+    if lst is not None:
+        vals = (list(lst) * ((batch + len(lst) - 1) // len(lst)))[:batch]
+        lens = torch.tensor(vals, dtype=torch.int32)
+    else:
+        lens = torch.full((batch,), params["context_len"], dtype=torch.int32)
+    max_blocks = params["max_model_len"] // bs
+    total = batch * ((int(lens.max()) + bs - 1) // bs)
+    table = torch.randint(0, max(total, 1), (batch, max_blocks), generator=gen, dtype=torch.int32)
+
+    def uni(shape, lo, hi):
+        return (torch.rand(shape, generator=gen, dtype=torch.float32) * (hi - lo) + lo).to(torch.bfloat16)
+
+    query = uni((batch, hq, d), -0.5, 0.5)
+    key = uni((total, bs, hkv, d), -0.5, 0.5)
+    value = uni((total, bs, hkv, d), -1.0, 1.0)
+    cfg = DecodeConfig("reference", -1, batch, hq, hkv, d, d, bs, int(lens.min()), int(lens.max()),
+                       max_blocks=max_blocks, out_dtype=torch.float32)
+    return DecodeCase(cfg, seed, query, key, value, table, lens, 1.0)
+
+
 # ---------------------------------------------------------------------------
 # Roofline accounting
 # ---------------------------------------------------------------------------

@@ -99,20 +99,63 @@ def test_callable_byte_layout():
     assert first_child % 64 == 0 and first_child >= 4
 
 
-def test_register_recognises_the_reference_chain_only():
+def test_register_recognises_the_reference_pa_callables_only():
     lib = _lib.lib()
     ctx = lib.create_device_context()
     try:
         assert lib.simpler_register_callable(ctx, 0, pa.reference_chain_callable().address()) == 0
+        assert lib.simpler_hip_callable_family(ctx, 0) == 0
         assert lib.simpler_register_callable(ctx, 1, pa.native_callable().address()) == 0
+        assert lib.simpler_hip_callable_family(ctx, 1) == 3
         other = ChipCallable.build(signature=[ArgDirection.IN], func_name="vector_add", binary=b"",
                                    children=[(0, CoreCallable.build([ArgDirection.IN]))])
         assert lib.simpler_register_callable(ctx, 2, other.address()) == -2
+        assert lib.simpler_hip_callable_family(ctx, 2) == -1
         # same orchestration signature but a different incore chain is not the PA chain
         wrong = ChipCallable.build(signature=pa.ORCH_SIGNATURE, func_name="aicpu_orchestration_entry", binary=b"",
                                    children=[(i, CoreCallable.build([ArgDirection.IN])) for i in range(4)])
         assert lib.simpler_register_callable(ctx, 3, wrong.address()) == -2
         assert lib.simpler_register_callable(ctx, 64, pa.native_callable().address()) == -1
+    finally:
+        lib.destroy_device_context(ctx)
+
+
+@pytest.mark.parametrize("name", sorted(pa.REFERENCE_CALLABLES))
+def test_every_reference_pa_callable_registers_with_its_family(name):
+    """Each paged-attention CALLABLE the reference defines (chain, grouped
+    "unroll", SPMD mix) registers with 0 and is classified into its family."""
+    lib = _lib.lib()
+    ctx = lib.create_device_context()
+    try:
+        assert lib.simpler_register_callable(ctx, 5, pa.reference_callable(name).address()) == 0
+        fam = lib.simpler_hip_callable_family(ctx, 5)
+        assert {0: "chain", 1: "unroll", 2: "spmd"}[fam] == pa.REFERENCE_FAMILIES[name]
+    finally:
+        lib.destroy_device_context(ctx)
+
+
+def test_register_rejects_mixed_or_incomplete_families():
+    """A chain whose children mix the two families' QK/PV signatures, repeat a
+    func id, or miss one is not any reference callable."""
+    lib = _lib.lib()
+    D = ArgDirection
+
+    def build(children):
+        return ChipCallable.build(signature=pa.ORCH_SIGNATURE, func_name="aicpu_orchestration_entry", binary=b"",
+                                  children=[(fid, CoreCallable.build(sig)) for fid, sig in children])
+
+    chain, unroll, spmd = pa.INCORE_SIGNATURES, pa.UNROLL_INCORE_SIGNATURES, pa.SPMD_INCORE_SIGNATURES
+    bad = [
+        [(0, unroll[0]), (1, chain[1]), (2, chain[2]), (3, chain[3])],  # unroll QK with chain PV
+        [(0, chain[0]), (1, chain[1]), (1, chain[1]), (3, chain[3])],   # func id 1 twice, 2 missing
+        [(0, chain[0]), (1, chain[1]), (2, chain[2])],                  # UP missing
+        [(0, spmd[0])],                                                 # half of the SPMD mix
+        [(0, spmd[0]), (1, [D.IN] * 9)],                                # wrong AIV payload
+    ]
+    ctx = lib.create_device_context()
+    try:
+        for i, children in enumerate(bad):
+            assert lib.simpler_register_callable(ctx, i, build(children).address()) == -2, i
     finally:
         lib.destroy_device_context(ctx)
 

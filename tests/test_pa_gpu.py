@@ -353,10 +353,12 @@ def test_decode_replays_from_a_hip_graph(shape, device):
         pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out,
                                   case.scale, causal=case.config.causal)
 
-    decode()  # sizes and zeroes the workspace outside the capture
+    side = torch.cuda.Stream(device)
+    with torch.cuda.stream(side):
+        decode()  # sizes and zeroes the capture stream's workspace outside the capture
     torch.cuda.synchronize(device)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         decode()
     torch.cuda.synchronize(device)
     expected = []
@@ -379,7 +381,7 @@ def _poison_workspace(device):
     fp32), keeping the first 256 bytes (error word, zeros): a piece the merge
     reads but no segment wrote turns the output into NaN."""
     torch.cuda.synchronize(device)
-    buf = pa._WORKSPACE._buf[device.index or 0]
+    buf = pa._WORKSPACE._buf[(device.index or 0, torch.cuda.current_stream(device).cuda_stream)]
     buf[256:].fill_(255)
     torch.cuda.synchronize(device)
 
@@ -420,3 +422,80 @@ def test_many_short_tiles(workers, device):
     got = run_gpu(case, device, num_workers=workers)
     assert np.all(got[3] == 0)
     assert_close(got, oracle_numpy(case), what=f"16640 tiles w{workers}")
+
+
+def test_graph_keeps_its_workspace_when_the_stream_grows_one(device):
+    """A graph captured on a stream keeps using the workspace it captured after
+    an eager call on that stream needs a larger one (the old buffer is retired,
+    not freed). The first capture also creates the stream's workspace inside the
+    capture (its zeroing is a kernel, recorded in the graph). Replays alternate
+    with eager work and each must match the oracle."""
+    print("[case] graph replay after workspace growth", flush=True)
+    small = make_custom_case(batch=2, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                             context_lens=[300, 1000], seed=941)
+    big = make_case("cfg3_long", batch_override=2)
+    ds, db = small.to(device), big.to(device)
+    ref_small, ref_big = oracle_numpy(small), oracle_c(big, n_threads=16)
+    out_s = torch.empty(small.out_shape(), dtype=torch.float32, device=device)
+    out_b = torch.empty(big.out_shape(), dtype=torch.float32, device=device)
+    side = torch.cuda.Stream(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        pa.paged_attention_decode(ds.query, ds.key_cache, ds.value_cache, ds.block_table, ds.context_lens, out_s,
+                                  small.scale, num_workers=64)
+    torch.cuda.synchronize(device)
+    for i in range(3):
+        with torch.cuda.stream(side):  # eager, same stream: grows the workspace on the first pass
+            pa.paged_attention_decode(db.query, db.key_cache, db.value_cache, db.block_table, db.context_lens,
+                                      out_b, big.scale, num_workers=4096 + 512 * i)
+        torch.cuda.synchronize(device)
+        assert_close(out_b.cpu().numpy(), ref_big, what=f"eager big {i}")
+        out_s.fill_(float("nan"))
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert_close(out_s.cpu().numpy(), ref_small, what=f"graph replay {i} after growth")
+    with torch.cuda.stream(side):
+        pa.check_errors(device)
+
+
+@pytest.mark.parametrize("bad", ["negative", "past_table", "causal_short"])
+def test_bad_device_lengths_are_reported_then_next_run_is_good(bad, device):
+    """Device-resident context_lens are only seen by the kernels: a length below
+    0, beyond what the block-table row holds, or (causal) shorter than q_len is
+    reported as SIMPLER_HIP_ERR_BAD_LENGTH (-7) by the check, and the next call
+    with good lengths on the same workspace matches the oracle."""
+    print(f"[case] bad device length: {bad}", flush=True)
+    causal = bad == "causal_short"
+    case = make_custom_case(batch=3, num_heads=16, kv_heads=2, head_dim=128, block_size=64,
+                            context_lens=[200, 64, 130], seed=950, q_len=4 if causal else 1, causal=causal)
+    d = case.to(device)
+    bad_lens = d.context_lens.clone()
+    bad_lens[1] = {"negative": -5, "past_table": case.block_table.shape[1] * 64 + 1, "causal_short": 2}[bad]
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, bad_lens, out, case.scale,
+                              causal=causal)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    pa.check_errors(device)  # cleared
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out, case.scale,
+                              causal=causal)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what=f"good run after {bad}")
+
+
+def test_mla_bad_device_length_is_reported(device):
+    case = _mla_case(heads=128, lens=[200, 70], seed=951)
+    d = case.to(device)
+    bad_lens = d.context_lens.clone()
+    bad_lens[0] = -1
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, bad_lens, out, case.scale)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    pa.check_errors(device)

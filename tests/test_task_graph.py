@@ -61,6 +61,26 @@ def test_vector_example_dag(g):
     assert [g.fanin(i) for i in range(5)] == [[], [0], [0], [1, 2], [0, 3]]
 
 
+def test_paged_attention_empty_context_gets_a_zero_fill_task():
+    """An empty context has no block task; its out rows are written by one
+    zero-fill task after the scope's alloc task."""
+    g = TaskGraph("record")
+    b, hq, d, bs, nblk, maxb = 2, 16, 64, 64, 4, 2
+    lens = np.array([0, 100], np.int32)
+    table = np.arange(b * maxb, dtype=np.int32).reshape(b, maxb)
+    bt = ChipTensor.make(table.ctypes.data, table.shape, DataType.INT32)
+    cl = ChipTensor.make(lens.ctypes.data, lens.shape, DataType.INT32)
+    q = ext(0x1000000, (b, hq, d), DataType.BFLOAT16)
+    kc = ext(0x2000000, (nblk, bs, 1, d), DataType.BFLOAT16)
+    vc = ext(0x3000000, (nblk, bs, 1, d), DataType.BFLOAT16)
+    out = ext(0x4000000, (b, hq, d))
+    g.orchestrate_paged_attention([q, kc, vc, bt, cl, out], 1 / np.sqrt(d))
+    # sequence 0: alloc + zero fill; sequence 1: alloc + 2 blocks x (QK, SF, PV, UP)
+    assert g.task_count == 2 + (1 + 4 * 2)
+    assert g.fanin(1) == []  # the fill depends on nothing
+    g.close()
+
+
 def test_paged_attention_dag_structure():
     g = TaskGraph("record")
     b, hq, d, bs, nblk, maxb = 2, 16, 128, 128, 16, 4

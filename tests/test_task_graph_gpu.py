@@ -178,6 +178,24 @@ def test_paged_attention_ragged_and_multi_tile(device):
     assert_close(out.cpu().numpy(), oracle_numpy(case), what="task graph ragged")
 
 
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_empty_context_writes_zeros(device, mode):
+    """An empty context submits no block task; the orchestration writes its rows
+    as zeros (a zero-fill task), as the fused decode defines them."""
+    print(f"[case] tg empty context mode={mode}", flush=True)
+    case = make_custom_case(batch=3, num_heads=16, kv_heads=1, head_dim=64, block_size=64,
+                            context_lens=[0, 65, 0], seed=6, max_blocks=2)
+    d = case.to(device)
+    out = torch.full(case.out_shape(), float("nan"), dtype=torch.float32, device=device)
+    with TaskGraph(mode) as g:
+        g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+        g.launch()
+        g.wait()
+    got = out.cpu().numpy()
+    assert np.all(got[0] == 0) and np.all(got[2] == 0)
+    assert_close(got, oracle_numpy(case), what=f"task graph empty context {mode}")
+
+
 def test_bad_block_is_reported_before_any_launch(device):
     case = make_case("cfg1_small")
     d = case.to(device)

@@ -141,3 +141,27 @@ def test_worker_rejects_wrong_dtypes(worker):
     args.add_scalar(1.0)
     with pytest.raises(RuntimeError):
         worker.run(handle, args)
+
+
+def test_worker_reports_bad_device_length_then_recovers(worker, device):
+    """A device-resident context_lens entry longer than its block-table row is
+    only seen by the kernel: the run fails with SIMPLER_HIP_ERR_BAD_LENGTH (-7)
+    and the next good run on the same context matches the oracle."""
+    print("[case] worker device bad length, then a good run", flush=True)
+    case = make_custom_case(batch=3, num_heads=16, kv_heads=2, head_dim=64, block_size=16,
+                            context_lens=[40, 17, 64], seed=12, max_blocks=8)
+    d = case.to(device)
+    handle = worker.register(pa.reference_chain_callable())
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    good_lens = d.context_lens
+    d.context_lens = good_lens.clone()
+    d.context_lens[2] = 8 * 16 + 1
+    torch.cuda.synchronize(device)
+    with pytest.raises(RuntimeError, match="-7"):
+        worker.chip_worker.run(handle, device_args(d, out))
+    d.context_lens = good_lens
+    out.zero_()
+    torch.cuda.synchronize(device)
+    worker.chip_worker.run(handle, device_args(d, out))
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what="worker run after a bad length")
+    worker.unregister(handle)
