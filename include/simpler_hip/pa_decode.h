@@ -132,6 +132,24 @@ int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *args, void *worksp
  * [0, max_blocks_per_seq*block_size]), else 0. Clears the flags. Synchronous. */
 int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * simpler_hip_pa_decode for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Instead of a caller workspace
+ * it uses a fixed device array of SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES inside
+ * this library, one per GPU, held until the process ends; it calls no
+ * hipMalloc/hipFree. Same arguments, kernels and results as
+ * simpler_hip_pa_decode on the same args. Returns SIMPLER_HIP_ERR_WORKSPACE
+ * (and says so on stderr) when the decode's plan needs more scratch than that
+ * (possible only with a forced num_workers). Calls on one GPU share its array:
+ * calls that may overlap on one GPU (different streams) race and must not be
+ * made. Out-of-pool block ids and bad lengths found by the kernels are handled
+ * as in simpler_hip_pa_decode (skipped / clamped) but not reported: there is
+ * no workspace to pass to simpler_hip_pa_decode_check.
+ */
+#define SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES (80u << 20)
+int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stream);
+
 /* Measurement helpers: name of the main kernel the args select, and the
  * number of worker wavefronts a launch uses. */
 const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args);

@@ -1908,6 +1908,72 @@ extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void
     return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream, phases, nullptr);
 }
 
+// ---------------------------------------------------------------------------
+// The entry point that allocates nothing: simpler_hip_pa_decode with the
+// workspace replaced by a fixed device array of this library.
+// ---------------------------------------------------------------------------
+
+namespace simpler_hip {
+namespace {
+
+// Every decode of the direct entry fits here at the default worker count on
+// MI355X (256 CUs): a GQA plan needs at most 2048 partial slots of 16 rows x
+// Dv fp32 (Dv 128: 16 MiB, Dv 256: 32 MiB), the MLA plan 2048 slots of 16 x 512
+// fp32 (64 MiB), plus (m, l) pairs, the error word and the zero page.
+constexpr size_t kScratchBytes = (size_t)SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes % 256 == 0, "scratch size");
+
+// One copy per GPU the library runs on, held until the process ends. In host
+// code `scratch` is only a stand-in for the symbol: its device address comes
+// from hipGetSymbolAddress, per device.
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// This device's address of `scratch`, looked up once per device (with that
+// device current) and kept; nullptr if the lookup fails.
+void *scratch_on_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace simpler_hip
+
+extern "C" int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *a, void *stream) {
+    int rc = validate(a);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    const KernelPair k = pick_kernel(a);
+    if (!k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    const size_t need = make_plan(a, k).total;
+    if (need > kScratchBytes) {
+        fprintf(stderr,
+                "[simpler_hip] simpler_hip_pa_decode_noalloc: this decode needs %zu bytes of scratch, above the "
+                "fixed %zu (use fewer workers or simpler_hip_pa_decode with a workspace)\n",
+                need, kScratchBytes);
+        return SIMPLER_HIP_ERR_WORKSPACE;
+    }
+    void *ws = scratch_on_current_device();
+    if (!ws) return SIMPLER_HIP_ERR_LAUNCH;
+    // Nothing in the scratch has to start at zero: every partial slot the
+    // merge reads is written by the same call's main kernel, and the zero
+    // page's contents never reach a result. The error word only accumulates.
+    return simpler_hip::pa_decode_launch(a, ws, kScratchBytes, stream, SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE,
+                                         nullptr);
+}
+
 extern "C" int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream) {
     if (!workspace || workspace_bytes < sizeof(unsigned)) return SIMPLER_HIP_ERR_WORKSPACE;
     unsigned flag = 0;
