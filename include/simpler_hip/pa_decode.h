@@ -41,25 +41,32 @@ enum {
  * (src/common/task_interface/data_type.h:47-67). */
 enum { SIMPLER_HIP_DT_FLOAT32 = 0, SIMPLER_HIP_DT_FLOAT16 = 1, SIMPLER_HIP_DT_BFLOAT16 = 6 };
 
-/* KV-cache element formats. FP8_E4M3: OCP E4M3FN bytes (the reference's
- * DataType FP8E4M3FN, data_type.h:63) with one fp32 scale per (physical block,
- * kv head); head dims 128, block sizes 16/32/64/128, GQA path (not MLA). */
-enum { SIMPLER_HIP_KV_BF16 = 0, SIMPLER_HIP_KV_FP8_E4M3 = 1 };
+/* Element formats of the query and KV caches. BF16: bf16 query and caches.
+ * FP8_E4M3: bf16 query, OCP E4M3FN cache bytes (the reference's DataType
+ * FP8E4M3FN, data_type.h:63) with one fp32 scale per (physical block, kv
+ * head); head dims 128, block sizes 16/32/64/128, GQA path (not MLA).
+ * FP16: fp16 query and caches (the dtype of the reference's GQA scene cases,
+ * tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention_highperf/
+ * test_spmd_paged_attention_highperf.py:170-232); p is rounded to fp16 as
+ * the golden rounds it to the input dtype; GQA path (not MLA). */
+enum { SIMPLER_HIP_KV_BF16 = 0, SIMPLER_HIP_KV_FP8_E4M3 = 1, SIMPLER_HIP_KV_FP16 = 2 };
 
 /*
  * One paged-attention decode call. All pointers are device pointers.
  *
- * query        bf16 [batch, q_len, num_heads, head_dim_k]   (q_len = 1: [batch, num_heads, Dk])
- * key_cache    bf16 (or fp8, see kv_format), element (blk, t, kvh, d) at
+ * query        bf16 (fp16 with kv_format FP16) [batch, q_len, num_heads, head_dim_k]
+ *              (q_len = 1: [batch, num_heads, Dk])
+ * key_cache    bf16 (fp8 or fp16, see kv_format), element (blk, t, kvh, d) at
  *              blk*k_block_stride + t*k_token_stride + kvh*k_head_stride + d
  *              (contiguous BSND [num_blocks, block_size, kv_heads, Dk]:
  *               strides BS*Hkv*Dk, Hkv*Dk, Dk)
- * value_cache  bf16, same addressing with the v_* strides and Dv columns.
+ * value_cache  same element type, same addressing with the v_* strides and Dv columns.
  *              MLA: value_cache == key_cache with the K strides and Dv <= Dk
  *              (V is the first Dv columns of K).
  * block_table  int32 [batch, max_blocks_per_seq], entries in [0, num_blocks)
  * context_lens int32 [batch], 0 <= len <= max_blocks_per_seq*block_size
- * out          [batch, q_len, num_heads, Dv] of out_dtype (FLOAT32 or BFLOAT16)
+ * out          [batch, q_len, num_heads, Dv] of out_dtype: FLOAT32 or BFLOAT16
+ *              (bf16 and fp8 caches), FLOAT32 or FLOAT16 (fp16 caches)
  * scale        softmax scale applied to q.k in fp32
  * causal       q_len > 1 only: query token i sees context_len - (q_len-1-i) tokens
  */
@@ -87,7 +94,7 @@ typedef struct SimplerHipPaDecodeArgs {
     /* 0 = one worker wavefront per wave slot of the device; > 0 forces the
      * number of workers the (tile, KV block) work list is divided among. */
     int32_t num_workers;
-    /* SIMPLER_HIP_KV_BF16 (0) or SIMPLER_HIP_KV_FP8_E4M3 (1). */
+    /* SIMPLER_HIP_KV_BF16 (0), SIMPLER_HIP_KV_FP8_E4M3 (1) or SIMPLER_HIP_KV_FP16 (2). */
     int32_t kv_format;
     /* kv_format FP8_E4M3 only: fp32 [num_blocks, num_kv_heads] dequantisation
      * scales; cache element (blk, t, kvh, d) stands for

@@ -166,12 +166,16 @@ int simpler_hip_set_execution(DeviceContextHandle ctx, int32_t execution);
  * grouped split-K chain whose QK and PV take three inputs (paged_attention_unroll,
  * *_unroll_manual_scope, *_unroll_4dims); SPMD: the cooperative AIC/AIV task
  * (spmd_paged_attention); NATIVE: the callable named
- * simpler_hip_paged_attention_decode. All run on the fused decode kernel. */
+ * simpler_hip_paged_attention_decode; HIGHPERF: the high-performance SPMD
+ * task (spmd_paged_attention_highperf: query, caches, block_table, out,
+ * workspaces, a tiling tensor carrying the lengths and the scale). All run on
+ * the fused decode kernel. */
 enum {
     SIMPLER_HIP_PA_CHAIN = 0,
     SIMPLER_HIP_PA_UNROLL = 1,
     SIMPLER_HIP_PA_SPMD = 2,
-    SIMPLER_HIP_PA_NATIVE = 3
+    SIMPLER_HIP_PA_NATIVE = 3,
+    SIMPLER_HIP_PA_HIGHPERF = 4
 };
 int simpler_hip_callable_family(DeviceContextHandle ctx, int32_t callable_id);
 

@@ -72,6 +72,13 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 # ---------------------------------------------------------------------------
 
 
+def fp16_round(x: np.ndarray) -> np.ndarray:
+    """fp32 → nearest fp16 (IEEE round-to-nearest-even, subnormals kept) → fp32,
+    as torch's ``.to(torch.float16)``."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def _row_lengths(ctx: int, q_len: int, g: int, causal: bool) -> np.ndarray:
     """Valid context length for each (query token i, group head) row of one KV head."""
     i = np.repeat(np.arange(q_len), g)
@@ -90,11 +97,15 @@ def paged_attention_decode(
     *,
     causal: bool = False,
     v_dim: int | None = None,
+    p_dtype: str = "bf16",
 ) -> np.ndarray:
     """Blockwise online-softmax paged attention (the reference golden's algorithm).
 
     query:       fp32 ``[B, q_len, Hq, Dk]`` (or ``[B, Hq, Dk]`` for q_len 1), values
-                 already bf16-representable.
+                 already representable in the input dtype.
+    p_dtype:     the input dtype p is rounded to before the row sum and PV
+                 (``goldens/paged_attention.py:168``: ``p.to(query dtype)``):
+                 ``"bf16"`` or ``"fp16"``.
     key_cache:   fp32 ``[num_blocks, BS, Hkv, Dk]``.
     value_cache: fp32 ``[num_blocks, BS, Hkv, Dv]``; ``None`` selects MLA, where V is
                  ``key_cache[..., :v_dim]``.
@@ -138,7 +149,7 @@ def paged_attention_decode(
                 with np.errstate(invalid="ignore", over="ignore"):
                     p = np.exp(s - mb[:, None]).astype(np.float32)
                 p = np.where(valid, p, np.float32(0.0))
-                p = bf16_round(p)
+                p = bf16_round(p) if p_dtype == "bf16" else fp16_round(p)
                 lb = p.sum(axis=1, dtype=np.float32)
                 ob = (p @ v).astype(np.float32)
                 if m is None:

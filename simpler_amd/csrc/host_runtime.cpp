@@ -73,6 +73,7 @@ enum PaFamily {
                                         // *_unroll_manual_scope, *_unroll_4dims
     kPaSpmd = SIMPLER_HIP_PA_SPMD,      // one cooperative AIC/AIV mix task: spmd_paged_attention
     kPaNative = SIMPLER_HIP_PA_NATIVE,  // the name simpler_hip_paged_attention_decode
+    kPaHighperf = SIMPLER_HIP_PA_HIGHPERF,  // spmd_paged_attention_highperf: lengths and scale in a tiling tensor
 };
 
 struct Callable {
@@ -120,6 +121,7 @@ struct NativeRun {
     size_t staged_bytes[kMaxRunTensors];
     int32_t dir[kMaxRunTensors];
     uint64_t scale_bits;
+    int32_t *host_lens;  // highperf family: context lengths taken from the tiling tensor (malloc'd)
     SimplerChipTensor tensors[kMaxRunTensors];  // the run's tensors as device work sees them
     SimplerHipPaDecodeArgs args;
 };
@@ -153,6 +155,15 @@ const int32_t kPvUnrollSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, 
 const int32_t kSpmdMixSig[] = {SIMPLER_ARG_IN,    SIMPLER_ARG_IN,  SIMPLER_ARG_IN,  SIMPLER_ARG_IN, SIMPLER_ARG_IN,
                                SIMPLER_ARG_INOUT, SIMPLER_ARG_OUT, SIMPLER_ARG_OUT, SIMPLER_ARG_OUT};
 
+// The high-performance SPMD callable (tests/st/a2a3/tensormap_and_ringbuffer/
+// spmd_paged_attention_highperf/test_spmd_paged_attention_highperf.py:96-165):
+// query, key_cache, value_cache, block_table, out, eight workspaces, tiling,
+// null; both halves of the mix task declare the same 15-tensor payload.
+const int32_t kHighperfSig[] = {SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_OUT,
+                                SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN,
+                                SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN, SIMPLER_ARG_IN};
+constexpr int kHighperfTensors = 15;
+
 struct ChildSig {
     const int32_t *sig;
     int32_t n;
@@ -167,6 +178,8 @@ const PaFamilySpec kPaFamilies[] = {
     {kPaUnroll, 4, {{kQkUnrollSig, 4}, {kSfSig, 4}, {kPvUnrollSig, 4}, {kUpSig, 7}}},
     {kPaSpmd, 2, {{kSpmdMixSig, 9}, {kSpmdMixSig, 9}, {nullptr, 0}, {nullptr, 0}}},
 };
+const PaFamilySpec kHighperfFamily = {
+    kPaHighperf, 2, {{kHighperfSig, kHighperfTensors}, {kHighperfSig, kHighperfTensors}, {nullptr, 0}, {nullptr, 0}}};
 
 bool sig_equals(const int32_t *a, int32_t na, const int32_t *b, int32_t nb) {
     if (na != nb) return false;
@@ -211,11 +224,15 @@ CallableKind classify(const uint8_t *blob, Callable &out) {
         return kPagedAttention;
     }
     if (sig_equals(h.signature_, h.sig_count_, kVecOrchSig, 3) && h.child_count_ == 3) return classify_vector(h, blob);
-    if (!sig_equals(h.signature_, h.sig_count_, kOrchSig, 6)) return kNone;
+    const bool highperf = sig_equals(h.signature_, h.sig_count_, kHighperfSig, kHighperfTensors);
+    if (!highperf && !sig_equals(h.signature_, h.sig_count_, kOrchSig, 6)) return kNone;
     // The paged-attention orchestrations: the children (in any order) must be
     // exactly one family's func ids with that family's signatures.
     const uint8_t *storage = blob + SIMPLER_CHIP_CALLABLE_STORAGE_OFFSET;
-    for (const PaFamilySpec &f : kPaFamilies) {
+    const PaFamilySpec *families = highperf ? &kHighperfFamily : kPaFamilies;
+    const int n_families = highperf ? 1 : (int)(sizeof(kPaFamilies) / sizeof(kPaFamilies[0]));
+    for (int fi = 0; fi < n_families; ++fi) {
+        const PaFamilySpec &f = families[fi];
         if (h.child_count_ != f.children) continue;
         bool seen[4] = {false, false, false, false};
         bool ok = true;
@@ -270,10 +287,15 @@ int decode_pa_args(const SimplerChipStorageTaskArgs *a, SimplerHipPaDecodeArgs &
     // fp8 caches: FP8E4M3FN key/value caches, then tensors 6 and 7 = fp32
     // [num_blocks, kv_heads] K and V scales (no reference counterpart)
     const bool fp8 = k.dtype == SIMPLER_DT_FP8E4M3FN;
-    if (q.dtype != SIMPLER_DT_BFLOAT16 || (!fp8 && k.dtype != SIMPLER_DT_BFLOAT16) || v.dtype != k.dtype) {
-        logf("query must be BFLOAT16 and key_cache/value_cache both BFLOAT16 or both FP8E4M3FN");
+    const bool fp16 = q.dtype == SIMPLER_DT_FLOAT16;
+    const bool ok_dtypes = fp16 ? (k.dtype == SIMPLER_DT_FLOAT16 && v.dtype == SIMPLER_DT_FLOAT16)
+                                : (q.dtype == SIMPLER_DT_BFLOAT16 && (fp8 || k.dtype == SIMPLER_DT_BFLOAT16) &&
+                                   v.dtype == k.dtype);
+    if (!ok_dtypes) {
+        logf("query/key_cache/value_cache must be BFLOAT16 (caches BFLOAT16 or FP8E4M3FN) or all FLOAT16");
         return SIMPLER_HIP_ERR_UNSUPPORTED;
     }
+    if (fp16) pa.kv_format = SIMPLER_HIP_KV_FP16;
     if (fp8) {
         if (a->tensor_count_ < kPaTensors + 2) {
             logf("fp8 caches need tensors 6 and 7: k_scale and v_scale, fp32 [num_blocks, kv_heads]");
@@ -452,6 +474,72 @@ void release_staged(NativeRun *r) {
         r->staged_dev[i] = nullptr;
     }
     r->n_staged = 0;
+    free(r->host_lens);
+    r->host_lens = nullptr;
+}
+
+// Tiling-tensor layout of the high-performance SPMD callable
+// (tests/st/.../spmd_paged_attention_highperf/kernels/pa_tiling.py:18-62,360-430):
+// a header of TILING_HEAD_SIZE int32 words, then TILING_PARA_SIZE words per
+// sequence, word 1 of which is the sequence's KV length.
+constexpr int kTilingBatch = 0, kTilingNumHeads = 1, kTilingHeadDim = 2, kTilingBlockSize = 4, kTilingTor = 6,
+              kTilingKvHeads = 7, kTilingHeadSize = 17, kTilingParaSize = 18, kTilingParaKvSeqLen = 1;
+constexpr int kTilingMinHeader = 19;
+
+// Rewrites the high-performance callable's arguments into the common 7-argument
+// form (query, key_cache, value_cache, block_table, context_lens, out; scale):
+// the lengths and the scale come from the tiling tensor (tensor 13), read on
+// the host (copied back first when it is device-resident); the workspaces
+// (tensors 5..12) and tensor 14 are not used. r->host_lens keeps the lengths
+// until the run is finalised.
+int remap_highperf(const SimplerChipStorageTaskArgs *a, NativeRun *r, SimplerChipStorageTaskArgs *out) {
+    if (a->tensor_count_ < kHighperfTensors) {
+        logf("the high-performance paged-attention callable takes %d tensors (got %d)", kHighperfTensors,
+             a->tensor_count_);
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    const SimplerChipTensor &q = tensor_at(a, 0), &k = tensor_at(a, 1), &tl = tensor_at(a, 13);
+    uint64_t n = 1;
+    for (uint32_t d = 0; d < tl.ndims; ++d) n *= tl.shapes[d];
+    if (tl.dtype != SIMPLER_DT_INT32 || !contiguous(tl) || n < kTilingMinHeader || n > (1u << 26)) {
+        logf("tiling must be a contiguous INT32 tensor with a header");
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    std::vector<int32_t> w(n);
+    const void *src = (const void *)(uintptr_t)(tl.buffer.addr + tl.start_offset * 4);
+    if (tl.address_space == SIMPLER_ADDR_DEVICE) {
+        if (hipMemcpy(w.data(), src, n * 4, hipMemcpyDeviceToHost) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    } else {
+        memcpy(w.data(), src, n * 4);
+    }
+    const int64_t batch = w[kTilingBatch], head = w[kTilingHeadSize], para = w[kTilingParaSize];
+    if (q.ndims != 3 || k.ndims != 4 || batch != (int64_t)q.shapes[0] || w[kTilingNumHeads] != (int32_t)q.shapes[1] ||
+        w[kTilingHeadDim] != (int32_t)q.shapes[2] || w[kTilingBlockSize] != (int32_t)k.shapes[1] ||
+        w[kTilingKvHeads] != (int32_t)k.shapes[2] || head < kTilingMinHeader || para < kTilingParaKvSeqLen + 1 ||
+        (uint64_t)(head + batch * para) > n) {
+        logf("tiling header disagrees with the query [B, Hq, D] / key_cache [nblk, BS, Hkv, D] shapes");
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    r->host_lens = static_cast<int32_t *>(malloc((size_t)(batch > 0 ? batch : 1) * 4));
+    if (!r->host_lens) return SIMPLER_HIP_ERR_WORKSPACE;
+    for (int64_t b = 0; b < batch; ++b) r->host_lens[b] = w[head + b * para + kTilingParaKvSeqLen];
+    memset(out, 0, sizeof(*out));
+    for (int i = 0; i < 4; ++i) out->tensors_[i] = a->tensors_[i];
+    SimplerChipTensor &cl = out->tensors_[4];
+    cl.buffer.addr = (uint64_t)(uintptr_t)r->host_lens;
+    cl.buffer.size = (uint64_t)batch * 4;
+    cl.ndims = 1;
+    cl.shapes[0] = (uint32_t)batch;
+    cl.strides[0] = 1;
+    cl.dtype = SIMPLER_DT_INT32;
+    cl.is_contiguous = 1;
+    cl.address_space = SIMPLER_ADDR_HOST;
+    cl.extent_elem_cache = (uint64_t)batch;
+    out->tensors_[5] = a->tensors_[4];
+    out->tensor_count_ = kPaTensors;
+    out->scalars_[0] = (uint32_t)w[kTilingTor];  // the scale, as fp32 bits
+    out->scalar_count_ = 1;
+    return SIMPLER_HIP_OK;
 }
 
 }  // namespace
@@ -639,9 +727,22 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
     r->execution = cb.kind == kVectorExample && execution == SIMPLER_HIP_EXEC_FUSED ? SIMPLER_HIP_EXEC_TASK_GRAPH
                                                                                     : execution;
     int rc = SIMPLER_HIP_OK;
+    // The high-performance callable's arguments, rewritten into the common form
+    std::unique_ptr<SimplerChipStorageTaskArgs> remapped;
+    if (cb.kind == kPagedAttention && cb.family == kPaHighperf) {
+        remapped.reset(new (std::nothrow) SimplerChipStorageTaskArgs);
+        if (!remapped) rc = SIMPLER_HIP_ERR_WORKSPACE;
+        if (rc == SIMPLER_HIP_OK) rc = remap_highperf(a, r, remapped.get());
+        if (rc != SIMPLER_HIP_OK) {
+            release_staged(r);
+            r->magic = 0;
+            return rc;
+        }
+        a = remapped.get();
+    }
     if (cb.kind == kPagedAttention) {
         r->n_tensors = kPaTensors;
-        rc = decode_pa_args(a, r->args, 1);
+        rc = decode_pa_args(a, r->args, cb.family == kPaHighperf ? kMaxRunTensors : 1);
         if (rc == SIMPLER_HIP_OK && r->args.kv_format == SIMPLER_HIP_KV_FP8_E4M3) r->n_tensors = kPaTensors + 2;
         if (rc == SIMPLER_HIP_OK) rc = check_host_tables(a, r->args);
         if (rc == SIMPLER_HIP_OK && r->execution != SIMPLER_HIP_EXEC_FUSED &&
@@ -652,7 +753,7 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
             rc = SIMPLER_HIP_ERR_UNSUPPORTED;
         }
         if (rc == SIMPLER_HIP_OK && r->execution != SIMPLER_HIP_EXEC_FUSED && cb.family != kPaChain &&
-            cb.family != kPaNative) {
+            cb.family != kPaNative) {  // also the highperf family
             logf("the task-graph backend runs the per-block QK/SF/PV/UP orchestration only; the grouped and "
                  "SPMD paged-attention callables run on the fused kernel");
             rc = SIMPLER_HIP_ERR_UNSUPPORTED;
@@ -663,15 +764,17 @@ int simpler_prepare_run(DeviceContextHandle h, RuntimeHandle runtime, int32_t id
         rc = check_vector_args(a);
     }
     if (rc != SIMPLER_HIP_OK) {
+        release_staged(r);
         r->magic = 0;
         return rc;
     }
-    // Stage host tensors; directions from the callable signature.
+    // Stage host tensors; directions from the callable signature (for the
+    // rewritten high-performance arguments, those of the common form).
     const void *dev[kMaxRunTensors];
     for (int i = 0; i < r->n_tensors; ++i) {
         const SimplerChipTensor &t = tensor_at(a, i);
         const size_t esz = simpler_dtype_size(t.dtype);
-        const int dir = i < cb.sig_count ? cb.sig[i] : SIMPLER_ARG_IN;
+        const int dir = remapped ? kOrchSig[i] : (i < cb.sig_count ? cb.sig[i] : SIMPLER_ARG_IN);
         r->tensors[i] = t;
         if (t.address_space == SIMPLER_ADDR_DEVICE) {
             dev[i] = (const void *)(uintptr_t)(t.buffer.addr + t.start_offset * esz);

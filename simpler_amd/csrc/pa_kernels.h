@@ -1,0 +1,1589 @@
+// Fused split-K paged-attention decode for gfx950 (MI355X).
+//
+// Replaces the per-KV-block AICore task chain of simpler's paged attention
+// (examples/a2a3/tensormap_and_ringbuffer/paged_attention/kernels/):
+//   QK  aic/aic_qk_matmul.cpp:38-100        -> MFMA 16x16x32 bf16, S^T = K * Q^T
+//   SF  aiv/aiv_softmax_prepare.cpp:96-131  -> in-register mask/scale/rowmax/exp,
+//                                             P rounded to bf16 (RNE) before the
+//                                             row sum and before PV
+//   PV  aic/aic_pv_matmul.cpp:38-99         -> MFMA 16x16x16 bf16, O += P * V
+//   UP  aiv/aiv_online_update.cpp:125-224   -> register-resident online merge
+// plus the cross-split log-sum-exp merge of the reference's SplitKV path
+// (tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention_highperf/
+//  kernels/kernel/pa_kernel.cce:1634-1773), done by a second kernel.
+//
+// Numerics follow the reference golden (simpler_setup/goldens/paged_attention.py
+// :145-187) block for block: the softmax max is taken per KV block, p is rounded
+// to bf16 relative to that block max, l sums the rounded p, and blocks merge
+// with m' = max(m, m_blk). The accumulator is kept in the frame of the latest
+// block max ("block frame": A = O * e^{m - f}), so the per-block merge
+//   O' = e^{m-m'} O + e^{m_blk-m'} (P_blk V)
+// becomes A' = e^{f - m_blk} A + P_blk V, which MFMA accumulates in place.
+// A block whose max lies more than kFrameGap below the running max adds less
+// than e^-kFrameGap relative and is skipped, which bounds A by e^kFrameGap * |O|.
+//
+// Work decomposition (stream-K): the work is the flattened list of
+// (tile, KV block) pairs, tile = (batch, kv head, row tile), in that order
+// (optionally as one list per tile of a batch; see lane_tiles).
+// A row is one (query token, head in the GQA group) pair; 16 rows per tile
+// (MFMA N). The main kernel launches one worker (a wavefront, or sibling
+// wavefronts for several row tiles) per slot of the GPU (CUs x workers per CU
+// at this kernel's occupancy) and gives each an equal contiguous slice of that
+// list, computed on the device from context_lens, so ragged lengths cost no
+// imbalance and no tail. A tile that
+// lies inside one slice is finished (normalised and stored) by that wave; a
+// tile cut by slice boundaries leaves one partial (O, m, l) per piece, and a
+// second small kernel merges those by log-sum-exp. The kernel boundary orders
+// the partial writes before the merge; no device-scope fences are used.
+//
+// Lane (qd = lane/16, pc = lane%16):
+//   QK   A operand = K token pc of the tile, dims 32kk+8qd..+7 (one 16-B load,
+//                    or one 16-B LDS read when K is staged through LDS)
+//        B operand = Q row pc, same dims
+//        C         = S[row pc][tokens 4qd..4qd+3]   (S^T tile)
+//   PV   A operand = P[row pc][tokens 4qd..4qd+3]  == the QK C layout (no shuffle)
+//        B operand = V[tokens 4qd..4qd+3][dim 8pc+jj], built from four 16-B row
+//                    loads by an in-register 4x8 bf16 transpose
+//        C         = O[rows 4qd..4qd+3][dim 8pc+jj]
+// Within a segment, V of block i is issued first and K of block i+1 as soon
+// as K of block i is consumed (after QK(i), or once K(i) is staged in LDS), so
+// both streams are in flight during the math.
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <type_traits>
+#include <vector>
+
+#include "simpler_hip/pa_decode.h"
+
+namespace simpler_hip {
+namespace pa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
+constexpr float kFrameGap = 40.f;
+constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit (half-line K reads)
+constexpr int kWorkersPerSimdCu = 4;   // one worker per SIMD: full-row K reads and fp8 caches (see make_plan)
+constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
+
+struct KernelParams {
+    const uint16_t *q;
+    const uint16_t *k;
+    const uint16_t *v;
+    const int32_t *block_table;
+    const int32_t *context_lens;
+    void *out;
+    float *part_o;   // [workers][2 slots][16 rows][DV]
+    float *part_ml;  // [workers][2 slots][m[16], l[16]]
+    unsigned *error_flag;
+    const char *zeros;  // 256 bytes of the workspace that stay zero (LDS fill source)
+    const char *zero_page;  // zero bytes standing in for the 16-token tiles past a context's end, or null
+    const float *k_scale;  // fp8 caches: [num_blocks][kv_heads] dequantisation scales
+    const float *v_scale;
+    int64_t k_block_stride, k_token_stride, k_head_stride;
+    int64_t v_block_stride, v_token_stride, v_head_stride;
+    int32_t batch, q_len, num_heads, kv_heads, group, rows, row_tiles;
+    int32_t tiles_per_worker;  // row tiles a worker workgroup runs side by side (one wave each)
+    int32_t row_groups;        // ceil(row_tiles / tiles_per_worker): work-list tiles per kv head
+    int32_t block_size, max_blocks, num_pool_blocks;
+    int32_t workers;
+    int32_t lanes;  // independent work lists; list u holds tiles [u, u+1) * (tiles per batch / lanes) of each batch
+    float scale;
+    int32_t causal;
+    unsigned *err_mirror;  // host-visible copy of *error_flag written by the merge kernel, or null
+};
+
+__device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
+
+// V rows are read as whole 128-byte lines exactly once: non-temporal loads
+// keep them from displacing useful lines (measured ~11% more read bandwidth on
+// MI355X than plain loads). K is read as 64-byte halves of a line by two
+// consecutive instructions, so K uses plain loads, which let the L1 merge the
+// two halves into one line request (non-temporal K measured 5-10% slower).
+__device__ __forceinline__ u32x4_t stream_ld16(const char *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
+
+__device__ __forceinline__ u32x4_t lds_ld16(const char *base, uint32_t off) {
+    return *reinterpret_cast<const LDS_AS u32x4_t *>((const LDS_AS char *)base + off);
+}
+
+__device__ __forceinline__ void lds_st16(char *base, uint32_t off, u32x4_t v) {
+    *reinterpret_cast<LDS_AS u32x4_t *>((LDS_AS char *)base + off) = v;
+}
+
+// Orders one wave's LDS writes before its later reads of other lanes' data
+// (and those reads before later writes). The LDS executes a wave's
+// instructions in order, so this only has to stop the compiler from moving
+// LDS accesses across it; it emits no instruction.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
+    // fp32 -> bf16 round-to-nearest-even (gfx950: v_cvt_pk_bf16_f32)
+    const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+    return __builtin_bit_cast(unsigned, h);
+}
+
+// The 16-bit element type of the query and the caches: its MFMA forms and
+// the rounding of p to it (the golden rounds p to the input dtype before the
+// row sum and PV, goldens/paged_attention.py:168; the reference's GQA cases
+// are fp16, tests/st/.../spmd_paged_attention_highperf/
+// test_spmd_paged_attention_highperf.py:170-232).
+template <typename ET>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+    static constexpr unsigned kOnePair = 0x3f803f80u;  // two bf16 1.0
+    // 16x16x32: 8 elements per lane of each operand
+    static __device__ __forceinline__ f32x4_t mma32(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    }
+    // 16x16x16: 4 elements per lane of each operand
+    static __device__ __forceinline__ f32x4_t mma16(u32x2_t a, u32x2_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a), __builtin_bit_cast(i16x4_t, b),
+                                                         c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ unsigned pack2(float a, float b) { return pack_bf16x2(a, b); }
+};
+
+template <>
+struct Elem<_Float16> {
+    static constexpr unsigned kOnePair = 0x3c003c00u;  // two fp16 1.0
+    static __device__ __forceinline__ f32x4_t mma32(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                      0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4_t mma16(u32x2_t a, u32x2_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                     0, 0, 0);
+    }
+    // fp32 -> fp16 round-to-nearest-even (gfx950: v_cvt_pk_f16_f32)
+    static __device__ __forceinline__ unsigned pack2(float a, float b) {
+        return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+    }
+};
+
+// Four E4M3FN bytes -> four bf16 (two words); exact (every E4M3FN value is a
+// bf16 value). gfx950 v_cvt_scalef32_pk_bf16_fp8 with scale 1.
+__device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
+    const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    return (u32x2_t){__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi)};
+}
+
+// Eight E4M3FN bytes (two words) -> eight bf16 (one 16-byte MFMA operand).
+__device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(unsigned w0, unsigned w1) {
+    const u32x2_t a = fp8x4_to_bf16x4(w0), b = fp8x4_to_bf16x4(w1);
+    return (u32x4_t){a[0], a[1], b[0], b[1]};
+}
+
+
+template <typename OutT>
+struct OutStore;
+
+template <>
+struct OutStore<float> {
+    // 8 consecutive values
+    __device__ static void store8(void *base, int64_t off, const float (&v)[8]) {
+        float *p = reinterpret_cast<float *>(base) + off;
+        *reinterpret_cast<f32x4_t *>(p) = (f32x4_t){v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4_t *>(p + 4) = (f32x4_t){v[4], v[5], v[6], v[7]};
+    }
+    __device__ static void store4(void *base, int64_t off, f32x4_t v) {
+        *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(base) + off) = v;
+    }
+};
+
+template <>
+struct OutStore<_Float16> {
+    __device__ static void store8(void *base, int64_t off, const float (&v)[8]) {
+        uint16_t *p = reinterpret_cast<uint16_t *>(base) + off;
+        *reinterpret_cast<u32x4_t *>(p) =
+            (u32x4_t){Elem<_Float16>::pack2(v[0], v[1]), Elem<_Float16>::pack2(v[2], v[3]),
+                      Elem<_Float16>::pack2(v[4], v[5]), Elem<_Float16>::pack2(v[6], v[7])};
+    }
+    __device__ static void store4(void *base, int64_t off, f32x4_t v) {
+        uint16_t *p = reinterpret_cast<uint16_t *>(base) + off;
+        *reinterpret_cast<u32x2_t *>(p) = (u32x2_t){Elem<_Float16>::pack2(v[0], v[1]), Elem<_Float16>::pack2(v[2], v[3])};
+    }
+};
+
+template <>
+struct OutStore<__bf16> {
+    __device__ static void store8(void *base, int64_t off, const float (&v)[8]) {
+        uint16_t *p = reinterpret_cast<uint16_t *>(base) + off;
+        *reinterpret_cast<u32x4_t *>(p) = (u32x4_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                    pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    }
+    __device__ static void store4(void *base, int64_t off, f32x4_t v) {
+        uint16_t *p = reinterpret_cast<uint16_t *>(base) + off;
+        *reinterpret_cast<u32x2_t *>(p) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Work partition shared by both kernels
+// ---------------------------------------------------------------------------
+
+// Context length of sequence b, clamped to what its block-table row can hold.
+__device__ __forceinline__ int ctx_of(const KernelParams &P, int b) {
+    return min(max(P.context_lens[b], 0), P.max_blocks * P.block_size);
+}
+
+__device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
+    return (ctx_of(P, b) + P.block_size - 1) / P.block_size;
+}
+
+// Error word bits (workspace offset 0), read back by simpler_hip_pa_decode_check.
+constexpr unsigned kErrBadBlock = 1u;   // a block_table entry outside the pool (that block is skipped)
+constexpr unsigned kErrBadLength = 2u;  // a context_lens entry the kernels had to clamp
+
+// One wave of the grid (wave 0 of workgroup 0) checks every raw length: below
+// 0, above what the block-table row holds, or (causal) shorter than the query.
+// The kernels run such a sequence with its length clamped by ctx_of; the flag
+// turns that into an error for the caller, as the host-side table check does.
+__device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
+    if (blockIdx.x != 0 || threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const int64_t cap = (int64_t)P.max_blocks * P.block_size;
+    const int lo = P.causal ? P.q_len : 0;
+    bool bad = false;
+    for (int b = lane; b < P.batch; b += 64) {
+        const int len = P.context_lens[b];
+        bad |= len < lo || (int64_t)len > cap;
+    }
+    if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
+}
+
+// Work lists: the (tile, KV block) pairs of all batches form P.lanes lists of
+// equal length. List u holds, per batch, the tiles u*lt .. u*lt+lt-1 (lt =
+// tiles per batch / lanes), batch-major, then tile, then block; its
+// P.workers / lanes workers (ids u, u + lanes, u + 2*lanes, ...) take equal
+// contiguous slices of it. With lanes = tiles per batch, the workers of every
+// kv head get the same block ranges, so neighbouring workers read the
+// different heads of the same token rows at about the same time (the caches
+// interleave heads within a row).
+__device__ __forceinline__ int lane_tiles(const KernelParams &P) { return P.kv_heads * P.row_groups / P.lanes; }
+
+// Wave-level scan over the batch for one list. Work of batch b = blocks_of(b)
+// * lane_tiles. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
+// before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
+// *prefix_of_pos = the batch whose work range contains pos and the work before
+// it. `pos` may be given as a fraction of the total (pos_num / pos_den of it,
+// rounded up to whole chunks) so that one pass suffices. All results are
+// wave-uniform. One context_lens load per 64 sequences.
+__device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
+                         int *prefix_of_pos) {
+    const int lane = threadIdx.x & 63;
+    const int tpb = lane_tiles(P);
+    int carry = 0;
+    for (int base = 0; base < P.batch; base += 64) {
+        const int b = base + lane;
+        const int cnt = b < P.batch ? blocks_of(P, b) * tpb : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += y;
+        }
+        const int excl = carry + incl - cnt;
+        if (want_b >= base && want_b < base + 64) *prefix_of_want = __shfl(excl, want_b - base, 64);
+        if (pos >= 0) {
+            const unsigned long long hit = __ballot(cnt > 0 && pos >= excl && pos < excl + cnt);
+            if (hit) {
+                const int src = __ffsll((long long)hit) - 1;
+                *b_of_pos = base + src;
+                *prefix_of_pos = __shfl(excl, src, 64);
+            }
+        }
+        carry += __shfl(incl, 63, 64);
+    }
+    return carry;
+}
+
+// Slice c of a list (the list's c-th worker), in one pass over the batch when
+// there are at most 64 sequences: total work, then the batch containing
+// c*chunk.
+__device__ inline int locate_slice(const KernelParams &P, int c, int *start, int *end, int *b_of_start,
+                            int *prefix_of_start) {
+    const int lane = threadIdx.x & 63;
+    const int per_list = max(P.workers / P.lanes, 1);
+    if (P.batch > 64) {
+        const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
+        const int chunk = (total + per_list - 1) / per_list;
+        *start = c * chunk;
+        *end = min(*start + chunk, total);
+        if (*start < *end) scan_work(P, -1, nullptr, *start, b_of_start, prefix_of_start);
+        return total;
+    }
+    const int tpb = lane_tiles(P);
+    const int cnt = lane < P.batch ? blocks_of(P, lane) * tpb : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+    }
+    const int total = __shfl(incl, 63, 64);
+    const int chunk = (total + per_list - 1) / per_list;
+    *start = c * chunk;
+    *end = min(*start + chunk, total);
+    const int excl = incl - cnt;
+    const unsigned long long hit = __ballot(cnt > 0 && *start >= excl && *start < excl + cnt);
+    if (hit) {
+        const int src = __ffsll((long long)hit) - 1;
+        *b_of_start = src;
+        *prefix_of_start = __shfl(excl, src, 64);
+    }
+    return total;
+}
+
+// Output element offset of (row r of kv head kvh, dim 0).
+__device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, int kvh, int r, int dv) {
+    const int i = r / P.group, hh = r - i * P.group;
+    return ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * dv;
+}
+
+// ---------------------------------------------------------------------------
+// One segment: KV blocks [blk_begin, blk_end) of tile (b, kvh, rt)
+// ---------------------------------------------------------------------------
+
+// KV8: K and V caches hold E4M3FN bytes with one fp32 scale per (block, kv
+// head). They are widened to bf16 in registers (exact) right before the
+// MFMAs. The K scale folds into the softmax scale. The V scale is carried as
+// the accumulator's frame: A is kept in units of the V scale of the last block
+// it absorbed, and moving to a block with another scale multiplies the
+// rescale factor by old/new. Each K load then reads 16 dims (16 bytes) of a
+// token, so the QK contraction visits dims in a permuted order: k-step kk of
+// lane group qd holds dims 16·qd + 64·(kk/2) + 8·(kk%2) .. +7, and Q is loaded
+// in the same order.
+//
+// KLDS (bf16, DK = 128): K is read like V, as whole 256-byte token rows (lane
+// (qd, pc) reads 16-byte chunk pc of token 4qd+e of each 16-token tile, so
+// one instruction covers four full rows), with non-temporal loads, and is
+// rearranged into the QK operand layout through this wave's BS x 256-byte LDS
+// buffer `klds`. Chunk c of token T sits at slot c ^ (T & 15) of the token's
+// LDS row, so the row writes and the operand reads each touch 16 distinct
+// 16-byte slots per 16 lanes. The K registers are free once a block is in
+// LDS, so the next block's K is issued before this block's QK.
+//
+// ctx and nblk are sequence b's (clamped) context length and block count.
+// ET: the element type of the query and bf16/fp16 caches (fp8 caches widen
+// to bf16, so KV8 takes ET = bf16).
+template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16>
+__device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
+                                            const int ctx, const int nblk, const int blk_begin, const int blk_end,
+                                            float *const part_o, float *const part_ml,
+                                            const bool sync_siblings, char *const klds = nullptr) {
+    constexpr int NT = BS / 16;            // 16-token tiles per KV block
+    constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
+    constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
+    constexpr int ESZ = KV8 ? 1 : 2;       // cache element bytes
+    static_assert(!KV8 || (DK % 64 == 0 && DV % 128 == 0), "fp8 caches: head dims multiple of 64 (K), 128 (V)");
+    static_assert(!KLDS || (!KV8 && DK == 128), "K through LDS: 16-bit caches, DK = 128");
+    static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
+    const int lane = threadIdx.x & 63;
+    const int qd = lane >> 4;
+    const int pc = lane & 15;
+    const int rows_here = min(16, P.rows - rt * 16);
+
+    // ---- Q^T operand (row pc, dims 32kk+8qd..) and this row's visible length ----
+    int rowlen = 0;
+    u32x4_t qv[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+    if (pc < rows_here) {
+        const int r = rt * 16 + pc;
+        const int i = r / P.group, hh = r - i * P.group;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
+            if (DK % 32 == 0 || dim < DK) qv[kk] = ld16(qrow + dim);
+        }
+        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+    }
+    // shortest visible length over the valid rows of this tile (wave-uniform):
+    // blocks that end at or before it need no masking.
+    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
+
+    // Block-table entries are read through the scalar cache (constant address
+    // space): the load is counted by lgkmcnt, so waiting for it never waits for
+    // the K/V loads in flight. (A vector load issued after V(i) and needed for
+    // K(i+1) would make the K(i+1) loads wait for all of V(i).)
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
+
+    f32x4_t acc[DVS][8];
+#pragma unroll
+    for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    // Row sums of the rounded p on the matrix unit (P x ones), kept in A's
+    // frame: every lane holds rows 4qd+e like A's columns.
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const u32x2_t ones4 = (u32x2_t){Elem<ET>::kOnePair, Elem<ET>::kOnePair};  // 1.0 of the element type
+    constexpr float kLog2e = 1.4426950408889634f;
+    float m_run = kNegClamp, f_run = kNegClamp;
+
+    // bf16: the operands themselves; fp8: the raw bytes (half the registers)
+    u32x4_t kreg[NT][KV8 ? KS / 2 : KS];
+    u32x4_t vreg[NT][DVS][KV8 ? 1 : 4];
+    u32x2_t vraw[NT][DVS][KV8 ? 4 : 1];
+    float vs_frame = 1.f;  // KV8: the V scale A is expressed in (this lane's row)
+
+    // Addresses: a wave-uniform byte base plus one 32-bit per-lane offset that
+    // is the same for every block.
+    const int64_t k_tok_b = P.k_token_stride * ESZ, v_tok_b = P.v_token_stride * ESZ;
+    const uint32_t k_lane = KLDS ? (uint32_t)(4 * qd * k_tok_b + 16 * pc) : (uint32_t)(pc * k_tok_b + 16 * qd);
+    uint32_t kw_off[4], kr_off[KS];  // KLDS: LDS byte offsets of this lane's row writes / operand reads
+    if constexpr (KLDS) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw_off[e] = (4 * qd + e) * 256 + ((pc ^ (4 * qd + e)) << 4);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) kr_off[kk] = pc * 256 + (((4 * kk + qd) ^ pc) << 4);
+    }
+    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 8 * ESZ * pc);
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * ESZ;
+    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * ESZ;
+
+    auto checked = [&](int phys, bool &bad) -> int {
+        bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
+        return bad ? 0 : phys;
+    };
+    // Base of 16-token tile t of block blk: tiles wholly past the context's end
+    // read the zero page instead (the same lane offsets, L2-resident zeros), so
+    // a sequence's last block costs only its valid tiles of HBM traffic while
+    // the loads stay unconditional (their wait counts stay exact). Scores of
+    // those tokens are masked and their V rows zeroed as before.
+    auto tile_base = [&](const char *blk_base, int blk, int t, int64_t tok_b) -> const char * {
+        const bool past = P.zero_page && 16 * t >= ctx - blk * BS;
+        return past ? P.zero_page : blk_base + (int64_t)(16 * t) * tok_b;
+    };
+    auto load_k = [&](auto &kdst, int phys, int blk) {
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * ESZ;
+        if constexpr (KLDS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const char *tb = tile_base(kb, blk, t, k_tok_b);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const char *kt = tb + (int64_t)e * k_tok_b + k_lane;
+                    kdst[t][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(kt) : stream_ld16(kt);
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const char *kt = tile_base(kb, blk, t, k_tok_b);
+#pragma unroll
+            for (int kk = 0; kk < (KV8 ? KS / 2 : KS); ++kk) {
+                if (KV8 || DK % 32 == 0 || 32 * kk + 8 * qd < DK)
+                    kdst[t][kk] = *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk);
+                else
+                    kdst[t][kk] = (u32x4_t){0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto load_v = [&](auto &vdst, auto &vrawdst, int phys, int blk) {
+        const char *vb = v_head + (int64_t)phys * P.v_block_stride * ESZ;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const char *vt = tile_base(vb, blk, t, v_tok_b) + (int64_t)e * v_tok_b;
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds) {
+                    if constexpr (KV8) {
+                        const u32x2_t *src = reinterpret_cast<const u32x2_t *>(vt + v_lane + 128 * ds);
+                        vrawdst[t][ds][e] = V_SHARED ? *src : __builtin_nontemporal_load(src);
+                    } else if (DV % 128 == 0 || 128 * ds + 8 * pc < DV) {
+                        vdst[t][ds][e] = V_SHARED ? *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds)
+                                                  : stream_ld16(vt + v_lane + 256 * ds);
+                    } else {
+                        vdst[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                    }
+                }
+            }
+    };
+
+    // One KV block: QK on kr (or the LDS copy), softmax, PV on vr / vrw.
+    // before_qk and after_qk place the single-buffer pipeline's loads of the
+    // next block's K.
+    auto compute_block = [&](const int blk, const int phys_b, const bool blk_bad, auto &kr, auto &vr, auto &vrw,
+                             auto &&before_qk, auto &&after_qk) {
+        const bool first = (blk == blk_begin);
+        if (blk_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
+        float sc = P.scale, vs = 1.f;
+        if constexpr (KV8) {  // this block's dequantisation scales (wave-uniform, scalar loads)
+            typedef const __attribute__((address_space(4))) float *cfloat_p;
+            const int64_t si = (int64_t)phys_b * P.kv_heads + kvh;
+            sc = P.scale * ((cfloat_p)P.k_scale)[si];
+            vs = ((cfloat_p)P.v_scale)[si];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        before_qk();
+
+        // ---- QK: S^T tiles ----
+        f32x4_t s[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                u32x4_t kop;
+                if constexpr (KV8) {
+                    const u32x4_t raw = kr[t][kk >> 1];
+                    kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
+                } else if constexpr (KLDS) {
+                    kop = lds_ld16(klds, t * 4096 + kr_off[kk]);
+                } else {
+                    kop = kr[t][kk];
+                }
+                c = Elem<ET>::mma32(kop, qv[kk], c);
+            }
+            s[t] = c;
+        }
+
+        __builtin_amdgcn_sched_barrier(0);
+        after_qk();
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- softmax prepare: mask, block max of s*scale (golden :145-165).
+        // For scale > 0 the max of the scaled scores is the scaled max, so the
+        // scale folds into the exponent below; otherwise scale first ----
+        if (!(sc > 0.f)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
+        const int blk0 = blk * BS;
+        const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
+        const int rvalid = blk_bad ? 0 : rowlen - blk0;  // tokens of this block visible to row pc
+        // one wave-uniform branch around the masking (per-element selects
+        // would run on every block)
+        if (!full) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mb = fmaxf(mx * sc, kNegClamp);
+
+        // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
+        const float mnew = first ? mb : fmaxf(m_run, mb);
+        const bool use = first || (mb >= mnew - kFrameGap);
+        const float cfe = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);  // e^{f - m_blk}
+        float cf = cfe;
+        const bool v_zero = KV8 && vs == 0.f;  // this block's V is zero: nothing to add
+        if (KV8 && use && !v_zero) {            // move this row's A into the block's V-scale frame
+            cf *= vs_frame / vs;
+            vs_frame = vs;
+        }
+
+        // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e -
+        // m_blk*log2e)); a skipped block (use false) gives p = 0 ----
+        const float mb2 = use ? mb * kLog2e : INFINITY;
+        const float sc2 = sc * kLog2e;
+        u32x2_t pa[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
+            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
+        }
+        m_run = mnew;
+        if (use) f_run = mb;
+
+        // ---- rescale A (and its row sums) to the new frame (rows 4qd+e live
+        // in lane 4qd+e's factors) ----
+        {
+            f32x4_t cv, cl;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                cv[e] = __shfl(cf, 4 * qd + e, 64);
+                cl[e] = KV8 ? __shfl(cfe, 4 * qd + e, 64) : cv[e];
+            }
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
+            lacc *= cl;
+        }
+        // row sums of the rounded p (every column of P x ones is the sum),
+        // also for a block whose V adds nothing
+#pragma unroll
+        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
+
+        // ---- PV: A += P * V ----
+        const int vvalid = (blk_bad || v_zero) ? 0 : min(BS, ctx - blk0);  // tokens with defined V
+        // V rows past the context's end (and of an out-of-pool block) are
+        // zeroed once, under one wave-uniform branch ahead of PV, where the
+        // selects would run on every block. The K-through-LDS kernel keeps
+        // them in PV, which measured faster there (cfg2: 112.5 against
+        // 113.2 us per step; fp8 63.1 against 62.8 the other way).
+        constexpr bool kZeroAhead = !KLDS;
+        if (kZeroAhead && vvalid < BS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= vvalid)
+#pragma unroll
+                        for (int ds = 0; ds < DVS; ++ds) {
+                            if constexpr (KV8)
+                                vrw[t][ds][e] = (u32x2_t){0u, 0u};
+                            else
+                                vr[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                        }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (KV8 && v_zero) break;  // wave-uniform: the block adds nothing
+            u32x4_t vt4[DVS][4];       // 8 bf16 dims of tokens 16t + 4qd + e
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (KV8)
+                        vt4[ds][e] = fp8x8_to_bf16x8(vrw[t][ds][e][0], vrw[t][ds][e][1]);
+                    else
+                        vt4[ds][e] = vr[t][ds][e];
+                }
+            if (!kZeroAhead && vvalid < BS) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= vvalid)
+#pragma unroll
+                        for (int ds = 0; ds < DVS; ++ds) vt4[ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int w = jj >> 1;
+                    const unsigned a0 = vt4[ds][0][w], a1 = vt4[ds][1][w];
+                    const unsigned a2 = vt4[ds][2][w], a3 = vt4[ds][3][w];
+                    // the bf16 of dim 2w + (jj & 1) of tokens (0, 1) and (2, 3):
+                    // low halves (bytes 0-1 of each) or high halves (bytes 2-3),
+                    // one v_perm_b32 each (bytes 0-3 from the second operand,
+                    // 4-7 from the first)
+                    constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                    const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                    const unsigned d0 = __builtin_amdgcn_perm(a1, a0, sel);
+                    const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
+                    acc[ds][jj] = Elem<ET>::mma16(pa[t], (u32x2_t){d0, d1}, acc[ds][jj]);
+                }
+        }
+    };
+
+    // Per block i: V(i) is issued first, then QK(i) consumes K(i) (issued
+    // during block i-1), then K(i+1) is issued (with K staged through LDS: as
+    // soon as K(i) is in LDS, before QK(i)), then softmax and PV(i). The
+    // scheduling barriers keep the compiler from sinking loads past the math,
+    // which would serialise the memory latency. The segment's last block is
+    // peeled off (no K(i+1)): with the prefetch under a run-time condition the
+    // compiler's wait counts would have to cover the path without it, so PV(i)
+    // would wait for K(i+1) as well.
+    bool bad = false;
+    int phys = checked(bt_row[blk_begin], bad);
+    load_k(kreg, phys, blk_begin);
+    auto step = [&](const int blk, auto has_next) {
+        constexpr bool NEXT = decltype(has_next)::value;
+        const bool blk_bad = bad;
+        const int phys_b = phys;
+        const int raw_next = NEXT ? bt_row[blk + 1] : 0;  // in flight during this block's loads
+        __builtin_amdgcn_sched_barrier(0);
+        // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
+        // block's loads together lets the caches serve the second request.
+        if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
+        load_v(vreg, vraw, phys_b, blk);
+        auto stage_k_and_prefetch = [&] {
+            if constexpr (KLDS) {
+                // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
+                wave_lds_sync();
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) lds_st16(klds, t * 4096 + kw_off[e], kreg[t][e]);
+                wave_lds_sync();
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (NEXT) {
+                    phys = checked(raw_next, bad);
+                    load_k(kreg, phys, blk + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        auto prefetch_k = [&] {
+            if constexpr (!KLDS && NEXT) {
+                phys = checked(raw_next, bad);
+                load_k(kreg, phys, blk + 1);
+            }
+        };
+        compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k);
+    };
+    for (int blk = blk_begin; blk + 1 < blk_end; ++blk) step(blk, std::true_type{});
+    step(blk_end - 1, std::false_type{});
+
+    // ---- finish: O = e^{f-m} A and l = e^{f-m} L, in the frame of m ----
+    const float oscl = __expf(f_run - m_run);  // row pc's
+    const float osc = oscl * vs_frame;
+    float l_e[4], o_e[4];  // rows 4qd+e
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        l_e[e] = lacc[e] * __shfl(oscl, 4 * qd + e, 64);
+        o_e[e] = __shfl(osc, 4 * qd + e, 64);
+    }
+    // row pc's l: element pc % 4 of the lanes of group pc / 4
+    float l_tot;
+    {
+        float lr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lr[e] = __shfl(l_e[e], 16 * (pc >> 2) + pc, 64);
+        const int ep = pc & 3;
+        l_tot = ep == 0 ? lr[0] : ep == 1 ? lr[1] : ep == 2 ? lr[2] : lr[3];
+    }
+
+    if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 4 * qd + e;
+            if (row >= rows_here) continue;
+            const int64_t off = out_row_offset(P, b, kvh, rt * 16 + row, DV);
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds) {
+                if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
+                float v[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) v[jj] = l_e[e] > 0.f ? (o_e[e] * acc[ds][jj][e]) / l_e[e] : 0.f;
+                OutStore<OutT>::store8(P.out, off + 128 * ds + 8 * pc, v);
+            }
+        }
+        return;
+    }
+
+    // ---- a piece of the tile: partial (O relative to m, plus m and l) ----
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int row = 4 * qd + e;
+        if (row >= rows_here) continue;
+#pragma unroll
+        for (int ds = 0; ds < DVS; ++ds) {
+            if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
+            float *dst = part_o + row * DV + 128 * ds + 8 * pc;
+            *reinterpret_cast<f32x4_t *>(dst) =
+                (f32x4_t){acc[ds][0][e], acc[ds][1][e], acc[ds][2][e], acc[ds][3][e]} * o_e[e];
+            *reinterpret_cast<f32x4_t *>(dst + 4) =
+                (f32x4_t){acc[ds][4][e], acc[ds][5][e], acc[ds][6][e], acc[ds][7][e]} * o_e[e];
+        }
+    }
+    if (qd == 0) {
+        part_ml[pc] = m_run;
+        part_ml[16 + pc] = l_tot;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Main kernel: one wavefront per wave slot, one equal slice of the work each
+// ---------------------------------------------------------------------------
+
+// MAXW = 1: one wave per worker (one row tile per kv head); MAXW = 4: up to
+// four sibling waves, one per row tile, walk the same KV blocks, so V is loaded
+// through the caches (the siblings hit each other's lines) rather than
+// streamed past them.
+template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16>
+__global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
+    static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
+    static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
+    // single-tile bf16 workers with 128-dim heads stage K through LDS
+    constexpr bool KLDS = MAXW == 1 && !KV8 && DK == 128;
+    __shared__ __attribute__((aligned(16))) char klds[KLDS ? BS * 256 : 16];
+    flag_bad_lengths(P);
+    const int w = blockIdx.x;
+    const int wave = MAXW == 1 ? 0 : (int)(threadIdx.x >> 6);
+    const int tpb = lane_tiles(P);
+    const int list = w % P.lanes;
+    int start = 0, end = 0, b = 0, prefix = 0;
+    locate_slice(P, w / P.lanes, &start, &end, &b, &prefix);
+    // wave-uniform values (cross-lane results), kept in scalar registers so that
+    // block-table and scale reads derived from them are scalar loads
+    start = __builtin_amdgcn_readfirstlane(start);
+    end = __builtin_amdgcn_readfirstlane(end);
+    b = __builtin_amdgcn_readfirstlane(b);
+    prefix = __builtin_amdgcn_readfirstlane(prefix);
+    if (start >= end) return;
+    int ctx = __builtin_amdgcn_readfirstlane(ctx_of(P, b));  // the segment's sequence, read once
+    int nb = (ctx + BS - 1) / BS;
+    if (nb == 0) return;  // not reached: the batch holding `start` has work
+    const int rel = start - prefix;
+    int j = rel / nb;
+    int blk = rel - j * nb;
+    int pos = start;
+    int slot = 0;
+    while (pos < end && nb > 0) {
+        const int seg = min(end - pos, nb - blk);
+        const int jt = list * tpb + j;  // tile of the batch
+        const int kvh = jt / P.row_groups, rg = jt - kvh * P.row_groups;
+        const int rt = rg * P.tiles_per_worker + wave;  // this wave's row tile
+        // A worker touches at most two tiles partially: the first and the last
+        // of its slice (slots 0 and 1); tiles in between are finished here.
+        const int64_t piece = ((int64_t)w * P.tiles_per_worker + wave) * 2 + slot;
+        float *po = P.part_o + piece * 16 * DV;
+        float *pml = P.part_ml + piece * 32;
+        // every wave of the group has a row tile: all run the same blocks, so
+        // a per-block barrier among them is matched
+        const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
+        if (rt < P.row_tiles)
+            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml,
+                                                                     MAXW > 1 && full_group, klds);
+        pos += seg;
+        slot = 1;
+        if (pos >= end) break;
+        blk = 0;
+        if (++j == tpb) {
+            j = 0;
+            do {
+                ++b;
+                ctx = __builtin_amdgcn_readfirstlane(ctx_of(P, b));
+                nb = (ctx + BS - 1) / BS;
+            } while (nb == 0 && b + 1 < P.batch);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Merge kernel: one workgroup per tile; log-sum-exp merge of the pieces
+// (pa_kernel.cce:1666-1773 CombineScale), and zeros for empty contexts.
+// ---------------------------------------------------------------------------
+
+// Threads per merge workgroup: one 16-byte unit of a tile's 16 x DV output per
+// thread up to DV = 128 (512 threads), four per thread for MLA's DV = 512.
+template <int DV> constexpr int merge_threads() { return DV * 4 < 512 ? (DV * 4 < 64 ? 64 : DV * 4) : 512; }
+constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weights
+
+template <int DV, typename OutT>
+__global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const KernelParams P) {
+    constexpr int MT = merge_threads<DV>();
+    constexpr int UNITS = 16 * (DV / 4);            // 16-byte units of a full tile
+    constexpr int UPT = (UNITS + MT - 1) / MT;      // units per thread
+    constexpr int PRE = UPT == 1 ? 8 : 4;           // pieces per unit read before the weights are known
+    const int tid = threadIdx.x;
+    // The main kernel is done: hand its error word to the host through
+    // pinned memory (a run's wait then needs no device-to-host copy).
+    if (P.err_mirror && blockIdx.x == 0 && tid == 0)
+        __hip_atomic_store(P.err_mirror, __hip_atomic_load(P.error_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int tpb = P.kv_heads * P.row_tiles;
+    const int tile = blockIdx.x;  // (batch, kv head, row tile)
+    const int b = tile / tpb, jr = tile - b * tpb;
+    const int kvh = jr / P.row_tiles, rt = jr - kvh * P.row_tiles;
+    const int rg = rt / P.tiles_per_worker, wave = rt - rg * P.tiles_per_worker;
+    const int jt = kvh * P.row_groups + rg;  // tile of the batch in the work lists
+    const int list = jt / lane_tiles(P), j = jt - list * lane_tiles(P);
+    const int rows_here = min(16, P.rows - rt * 16);
+    int prefix = 0;
+    const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
+    const int nb = blocks_of(P, b);
+    if (nb == 0) {  // empty context: defined as a zero output
+        for (int idx = tid; idx < rows_here * (DV / 4); idx += MT) {
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+            OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4,
+                                   (f32x4_t){0.f, 0.f, 0.f, 0.f});
+        }
+        return;
+    }
+    const int per_list = max(P.workers / P.lanes, 1);
+    const int chunk = (total + per_list - 1) / per_list;
+    const int t0 = prefix + j * nb;
+    const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;  // slices of the list
+    if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
+    // Log-sum-exp over the pieces: the row max and total l from the (m, l)
+    // pairs first, then O = sum_w e^{m_w - M} O_w / L, whose piece loads do not
+    // depend on each other and stay in flight together.
+    auto piece_of = [&](int c) -> int64_t {
+        const int slot = (c * chunk >= t0) ? 0 : 1;
+        const int64_t w = (int64_t)c * P.lanes + list;  // the worker that ran slice c
+        return (w * P.tiles_per_worker + wave) * 2 + slot;
+    };
+    const int np = w_last - w_first + 1;
+    if (np <= kMergeLdsPieces) {
+        // Per-(row, piece) weights e^{m_w - M} / L once per workgroup, then the
+        // partial rows stream through with no dependent loads in the way. Every
+        // unit of the thread has its first PRE pieces read together with the
+        // (m, l) loads: they do not depend on the weights, so the merge is one
+        // memory round trip after the work scan, not one per unit.
+        __shared__ float wgt[16][kMergeLdsPieces];  // m of each (row, piece), then its weight
+        __shared__ float lsum[16][kMergeLdsPieces];
+        const int units = rows_here * (DV / 4);
+        f32x4_t pre[UPT][PRE];
+#pragma unroll
+        for (int u = 0; u < UPT; ++u) {
+            const int idx = tid + u * MT;
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+#pragma unroll
+            for (int k = 0; k < PRE; ++k)
+                pre[u][k] = (idx < units && k < np)
+                                ? *reinterpret_cast<const f32x4_t *>(P.part_o + (piece_of(w_first + k) * 16 + row) * DV +
+                                                                     4 * c4)
+                                : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
+        for (int e = tid; e < 16 * np; e += MT) {  // all (m, l) loads in flight at once
+            const int row = e / np, k = e - row * np;
+            const int64_t pc = piece_of(w_first + k);
+            wgt[row][k] = P.part_ml[pc * 32 + row];
+            lsum[row][k] = P.part_ml[pc * 32 + 16 + row];
+        }
+        __syncthreads();
+        if (tid < 16) {
+            float M = -INFINITY;
+            for (int k = 0; k < np; ++k) M = fmaxf(M, wgt[tid][k]);
+            float L = 0.f;
+            for (int k = 0; k < np; ++k) {
+                const float c = __expf(wgt[tid][k] - M);
+                wgt[tid][k] = c;
+                L += c * lsum[tid][k];
+            }
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            for (int k = 0; k < np; ++k) wgt[tid][k] *= inv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < UPT; ++u) {
+            const int idx = tid + u * MT;
+            if (idx >= units) break;
+            const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+            f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < PRE; ++k)
+                if (k < np) o += wgt[row][k] * pre[u][k];
+#pragma unroll 4
+            for (int k = PRE; k < np; ++k) {
+                const int64_t piece = piece_of(w_first + k);
+                o += wgt[row][k] * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
+            }
+            OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, o);
+        }
+        return;
+    }
+    for (int idx = tid; idx < rows_here * (DV / 4); idx += MT) {
+        const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
+        float M = -INFINITY;
+        for (int w = w_first; w <= w_last; ++w) M = fmaxf(M, P.part_ml[piece_of(w) * 32 + row]);
+        float L = 0.f;
+        f32x4_t o = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int w = w_first; w <= w_last; ++w) {
+            const int64_t piece = piece_of(w);
+            const float c = __expf(P.part_ml[piece * 32 + row] - M);
+            L += c * P.part_ml[piece * 32 + 16 + row];
+            o += c * *reinterpret_cast<const f32x4_t *>(P.part_o + (piece * 16 + row) * DV + 4 * c4);
+        }
+        const f32x4_t res = L > 0.f ? o / L : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        OutStore<OutT>::store4(P.out, out_row_offset(P, b, kvh, rt * 16 + row, DV) + 4 * c4, res);
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// MLA decode: one latent KV head shared by every query head (Hkv = 1 in the
+// DeepSeek shape, Dk = 576, Dv = 512), V = the first Dv dims of K.
+//
+// A worker workgroup of four waves owns 64 query rows (a "row group", 16 rows
+// per wave). Each KV block is copied from HBM into LDS with direct
+// global->LDS loads (double buffered: the next block is in flight during the
+// math on this one) and consumed by the four waves. The row groups of one
+// work slice run as sibling workgroups whose ids differ by multiples of 8, so
+// they land on the same XCD and the second reader of a block hits its L2.
+// Q (Dk/32 operand quads) and O^T (Dv x 16 rows, fp32) stay in registers:
+//   QK  S^T[token][row] = K[token][:] . Q[row][:]   MFMA 16x16x32 bf16,
+//       A = K rows from LDS (16-B reads), B = Q registers.
+//   PV  O^T[dim][row] += V^T[dim][token] . P^T[token][row]   MFMA 16x16x32,
+//       A = V^T from LDS by transposing reads (ds_read_b64_tr_b16),
+//       B = P^T, which is the QK result layout itself: lane l holds row l%16
+//       and, per 32-token k-step, tokens {4q..4q+3, 16+4q..16+4q+3}
+//       (q = l/16); the V^T reads pick the same token order.
+// Every lane of O^T holds a single query row, so the per-block rescale is one
+// scalar per lane. Numerics are the same per-block recipe as the decode kernel.
+//
+// LDS row layout: a token's Dk*2 bytes as 16-byte chunks, the row padded to a
+// chunk count = 10 (mod 16): 74 chunks (1184 B) for Dk = 576. Measured on
+// MI355X with the kernel's exact access patterns, that stride runs both the
+// K-operand reads (16 rows x 16 B per 16 lanes) and the transposing V^T reads
+// at full LDS speed (534-548 and 420-427 B/ns per CU), where 73, 76 and 77
+// chunks, with or without XOR swizzles of the chunk index, halve one of them.
+// ---------------------------------------------------------------------------
+
+template <int DK>
+struct MlaLayout {
+    static constexpr int kChunks = DK / 8;                                           // 16-B chunks per token
+    static constexpr int kRowChunks = kChunks + ((10 - kChunks % 16) % 16 + 16) % 16;  // = 10 (mod 16)
+    static constexpr int kRowBytes = kRowChunks * 16;
+};
+
+__device__ __forceinline__ i16x4_t lds_ld_tr(const char *base, uint32_t off) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4_t *)((LDS_AS char *)base + off));
+}
+
+constexpr int kMlaRowsPerGroup = 64;  // four waves x 16 rows
+
+// LDS exchange area of the MLA workgroup: P^T operands of the four waves'
+// rows ([wave][k-step][lane] x 16 B), then 2 x 64 per-row floats.
+template <int BS>
+struct MlaExchange {
+    static constexpr int kPBytes = 4 * (BS / 32) * 64 * 16;
+    static constexpr int kBytes = kPBytes + 2 * 64 * 4;
+};
+
+__device__ __forceinline__ void lds_stf(char *base, uint32_t off, float v) {
+    *reinterpret_cast<LDS_AS float *>((LDS_AS char *)base + off) = v;
+}
+
+__device__ __forceinline__ float lds_ldf(const char *base, uint32_t off) {
+    return *reinterpret_cast<const LDS_AS float *>((const LDS_AS char *)base + off);
+}
+
+// Workgroup barrier that orders LDS accesses only: the block fill and L2
+// prefetch loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Work slice and row group of workgroup w. Row groups of a slice are
+// w, w+8, w+16, ...: the same XCD under round-robin workgroup dispatch.
+__device__ __forceinline__ void mla_worker(int w, int slices, int groups, int *slice, int *group) {
+    const int full = slices / 8;  // complete sets of 8 slices
+    const int per_set = 8 * groups;
+    const int set = w / per_set;
+    if (set < full) {
+        *slice = set * 8 + (w & 7);
+        *group = (w / 8) % groups;
+    } else {
+        const int rem = slices - full * 8;  // > 0 here
+        const int x = w - full * per_set;
+        *slice = full * 8 + x % rem;
+        *group = x / rem;
+    }
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer loads straight into LDS (lane l -> LDS base + size*l). Lanes whose
+// offset is at or past the descriptor's record count are not fetched and
+// write zeros. Issued as inline asm on purpose: the compiler's wait
+// insertion would otherwise treat every later LDS read (the transposing reads
+// in particular) as possibly aliasing the fill and wait for all outstanding
+// vector memory before it, which serialises the next block's fill with this
+// block's math. Completion is instead awaited explicitly (s_waitcnt vmcnt at
+// the block barrier); loads the compiler does not count can only make its
+// own vmcnt waits stricter, since vector memory completes in order.
+// m0 holds the wave's LDS destination; nothing else in these kernels uses it.
+// One wait state separates the m0 write from the LDS-DMA load that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_fill16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_fill4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr_of(const char *p) {
+    return (uint32_t)(uintptr_t)(const LDS_AS char *)p;
+}
+
+// Raw buffer descriptor (stride 0, num_records in bytes). The values are
+// wave-uniform; readfirstlane puts them in scalar registers so the load needs
+// no per-lane descriptor loop.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t num_records) {
+    const uint64_t a = (uint64_t)base;
+    return (i32x4_t){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                     __builtin_amdgcn_readfirstlane((int)num_records), 0x00020000};
+}
+
+template <int BS, int DK, int DV, typename OutT>
+__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
+                                                const int groups, const int b, const int kvh, const int nblk,
+                                                const int blk_begin, const int blk_end, const int slot,
+                                                char *const smem0, char *const smem1, char *const sink,
+                                                char *const pexch) {
+    using L = MlaLayout<DK>;
+    constexpr int RB = L::kRowBytes;
+    constexpr int RC = L::kRowChunks;
+    constexpr int KC = L::kChunks;
+    constexpr int NI = BS * RC / 64;  // 1 KB direct-to-LDS loads per block
+    constexpr int NII = (NI + 3) / 4; // of which each wave issues at most NII
+    constexpr int KS = DK / 32;       // QK k-steps
+    constexpr int NT = BS / 16;       // 16-token tiles
+    constexpr int PS = BS / 32;       // PV k-steps
+    constexpr int NC = DV / 16;       // O^T column tiles
+    static_assert(BS % 32 == 0 && (BS * RC) % 64 == 0, "block of whole 32-token k-steps");
+    static_assert(DK % 32 == 0 && DV % 32 == 0 && DV <= DK, "V is a prefix of K");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int q = lane >> 4, pc = lane & 15;
+    const int r0 = rgrp * kMlaRowsPerGroup + 16 * wave;  // first query row of this wave
+    const int rows_here = min(16, P.rows - r0);
+    const bool active = rows_here > 0;
+    int ctx = P.context_lens[b];
+    ctx = min(max(ctx, 0), P.max_blocks * BS);
+
+    // ---- Q (B operand of QK): row pc, dims 32kk+8q..+7 ----
+    u32x4_t qv[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+    int rowlen = 0;
+    if (pc < rows_here) {
+        const int r = r0 + pc;
+        const int i = r / P.group, hh = r - i * P.group;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK + 8 * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) qv[kk] = ld16(qrow + 32 * kk);
+        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+    }
+    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - r0 / P.group) : ctx;
+
+    // Block-table entries are read through the scalar cache (constant
+    // address space): the load is counted by lgkmcnt, so waiting for it never
+    // waits for the vector-memory loads in flight (block fill, L2 prefetch).
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
+    auto phys_of = [&](int blk, bool &bad) -> int {
+        const int phys = bt_row[blk];
+        bad = (unsigned)phys >= (unsigned)P.num_pool_blocks;
+        return bad ? 0 : phys;
+    };
+
+    // ---- direct-to-LDS fill: LDS chunk p = 64*i + lane holds token p / RC,
+    // chunk p % RC. The per-lane byte offsets within a KV block
+    // are the same for every block; pad chunks re-read chunk 0 of their token.
+    // The descriptor's record count (valid tokens x token bytes, 0 for an
+    // out-of-pool block) makes every later token read zeros. ----
+    const uint32_t tok_b = (uint32_t)(P.k_token_stride * 2);  // block bytes < 2^31 (host-checked)
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
+    uint32_t voff[NII];
+#pragma unroll
+    for (int ii = 0; ii < NII; ++ii) {
+        const int pch = 64 * (4 * ii + wave) + lane;
+        const int row = pch / RC, pos = pch - row * RC;
+        voff[ii] = (uint32_t)row * tok_b + (pos < KC ? (uint32_t)pos << 4 : 0u);
+    }
+    // ---- L2 prefetch two blocks ahead: this row group's share of the block's
+    // 128-byte lines (tokens r with r % groups == rgrp), each touched by one
+    // 4-byte load into a scratch LDS slot, so the block's later fill is an L2
+    // hit for both row groups. Tokens past the context are not fetched. ----
+    constexpr int LPR = (DK * 2 + 127) / 128;  // lines per token
+    constexpr int NPF = (BS * LPR + 255) / 256;
+    // Every lane issues all NPF loads (lanes without a line of their own touch
+    // the group's first line again), so each wave has exactly NPF prefetch
+    // loads outstanding after its block fill: see the barrier below.
+    uint32_t pfoff[NPF];
+#pragma unroll
+    for (int pi = 0; pi < NPF; ++pi) {
+        const int idx = pi * 256 + (int)threadIdx.x;
+        const int rl = idx / LPR, ln = idx - rl * LPR;
+        const int row = rl * groups + rgrp;
+        pfoff[pi] = row < BS ? (uint32_t)row * tok_b + 128u * ln : (uint32_t)rgrp * tok_b;
+    }
+    auto prefetch = [&](int blk) {
+        bool bad = false;
+        const int phys = phys_of(blk, bad);
+        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
+        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
+        const uint32_t sink_addr = lds_addr_of(sink);
+#pragma unroll
+        for (int pi = 0; pi < NPF; ++pi) lds_fill4(rsrc, pfoff[pi], sink_addr);
+    };
+    auto issue = [&](int blk, char *dst) -> bool {
+        bool bad = false;
+        const int phys = phys_of(blk, bad);
+        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
+        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
+        const uint32_t dst_addr = lds_addr_of(dst) + 1024u * wave;
+#pragma unroll
+        for (int ii = 0; ii < NII; ++ii) {
+            const int i = 4 * ii + wave;
+            if (NI % 4 == 0 || i < NI) lds_fill16(rsrc, voff[ii], dst_addr + 4096u * ii);
+        }
+        return bad;
+    };
+
+    // O^T accumulators and the row-sum tile (ones x P^T: every lane holds its
+    // row's sum), both in the frame of the latest used block max f.
+    // PV's output dims are split across the four waves: wave w accumulates
+    // O^T column tiles NCW*w .. NCW*w + NCW-1 (dims 16 c ..) for the four row
+    // tiles of the workgroup (acc[cl][r]), so each wave reads a quarter of V^T
+    // from LDS; the P^T operands of all four row tiles come through pexch.
+    constexpr int NCW = NC / 4;
+    f32x4_t acc[NCW][4];
+#pragma unroll
+    for (int c = 0; c < NCW; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[c][r] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegClamp, f_run = kNegClamp;
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    constexpr float kLog2e = 1.4426950408889634f;
+
+    // per-lane LDS byte offsets within a block buffer
+    const uint32_t kofs = pc * RB + 16 * q;
+    const uint32_t vbase = (4 * q + (pc >> 2)) * RB + 8 * (pc & 1);
+    const uint32_t vofs_even = vbase + 16 * ((pc & 3) >> 1);
+    const uint32_t vofs_odd = vofs_even + 32;
+
+    // Scheduling: LDS reads are issued two stages ahead of the MFMAs that
+    // consume them (an LDS read takes longer than one stage of MFMAs), and the
+    // group barriers pin the order of reads, VALU work and MFMAs in a stage.
+    constexpr int kDsRead = 0x100, kValu = 0x002, kMfma = 0x008;
+    auto compute = [&](const char *kb, int blk, bool blk_bad) {
+        const bool first = (blk == blk_begin);
+        // ---- QK: stage = one 32-dim k-step over the NT token tiles ----
+        f32x4_t s[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) s[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        u32x4_t kf[3][NT];
+        auto load_k = [&](int kk, u32x4_t (&dst)[NT]) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) dst[t] = lds_ld16(kb, kofs + 64 * kk + t * 16 * RB);
+        };
+        load_k(0, kf[0]);
+        load_k(1, kf[1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            if (kk + 2 < KS) load_k(kk + 2, kf[(kk + 2) % 3]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kk % 3][t]),
+                                                              __builtin_bit_cast(bf16x8_t, qv[kk]), s[t], 0, 0, 0);
+            if (kk + 2 < KS) __builtin_amdgcn_sched_group_barrier(kDsRead, NT, 0);
+            __builtin_amdgcn_sched_group_barrier(kMfma, NT, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // ---- PV operand reads for the first two stages go out before the
+        // softmax math (they do not depend on it) ----
+        constexpr int NSC = NCW / 2;  // PV stages of two of this wave's O^T column tiles
+        i16x4_t vf[3][2][PS][2];
+        auto load_v = [&](int sc, i16x4_t (&dst)[2][PS][2]) {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const uint32_t co = (cc ? vofs_odd : vofs_even) + 64 * (NSC * wave + sc);
+#pragma unroll
+                for (int u = 0; u < PS; ++u) {
+                    dst[cc][u][0] = lds_ld_tr(kb, co + u * 32 * RB);
+                    dst[cc][u][1] = lds_ld_tr(kb, co + u * 32 * RB + 16 * RB);
+                }
+            }
+        };
+        load_v(0, vf[0]);
+        load_v(1, vf[1]);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- mask, block max of s*scale (golden :145-165). For scale > 0 the
+        // max of the scaled scores is the scaled max; otherwise scale first ----
+        float sc = P.scale;
+        if (!(sc > 0.f)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
+        const int blk0 = blk * BS;
+        const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
+        if (!full) {
+            const int rvalid = blk_bad ? 0 : rowlen - blk0;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * q + e >= rvalid) s[t][e] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mb = fmaxf(mx * sc, kNegClamp);
+        // ---- online merge (aiv_online_update.cpp:183-207) in the block frame ----
+        const float mnew = first ? mb : fmaxf(m_run, mb);
+        const bool use = first || (mb >= mnew - kFrameGap);
+        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e - m_blk*log2e)) ----
+        const float mb2 = use ? mb * kLog2e : INFINITY;  // a skipped block gives p = 0
+        const float sc2 = sc * kLog2e;
+        u32x4_t pk[PS];
+#pragma unroll
+        for (int u = 0; u < PS; ++u) {
+            unsigned wv[4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2], sc2, -mb2));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2 + 1], sc2, -mb2));
+                    wv[2 * hf + e2] = pack_bf16x2(p0, p1);
+                }
+            pk[u] = (u32x4_t){wv[0], wv[1], wv[2], wv[3]};
+        }
+        m_run = mnew;
+        if (use) f_run = mb;
+        // l (sum of the rounded p) on the matrix unit: ones x P^T
+        lacc *= cf;
+#pragma unroll
+        for (int u = 0; u < PS; ++u)
+            lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8_t, pk[u]), lacc, 0, 0, 0);
+
+        // ---- hand this wave's P^T and per-row factor to the other waves ----
+#pragma unroll
+        for (int u = 0; u < PS; ++u) lds_st16(pexch, ((wave * PS + u) * 64 + lane) * 16, pk[u]);
+        if (q == 0) lds_stf(pexch, MlaExchange<BS>::kPBytes + (wave * 16 + pc) * 4, cf);
+        lds_barrier();
+        u32x4_t pb[4][PS];  // P^T of row tile r (wave r's rows), k-step u
+        float cfr[4];       // e^{f - m_blk} of row pc of row tile r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int u = 0; u < PS; ++u) pb[r][u] = lds_ld16(pexch, ((r * PS + u) * 64 + lane) * 16);
+            cfr[r] = lds_ldf(pexch, MlaExchange<BS>::kPBytes + (r * 16 + pc) * 4);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[0][r] *= cfr[r];
+            acc[1][r] *= cfr[r];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- A' = e^{f - m_blk} A + P V: stage sc = this wave's column tiles
+        // 2sc, 2sc+1 for the four row tiles; the next stage's tiles are rescaled
+        // between this stage's MFMAs ----
+#pragma unroll
+        for (int sc = 0; sc < NSC; ++sc) {
+            if (sc + 2 < NSC) load_v(sc + 2, vf[(sc + 2) % 3]);
+            if (sc + 1 < NSC) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[2 * sc + 2][r] *= cfr[r];
+                    acc[2 * sc + 3][r] *= cfr[r];
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                for (int u = 0; u < PS; ++u) {
+                    const bf16x8_t va = __builtin_bit_cast(
+                        bf16x8_t,
+                        __builtin_shufflevector(vf[sc % 3][cc][u][0], vf[sc % 3][cc][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[2 * sc + cc][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            va, __builtin_bit_cast(bf16x8_t, pb[r][u]), acc[2 * sc + cc][r], 0, 0, 0);
+                }
+            if (sc + 2 < NSC) __builtin_amdgcn_sched_group_barrier(kDsRead, 4 * PS, 0);
+#pragma unroll
+            for (int g2 = 0; g2 < 8 * PS; ++g2) {
+                __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+                if (sc + 1 < NSC) __builtin_amdgcn_sched_group_barrier(kValu, 32 / (8 * PS), 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- block loop: wait + barrier, fill the other buffer with the next
+    // block, prefetch the one after into L2, math on this one ----
+    // Vector memory ops complete in order. At the top of iteration blk this
+    // wave has outstanding: the fill of blk, then (if issued) the NPF prefetch
+    // loads of blk+1. Waiting for "at most NPF outstanding" therefore
+    // completes the fill and leaves the prefetch in flight; with no prefetch
+    // issued the wait is for zero. lgkmcnt(0): this wave's LDS reads of the
+    // buffer about to be refilled are done.
+    // s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    constexpr unsigned kWaitFillOnly = 0x0070u | ((unsigned)NPF & 15u) | (((unsigned)NPF >> 4) << 14);
+    constexpr unsigned kWaitAll = 0x0070u;  // vmcnt(0) expcnt(7) lgkmcnt(0)
+    static_assert(NPF < 64, "vmcnt range");
+    bool bad_cur = issue(blk_begin, smem0);
+    for (int blk = blk_begin; blk < blk_end; ++blk) {
+        const bool even = ((blk - blk_begin) & 1) == 0;
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk > blk_begin && blk + 1 < blk_end)  // prefetch of blk+1 was issued after the fill of blk
+            __builtin_amdgcn_s_waitcnt(kWaitFillOnly);
+        else
+            __builtin_amdgcn_s_waitcnt(kWaitAll);
+        __builtin_amdgcn_s_barrier();  // every wave's fill landed; the other buffer is free
+        __builtin_amdgcn_sched_barrier(0);
+        bool bad_next = false;
+        if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
+        if (blk + 2 < blk_end) prefetch(blk + 2);
+        if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, kErrBadBlock);
+        compute(even ? smem0 : smem1, blk, bad_cur);
+        bad_cur = bad_next;
+    }
+    __syncthreads();  // the buffers are refilled by the next segment; pexch is free
+
+    // ---- finish: O = e^{f-m} A, l = e^{f-m} L. The row factors live with the
+    // row's wave; every wave holds a quarter of every row's dims ----
+    const float osc = __expf(f_run - m_run);
+    const float l_tot = lacc[0] * osc;
+    if (q == 0) {
+        lds_stf(pexch, (wave * 16 + pc) * 4, osc);
+        lds_stf(pexch, 256 + (wave * 16 + pc) * 4, lacc[0]);
+    }
+    lds_barrier();
+    const bool whole = blk_begin == 0 && blk_end == nblk;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rows_r = min(16, P.rows - (rgrp * kMlaRowsPerGroup + 16 * r));
+        if (pc >= rows_r) continue;
+        const int row = rgrp * kMlaRowsPerGroup + 16 * r + pc;
+        if (whole) {
+            const float lr = lds_ldf(pexch, 256 + (r * 16 + pc) * 4);
+            const float inv = lr > 0.f ? 1.f / lr : 0.f;  // the frame factor cancels
+            const int64_t off = out_row_offset(P, b, kvh, row, DV) + 4 * q;
+#pragma unroll
+            for (int cl = 0; cl < NCW; ++cl)
+                OutStore<OutT>::store4(P.out, off + 16 * (NCW * wave + cl), acc[cl][r] * inv);
+        } else {
+            const float oscr = lds_ldf(pexch, (r * 16 + pc) * 4);
+            const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + r) * 2 + slot;
+            float *dst = P.part_o + (piece * 16 + pc) * DV + 4 * q;
+#pragma unroll
+            for (int cl = 0; cl < NCW; ++cl)
+                *reinterpret_cast<f32x4_t *>(dst + 16 * (NCW * wave + cl)) = acc[cl][r] * oscr;
+        }
+    }
+    if (!whole && active && pc < rows_here && q == 0) {
+        const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + wave) * 2 + slot;
+        P.part_ml[piece * 32 + pc] = m_run;
+        P.part_ml[piece * 32 + 16 + pc] = l_tot;
+    }
+}
+
+// Worker workgroup = four waves = one row group of one work slice. The work
+// list holds (batch, kv head, KV block) entries; every row group of a slice
+// walks the same entries.
+template <int BS, int DK, int DV, typename OutT>
+__global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
+    using L = MlaLayout<DK>;
+    __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
+    __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
+    __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
+    // P^T of every wave's rows and per-row factors, handed between the waves
+    __shared__ __attribute__((aligned(16))) char pexch[MlaExchange<BS>::kBytes];
+    flag_bad_lengths(P);
+    const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
+    int slice = 0, rgrp = 0;
+    mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
+    const int tpb = P.kv_heads;  // work-list tiles per batch
+    int start = 0, end = 0, b = 0, prefix = 0;
+    locate_slice(P, slice, &start, &end, &b, &prefix);  // identical in every wave
+    // wave-uniform values, kept in scalar registers
+    start = __builtin_amdgcn_readfirstlane(start);
+    end = __builtin_amdgcn_readfirstlane(end);
+    b = __builtin_amdgcn_readfirstlane(b);
+    prefix = __builtin_amdgcn_readfirstlane(prefix);
+    if (start >= end) return;
+    int nb = blocks_of(P, b);
+    if (nb == 0) return;
+    const int rel = start - prefix;
+    int kvh = rel / nb;
+    int blk = rel - kvh * nb;
+    int pos = start;
+    int slot = 0;
+    while (pos < end && nb > 0) {
+        const int seg = min(end - pos, nb - blk);
+        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0, smem1,
+                                          sink, pexch);
+        pos += seg;
+        slot = 1;
+        if (pos >= end) break;
+        blk = 0;
+        if (++kvh == tpb) {
+            kvh = 0;
+            do {
+                ++b;
+                nb = blocks_of(P, b);
+            } while (nb == 0 && b + 1 < P.batch);
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Kernel sets. Each set is instantiated in its own translation unit
+// (pa_kernels_*.hip); the host side picks kernels through these functions.
+// ---------------------------------------------------------------------------
+
+typedef void (*KernelFn)(KernelParams);
+
+constexpr int kMlaDk = 576, kMlaDv = 512;
+
+struct KernelPair {
+    KernelFn main;        // one wave per worker (MLA: the four-wave LDS kernel); null if unsupported
+    KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
+    bool mla;
+    bool klds;  // `main` stages K through LDS (full-row K reads)
+};
+
+struct MergeFn {
+    KernelFn fn;  // null if unsupported
+    int threads;  // workgroup size
+};
+
+// GQA decode with 16-bit query and caches of element type `dt` (the
+// SIMPLER_HIP_DT_BFLOAT16 or SIMPLER_HIP_DT_FLOAT16 code), Dk == Dv.
+KernelPair pick_gqa_bf16(int bs, int d, int out_dtype);
+KernelPair pick_gqa_f16(int bs, int d, int out_dtype);
+// GQA decode with fp8 E4M3FN caches (bf16 query), Dk == Dv == 128.
+KernelPair pick_gqa_fp8(int bs, int d, int out_dtype);
+// MLA (Dk 576, Dv 512, V a prefix of K), bf16.
+KernelPair pick_mla(int bs, int out_dtype);
+// The split merge for output width dv.
+MergeFn pick_merge(int dv, int out_dtype);
+
+}  // namespace pa
+}  // namespace simpler_hip

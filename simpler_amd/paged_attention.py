@@ -25,9 +25,11 @@ from .task_interface import ArgDirection, ChipCallable, CoreCallable, DataType
 
 NATIVE_CALLABLE_NAME = "simpler_hip_paged_attention_decode"
 
-_OUT_DTYPES = {torch.float32: int(DataType.FLOAT32), torch.bfloat16: int(DataType.BFLOAT16)}
-# fp8 KV caches (E4M3FN bytes, include/simpler_hip/pa_decode.h SIMPLER_HIP_KV_FP8_E4M3)
-KV_BF16, KV_FP8_E4M3 = 0, 1
+_OUT_DTYPES = {torch.float32: int(DataType.FLOAT32), torch.bfloat16: int(DataType.BFLOAT16),
+               torch.float16: int(DataType.FLOAT16)}
+# element formats of query and caches (include/simpler_hip/pa_decode.h SIMPLER_HIP_KV_*):
+# bf16, fp8 E4M3FN caches with a bf16 query, fp16
+KV_BF16, KV_FP8_E4M3, KV_FP16 = 0, 1, 2
 _FP8_DTYPES = (torch.float8_e4m3fn, torch.uint8)
 _ERRORS = {
     -1: "invalid argument (shape, dtype, stride or alignment)",
@@ -121,8 +123,11 @@ def make_args(
     ``float(cache[blk, t, h, d]) * scale[blk, h]``.
     """
     fp8 = key_cache.dtype in _FP8_DTYPES
-    kv_dtype = key_cache.dtype if fp8 else torch.bfloat16
-    _check(query, "query", torch.bfloat16, (3, 4))
+    fp16 = query.dtype == torch.float16
+    kv_dtype = key_cache.dtype if fp8 else (torch.float16 if fp16 else torch.bfloat16)
+    if fp8 and fp16:
+        raise ValueError("fp8 caches take a bfloat16 query")
+    _check(query, "query", torch.float16 if fp16 else torch.bfloat16, (3, 4))
     _check(key_cache, "key_cache", kv_dtype, (4,))
     _check(value_cache, "value_cache", kv_dtype, (4,))
     if fp8:
@@ -136,8 +141,9 @@ def make_args(
         raise ValueError("k_scale/v_scale apply to fp8 caches only")
     _check(block_table, "block_table", torch.int32, (2,))
     _check(context_lens, "context_lens", torch.int32, (1,))
-    if out.dtype not in _OUT_DTYPES:
-        raise ValueError(f"out must be float32 or bfloat16, got {out.dtype}")
+    allowed = (torch.float32, torch.float16) if fp16 else (torch.float32, torch.bfloat16)
+    if out.dtype not in allowed:
+        raise ValueError(f"out must be one of {allowed} for {query.dtype} inputs, got {out.dtype}")
     for name, t in (("query", query), ("block_table", block_table), ("context_lens", context_lens), ("out", out)):
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
@@ -175,6 +181,8 @@ def make_args(
     if fp8:
         a.kv_format = KV_FP8_E4M3
         a.k_scale, a.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
+    elif fp16:
+        a.kv_format = KV_FP16
     return a
 
 
@@ -221,8 +229,10 @@ def paged_attention_decode(
     """Fused paged-attention decode; returns ``out`` ``[B, (q_len,) Hq, Dv]``.
 
     ``scale`` defaults to ``1/sqrt(head_dim_k)``. The reference's orchestration
-    writes FLOAT32 output (``paged_attention_orch.cpp:130``); BFLOAT16 is also
-    accepted. ``value_cache`` may be a view of ``key_cache`` (MLA: V = K[..., :Dv]).
+    writes FLOAT32 output (``paged_attention_orch.cpp:130``); BFLOAT16 (bf16
+    inputs) or FLOAT16 (fp16 inputs) is also accepted. Query and caches are
+    bfloat16, or float16 (the reference's GQA cases). ``value_cache`` may be a
+    view of ``key_cache`` (MLA: V = K[..., :Dv], bf16).
     """
     if scale is None:
         scale = 1.0 / math.sqrt(query.shape[-1])
@@ -323,49 +333,60 @@ SPMD_INCORE_SIGNATURES = {
     1: [D.IN, D.IN, D.IN, D.IN, D.IN, D.INOUT, D.OUT, D.OUT, D.OUT],  # PA_AIV
 }
 
-# Every paged-attention CALLABLE the reference defines, as (incore signatures,
-# child order by func id). All share the orchestration signature and the
-# 7-argument contract, so each registers and runs on the fused kernel.
+# The high-performance SPMD callable: query, key_cache, value_cache,
+# block_table, out, eight workspaces, tiling, null (tests/st/a2a3/
+# tensormap_and_ringbuffer/spmd_paged_attention_highperf/
+# test_spmd_paged_attention_highperf.py:96-165); both halves of the mix task
+# declare the same payload. Lengths and scale travel in the tiling tensor.
+HIGHPERF_SIGNATURE = [D.IN, D.IN, D.IN, D.IN, D.OUT] + [D.IN] * 10
+HIGHPERF_INCORE_SIGNATURES = {0: HIGHPERF_SIGNATURE, 1: HIGHPERF_SIGNATURE}
+
+# Every paged-attention CALLABLE the reference defines, as (orchestration
+# signature, incore signatures, child order by func id). Each registers and
+# runs on the fused kernel.
 REFERENCE_CALLABLES = {
     # examples/a2a3/tensormap_and_ringbuffer/paged_attention/test_paged_attention.py:25-61
-    "paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "paged_attention": (ORCH_SIGNATURE, INCORE_SIGNATURES, [0, 1, 2, 3]),
     # examples/a2a3/tensormap_and_ringbuffer/paged_attention_manual_scope/test_paged_attention_manual_scope.py:25-61
-    "paged_attention_manual_scope": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "paged_attention_manual_scope": (ORCH_SIGNATURE, INCORE_SIGNATURES, [0, 1, 2, 3]),
     # examples/a2a3/tensormap_and_ringbuffer/paged_attention_ringbuffer/test_paged_attention_ringbuffer.py:34-66
     # (children listed as func ids 0, 2, 1, 3)
-    "paged_attention_ringbuffer": (INCORE_SIGNATURES, [0, 2, 1, 3]),
+    "paged_attention_ringbuffer": (ORCH_SIGNATURE, INCORE_SIGNATURES, [0, 2, 1, 3]),
     # tests/st/a2a3/tensormap_and_ringbuffer/batch_paged_attention/test_batch_paged_attention.py:25-61
-    "batch_paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "batch_paged_attention": (ORCH_SIGNATURE, INCORE_SIGNATURES, [0, 1, 2, 3]),
     # tests/st/a2a3/tensormap_and_ringbuffer/multi_round_paged_attention/test_multi_round_paged_attention.py:30-66
-    "multi_round_paged_attention": (INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "multi_round_paged_attention": (ORCH_SIGNATURE, INCORE_SIGNATURES, [0, 1, 2, 3]),
     # tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll/test_paged_attention_unroll.py:25-61
-    "paged_attention_unroll": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "paged_attention_unroll": (ORCH_SIGNATURE, UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
     # examples/a2a3/tensormap_and_ringbuffer/paged_attention_unroll_manual_scope/
     # test_paged_attention_unroll_manual_scope.py:25-61
-    "paged_attention_unroll_manual_scope": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "paged_attention_unroll_manual_scope": (ORCH_SIGNATURE, UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
     # tests/st/a2a3/tensormap_and_ringbuffer/paged_attention_unroll_4dims/test_paged_attention_unroll_4dims.py:32-64
     # (query and out as [B, 1, H, D], :120-122)
-    "paged_attention_unroll_4dims": (UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
+    "paged_attention_unroll_4dims": (ORCH_SIGNATURE, UNROLL_INCORE_SIGNATURES, [0, 1, 2, 3]),
     # tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention/test_spmd_paged_attention.py:28-54
-    "spmd_paged_attention": (SPMD_INCORE_SIGNATURES, [0, 1]),
+    "spmd_paged_attention": (ORCH_SIGNATURE, SPMD_INCORE_SIGNATURES, [0, 1]),
+    # tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention_highperf/test_spmd_paged_attention_highperf.py:96-165
+    "spmd_paged_attention_highperf": (HIGHPERF_SIGNATURE, HIGHPERF_INCORE_SIGNATURES, [0, 1]),
 }
 
+_FAMILY_OF_SIGS = {id(INCORE_SIGNATURES): "chain", id(UNROLL_INCORE_SIGNATURES): "unroll",
+                   id(SPMD_INCORE_SIGNATURES): "spmd", id(HIGHPERF_INCORE_SIGNATURES): "highperf"}
 # The family simpler_hip_callable_family reports for each
-REFERENCE_FAMILIES = {
-    name: ("unroll" if sigs is UNROLL_INCORE_SIGNATURES else "spmd" if sigs is SPMD_INCORE_SIGNATURES else "chain")
-    for name, (sigs, _) in REFERENCE_CALLABLES.items()
-}
+REFERENCE_FAMILIES = {name: _FAMILY_OF_SIGS[id(sigs)] for name, (_, sigs, _) in REFERENCE_CALLABLES.items()}
+# The callables whose arguments are the 7-argument form (every one but highperf)
+SEVEN_ARGUMENT_CALLABLES = sorted(n for n, f in REFERENCE_FAMILIES.items() if f != "highperf")
 
 
 def reference_callable(name: str, orch_binary: bytes = b"",
                        incore_binaries: dict[int, bytes] | None = None) -> ChipCallable:
     """The reference's CALLABLE ``name`` (a key of ``REFERENCE_CALLABLES``), with
-    its incore signatures and child order. Binaries are carried, not executed."""
-    sigs, order = REFERENCE_CALLABLES[name]
+    its signatures and child order. Binaries are carried, not executed."""
+    orch_sig, sigs, order = REFERENCE_CALLABLES[name]
     incore_binaries = incore_binaries or {}
     children = [(fid, CoreCallable.build(signature=sigs[fid], binary=incore_binaries.get(fid, b""))) for fid in order]
     return ChipCallable.build(
-        signature=ORCH_SIGNATURE,
+        signature=orch_sig,
         func_name="aicpu_orchestration_entry",
         binary=orch_binary,
         children=children,

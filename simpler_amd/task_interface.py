@@ -538,12 +538,12 @@ class ChipWorker:
             self._handles[hid] = slot
             return CallableHandle(hid, slot)
 
-    PA_FAMILIES = {0: "chain", 1: "unroll", 2: "spmd", 3: "native"}
+    PA_FAMILIES = {0: "chain", 1: "unroll", 2: "spmd", 3: "native", 4: "highperf"}
 
     def callable_family(self, handle: CallableHandle) -> str | None:
         """Which paged-attention callable family a registration matched
         (``simpler_hip_callable_family``): ``"chain"``, ``"unroll"``, ``"spmd"``,
-        ``"native"``, or ``None`` for a callable that is not paged attention."""
+        ``"native"``, ``"highperf"``, or ``None`` for a callable that is not paged attention."""
         slot = self._handles.get(handle._handle_id)
         if slot is None:
             raise KeyError("unknown callable handle")

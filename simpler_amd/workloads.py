@@ -101,8 +101,9 @@ class DecodeCase:
         return (*self.query.shape[:-1], self.config.head_dim_v)
 
 
-def _randn_bf16(shape, gen: torch.Generator) -> torch.Tensor:
-    return torch.randn(shape, generator=gen, dtype=torch.float32).to(torch.bfloat16)
+def _randn_bf16(shape, gen: torch.Generator, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """N(0, 1) drawn in fp32, rounded to ``dtype`` (bf16 unless stated)."""
+    return torch.randn(shape, generator=gen, dtype=torch.float32).to(dtype)
 
 
 FP8_MAX = 448.0  # largest finite E4M3FN value
@@ -182,8 +183,10 @@ def make_case(cfg: DecodeConfig | str, seed: int | None = None, *, ctx_override:
 def make_custom_case(*, batch: int, num_heads: int, kv_heads: int, head_dim: int, block_size: int,
                      context_lens: list[int], seed: int, q_len: int = 1, causal: bool = False,
                      head_dim_v: int | None = None, mla: bool = False, max_blocks: int | None = None,
-                     pool_extra: int = 0, scale: float | None = None, value_range: float | None = None) -> DecodeCase:
-    """Arbitrary-shape case (tests): same draw order, pool = blocks needed + ``pool_extra``."""
+                     pool_extra: int = 0, scale: float | None = None, value_range: float | None = None,
+                     dtype: torch.dtype = torch.bfloat16) -> DecodeCase:
+    """Arbitrary-shape case (tests): same draw order, pool = blocks needed + ``pool_extra``;
+    query and caches in ``dtype`` (bf16, or fp16 for the reference's GQA dtype)."""
     dv = head_dim_v or head_dim
     cfg = DecodeConfig("custom", -1, batch, num_heads, kv_heads, head_dim, dv, block_size,
                        min(context_lens), max(context_lens), q_len=q_len, causal=causal, mla=mla,
@@ -199,11 +202,11 @@ def make_custom_case(*, batch: int, num_heads: int, kv_heads: int, head_dim: int
         table[b, :n] = perm[off : off + n]
         off += n
     qshape = (batch, q_len, num_heads, head_dim) if q_len > 1 else (batch, num_heads, head_dim)
-    query = _randn_bf16(qshape, gen)
-    key = _randn_bf16((pool, block_size, kv_heads, head_dim), gen)
-    value = key[..., :dv] if mla else _randn_bf16((pool, block_size, kv_heads, dv), gen)
+    query = _randn_bf16(qshape, gen, dtype)
+    key = _randn_bf16((pool, block_size, kv_heads, head_dim), gen, dtype)
+    value = key[..., :dv] if mla else _randn_bf16((pool, block_size, kv_heads, dv), gen, dtype)
     if value_range is not None:
-        query, key = (query.float() * value_range).to(torch.bfloat16), (key.float() * value_range).to(torch.bfloat16)
+        query, key = (query.float() * value_range).to(dtype), (key.float() * value_range).to(dtype)
         if mla:
             value = key[..., :dv]
     return DecodeCase(cfg, seed, query, key, value, table, lens,
@@ -224,8 +227,10 @@ def make_reference_case(params: dict, seed: int) -> DecodeCase:
 
     ``params`` takes the reference's case keys (``batch``, ``num_heads``,
     ``kv_head_num``, ``head_dim``, ``block_size``, ``context_len``,
-    ``max_model_len``, optional ``context_lens_list``)."""
+    ``max_model_len``, optional ``context_lens_list`` and ``dtype``: "bfloat16"
+    or "float16")."""
     batch, hq, hkv = params["batch"], params["num_heads"], params["kv_head_num"]
+    dtype = getattr(torch, params.get("dtype", "bfloat16"))
     d, bs = params["head_dim"], params["block_size"]
     gen = torch.Generator("cpu").manual_seed(seed)
     lst = params.get("context_lens_list")
@@ -239,7 +244,7 @@ def make_reference_case(params: dict, seed: int) -> DecodeCase:
     table = torch.randint(0, max(total, 1), (batch, max_blocks), generator=gen, dtype=torch.int32)
 
     def uni(shape, lo, hi):
-        return (torch.rand(shape, generator=gen, dtype=torch.float32) * (hi - lo) + lo).to(torch.bfloat16)
+        return (torch.rand(shape, generator=gen, dtype=torch.float32) * (hi - lo) + lo).to(dtype)
 
     query = uni((batch, hq, d), -0.5, 0.5)
     key = uni((total, bs, hkv, d), -0.5, 0.5)
@@ -247,6 +252,65 @@ def make_reference_case(params: dict, seed: int) -> DecodeCase:
     cfg = DecodeConfig("reference", -1, batch, hq, hkv, d, d, bs, int(lens.min()), int(lens.max()),
                        max_blocks=max_blocks, out_dtype=torch.float32)
     return DecodeCase(cfg, seed, query, key, value, table, lens, 1.0)
+
+
+# Tiling-tensor layout of the reference's high-performance SPMD paged attention
+# (tests/st/a2a3/tensormap_and_ringbuffer/spmd_paged_attention_highperf/kernels/
+# pa_tiling.py:18-62,360-430): int32 header words, then per sequence
+# TILING_PARA_SIZE words, word 1 of which is its KV length.
+TILING_HEAD_SIZE, TILING_PARA_SIZE = 44, 17
+
+
+def highperf_tiling(*, batch: int, num_heads: int, kv_heads: int, head_dim: int, num_blocks: int, block_size: int,
+                    max_blocks: int, scale: float, kv_seq_lens: list[int]) -> torch.Tensor:
+    """The header and per-sequence words of the reference's tiling tensor that
+    describe the problem (batch, heads, head dim, blocks, scale, KV lengths);
+    the reference's core-split fields (which its own kernel reads to divide
+    work among AICores) are left 0."""
+    import struct
+
+    t = [0] * (TILING_HEAD_SIZE + batch * TILING_PARA_SIZE)
+    t[0], t[1], t[2], t[3], t[4], t[5] = batch, num_heads, head_dim, num_blocks, block_size, max_blocks
+    t[6] = struct.unpack("<i", struct.pack("<f", float(scale)))[0]  # TOR: the scale's fp32 bits
+    t[7] = kv_heads
+    t[17], t[18] = TILING_HEAD_SIZE, TILING_PARA_SIZE
+    t[22] = max(kv_seq_lens) if kv_seq_lens else 0  # max KV length
+    t[28] = batch  # decoder batch
+    t[29] = head_dim  # head dim of V
+    for b, n in enumerate(kv_seq_lens):
+        base = TILING_HEAD_SIZE + b * TILING_PARA_SIZE
+        t[base + 0] = 1  # query tokens
+        t[base + 1] = int(n)  # KV length
+        t[base + 3] = block_size
+        t[base + 8] = b
+    return torch.tensor(t, dtype=torch.int32)
+
+
+def make_highperf_case(params: dict, seed: int) -> tuple[DecodeCase, torch.Tensor]:
+    """Inputs drawn the way the reference's high-performance SPMD scene test
+    draws them (``test_spmd_paged_attention_highperf.py:28-54,289-347``),
+    seeded: query and dense K/V ~ N(0, 1) in ``dtype`` (float16), K/V packed
+    into a paged pool ``[B * L/BS, BS, Hkv, D]`` whose block table is the
+    identity assignment, every length ``kv_seq``, scale 1/sqrt(D). Returns the
+    case and its tiling tensor."""
+    batch, hq, hkv, d = params["batch"], params["num_heads"], params["num_kv_heads"], params["head_dim"]
+    seq, bs = params["kv_seq"], params["block_size"]
+    dtype = getattr(torch, params.get("dtype", "float16"))
+    gen = torch.Generator("cpu").manual_seed(seed)
+    query = torch.randn(batch, hq, d, generator=gen).to(dtype)
+    k_dense = torch.randn(batch, seq, hkv * d, generator=gen).to(dtype)
+    v_dense = torch.randn(batch, seq, hkv * d, generator=gen).to(dtype)
+    nblk = seq // bs
+    key = k_dense.reshape(batch * nblk, bs, hkv, d).contiguous()
+    value = v_dense.reshape(batch * nblk, bs, hkv, d).contiguous()
+    table = (torch.arange(nblk, dtype=torch.int32)[None, :] + torch.arange(batch, dtype=torch.int32)[:, None] * nblk)
+    lens = torch.full((batch,), seq, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(d)
+    cfg = DecodeConfig("highperf", -1, batch, hq, hkv, d, d, bs, seq, seq, max_blocks=nblk, out_dtype=dtype)
+    case = DecodeCase(cfg, seed, query, key, value, table.contiguous(), lens, scale)
+    tiling = highperf_tiling(batch=batch, num_heads=hq, kv_heads=hkv, head_dim=d, num_blocks=batch * nblk,
+                             block_size=bs, max_blocks=nblk, scale=scale, kv_seq_lens=[seq] * batch)
+    return case, tiling
 
 
 # ---------------------------------------------------------------------------

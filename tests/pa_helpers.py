@@ -31,7 +31,8 @@ def oracle_numpy(case) -> np.ndarray:
     return pa_oracle.paged_attention_decode(
         f32(case.query), f32(case.key_cache), None if c.mla else f32(case.value_cache),
         case.block_table.numpy(), case.context_lens.numpy(), case.scale, causal=c.causal,
-        v_dim=c.head_dim_v if c.mla else None)
+        v_dim=c.head_dim_v if c.mla else None,
+        p_dtype="fp16" if case.query.dtype == torch.float16 else "bf16")
 
 
 def oracle_c(case, n_threads: int | None = None) -> np.ndarray:

@@ -129,7 +129,7 @@ def test_every_reference_pa_callable_registers_with_its_family(name):
     try:
         assert lib.simpler_register_callable(ctx, 5, pa.reference_callable(name).address()) == 0
         fam = lib.simpler_hip_callable_family(ctx, 5)
-        assert {0: "chain", 1: "unroll", 2: "spmd"}[fam] == pa.REFERENCE_FAMILIES[name]
+        assert {0: "chain", 1: "unroll", 2: "spmd", 4: "highperf"}[fam] == pa.REFERENCE_FAMILIES[name]
     finally:
         lib.destroy_device_context(ctx)
 

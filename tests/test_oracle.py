@@ -189,3 +189,52 @@ def test_bf16_helpers_round_to_nearest_even():
     np.testing.assert_array_equal(pa_oracle.bf16_round(x)[:5], expect)
     t = torch.tensor(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(pa_oracle.bf16_round(x), t)
+
+
+# ---- fp16 inputs (the reference's GQA scene cases are fp16; the golden rounds p
+# to the input dtype, goldens/paged_attention.py:168) ----------------------------
+
+def test_p_is_rounded_to_fp16_for_fp16_inputs():
+    # s0 = 0 (block max), s1 = -0.2138671875 (exact in fp16): exp(s1) = 0.807455...
+    # rounds to 1654/2048 in fp16 (spacing 2^-11 on [0.5, 1)), so the output is
+    # (1654/2048) / (1 + 1654/2048) = 1654/3702, not the bf16 value 207/463.
+    q = np.zeros((1, 1, 16), np.float32)
+    q[0, 0, 0] = 1.0
+    k = np.zeros((1, 16, 1, 16), np.float32)
+    k[0, 1, 0, 0] = -0.2138671875
+    v = np.zeros((1, 16, 1, 16), np.float32)
+    v[0, 1, 0, 0] = 1.0
+    args = (q, k, v, np.zeros((1, 1), np.int32), np.array([2], np.int32), 1.0)
+    out16 = pa_oracle.paged_attention_decode(*args, p_dtype="fp16")
+    assert out16[0, 0, 0] == pytest.approx(1654.0 / 3702.0, abs=2e-7)
+    out_bf = pa_oracle.paged_attention_decode(*args)
+    assert out_bf[0, 0, 0] == pytest.approx(207.0 / 463.0, abs=2e-7)
+    unrounded = math.exp(-0.2138671875) / (1 + math.exp(-0.2138671875))
+    assert abs(out16[0, 0, 0] - unrounded) > 3e-5
+
+
+def test_fp16_round_matches_torch():
+    g = torch.Generator().manual_seed(5)
+    x = torch.cat([torch.randn(4096, generator=g), torch.randn(512, generator=g) * 1e-6,  # fp16 subnormals
+                   torch.tensor([1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 2 ** -24 * 0.5, 2 ** -24 * 1.5, 65504.0])])
+    got = pa_oracle.fp16_round(x.numpy())
+    want = x.to(torch.float16).float().numpy()
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["gqa", "gqa_bs128", "causal", "case_varseq4"])
+def test_fp16_oracle_matches_fp64_textbook(name):
+    case = make_custom_case(seed=8, dtype=torch.float16, **SMALL_CASES[name])
+    c = case.config
+    got = oracle_numpy(case)
+    ref = pa_oracle.attention_fp64(
+        case.query.float().numpy(), case.key_cache.float().numpy(), case.value_cache.float().numpy(),
+        case.block_table.numpy(), case.context_lens.numpy(), case.scale, causal=c.causal)
+    # fp16 rounding of p (relative 2^-11) is the only deviation from the textbook
+    assert_close(got, ref, max_abs=5e-3, rel_l2=1.5e-3, what=name)
+    assert np.max(np.abs(got - ref)) > 1e-8
+    # and it differs from the bf16-rounded recipe on the same values
+    bf = pa_oracle.paged_attention_decode(
+        case.query.float().numpy(), case.key_cache.float().numpy(), case.value_cache.float().numpy(),
+        case.block_table.numpy(), case.context_lens.numpy(), case.scale, causal=c.causal, p_dtype="bf16")
+    assert np.max(np.abs(got - bf)) > 1e-6
