@@ -374,6 +374,80 @@ __device__ __forceinline__ int64_t out_row_offset(const KernelParams &P, int b, 
 // One segment: KV blocks [blk_begin, blk_end) of tile (b, kvh, rt)
 // ---------------------------------------------------------------------------
 
+// End of a segment (rows of row tile rt of (b, kvh), blocks [blk_begin,
+// blk_end)): O = e^{f-m} A and l = e^{f-m} L in the frame of the running max m
+// (A in units of vs_frame for fp8 V), then either the final output (the
+// segment covers the whole tile) or the tile piece (O relative to m, m, l)
+// for the merge kernel. Lane (qd, pc) holds A's rows 4qd+e and the state of
+// row pc.
+template <int DV, typename OutT>
+__device__ __forceinline__ void finish_segment(const KernelParams &P, const int b, const int kvh, const int rt,
+                                               const int nblk, const int blk_begin, const int blk_end,
+                                               float *const part_o, float *const part_ml,
+                                               const f32x4_t (&acc)[(DV + 127) / 128][8], const f32x4_t lacc,
+                                               const float m_run, const float f_run, const float vs_frame) {
+    constexpr int DVS = (DV + 127) / 128;
+    const int lane = threadIdx.x & 63;
+    const int qd = lane >> 4;
+    const int pc = lane & 15;
+    const int rows_here = min(16, P.rows - rt * 16);
+    const float oscl = __expf(f_run - m_run);  // row pc's
+    const float osc = oscl * vs_frame;
+    float l_e[4], o_e[4];  // rows 4qd+e
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        l_e[e] = lacc[e] * __shfl(oscl, 4 * qd + e, 64);
+        o_e[e] = __shfl(osc, 4 * qd + e, 64);
+    }
+    // row pc's l: element pc % 4 of the lanes of group pc / 4
+    float l_tot;
+    {
+        float lr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lr[e] = __shfl(l_e[e], 16 * (pc >> 2) + pc, 64);
+        const int ep = pc & 3;
+        l_tot = ep == 0 ? lr[0] : ep == 1 ? lr[1] : ep == 2 ? lr[2] : lr[3];
+    }
+
+    if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 4 * qd + e;
+            if (row >= rows_here) continue;
+            const int64_t off = out_row_offset(P, b, kvh, rt * 16 + row, DV);
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds) {
+                if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
+                float v[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) v[jj] = l_e[e] > 0.f ? (o_e[e] * acc[ds][jj][e]) / l_e[e] : 0.f;
+                OutStore<OutT>::store8(P.out, off + 128 * ds + 8 * pc, v);
+            }
+        }
+        return;
+    }
+
+    // ---- a piece of the tile: partial (O relative to m, plus m and l) ----
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int row = 4 * qd + e;
+        if (row >= rows_here) continue;
+#pragma unroll
+        for (int ds = 0; ds < DVS; ++ds) {
+            if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
+            float *dst = part_o + row * DV + 128 * ds + 8 * pc;
+            *reinterpret_cast<f32x4_t *>(dst) =
+                (f32x4_t){acc[ds][0][e], acc[ds][1][e], acc[ds][2][e], acc[ds][3][e]} * o_e[e];
+            *reinterpret_cast<f32x4_t *>(dst + 4) =
+                (f32x4_t){acc[ds][4][e], acc[ds][5][e], acc[ds][6][e], acc[ds][7][e]} * o_e[e];
+        }
+    }
+    if (qd == 0) {
+        part_ml[pc] = m_run;
+        part_ml[16 + pc] = l_tot;
+    }
+}
+
 // KV8: K and V caches hold E4M3FN bytes with one fp32 scale per (block, kv
 // head). They are widened to bf16 in registers (exact) right before the
 // MFMAs. The K scale folds into the softmax scale. The V scale is carried as
@@ -762,62 +836,197 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     for (int blk = blk_begin; blk + 1 < blk_end; ++blk) step(blk, std::true_type{});
     step(blk_end - 1, std::false_type{});
 
-    // ---- finish: O = e^{f-m} A and l = e^{f-m} L, in the frame of m ----
-    const float oscl = __expf(f_run - m_run);  // row pc's
-    const float osc = oscl * vs_frame;
-    float l_e[4], o_e[4];  // rows 4qd+e
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        l_e[e] = lacc[e] * __shfl(oscl, 4 * qd + e, 64);
-        o_e[e] = __shfl(osc, 4 * qd + e, 64);
-    }
-    // row pc's l: element pc % 4 of the lanes of group pc / 4
-    float l_tot;
-    {
-        float lr[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) lr[e] = __shfl(l_e[e], 16 * (pc >> 2) + pc, 64);
-        const int ep = pc & 3;
-        l_tot = ep == 0 ? lr[0] : ep == 1 ? lr[1] : ep == 2 ? lr[2] : lr[3];
-    }
+    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run,
+                             vs_frame);
+}
 
-    if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
+// ---------------------------------------------------------------------------
+// Blocks whose K or V does not fit the registers as a whole (block_size x
+// head_dim above 16384 elements, e.g. 128 tokens x 256 dims): the block's K
+// and V are loaded in groups of GT 16-token tiles. QK runs over every tile of
+// the block before the softmax, whose max is the whole block's (as the
+// golden's), then PV group by group. Same lane layouts and arithmetic as
+// run_segment's register path; loads are not prefetched across blocks.
+// ---------------------------------------------------------------------------
+
+template <int BS, int DK, int DV, typename OutT, typename ET>
+__device__ __forceinline__ void run_segment_big(const KernelParams &P, const int b, const int kvh, const int rt,
+                                                const int ctx, const int nblk, const int blk_begin, const int blk_end,
+                                                float *const part_o, float *const part_ml) {
+    constexpr int NT = BS / 16;            // 16-token tiles per KV block
+    constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
+    constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
+    // tiles per load group: at most 128 registers of K (KS x 4 per tile) and of V (DVS x 16 per tile)
+    constexpr int GK = 32 / KS > 0 ? 32 / KS : 1;
+    constexpr int GV = 8 / DVS > 0 ? 8 / DVS : 1;
+    constexpr int GT0 = GK < GV ? GK : GV;
+    constexpr int GT = GT0 < NT ? GT0 : NT;
+    static_assert(NT % GT == 0, "load groups divide the block");
+    const int lane = threadIdx.x & 63;
+    const int qd = lane >> 4;
+    const int pc = lane & 15;
+    const int rows_here = min(16, P.rows - rt * 16);
+
+    int rowlen = 0;
+    u32x4_t qv[KS];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int row = 4 * qd + e;
-            if (row >= rows_here) continue;
-            const int64_t off = out_row_offset(P, b, kvh, rt * 16 + row, DV);
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+    if (pc < rows_here) {
+        const int r = rt * 16 + pc;
+        const int i = r / P.group, hh = r - i * P.group;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
 #pragma unroll
-            for (int ds = 0; ds < DVS; ++ds) {
-                if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
-                float v[8];
+        for (int kk = 0; kk < KS; ++kk)
+            if (DK % 32 == 0 || 32 * kk + 8 * qd < DK) qv[kk] = ld16(qrow + 32 * kk + 8 * qd);
+        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+    }
+    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
+
+    f32x4_t acc[DVS][8];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) v[jj] = l_e[e] > 0.f ? (o_e[e] * acc[ds][jj][e]) / l_e[e] : 0.f;
-                OutStore<OutT>::store8(P.out, off + 128 * ds + 8 * pc, v);
+    for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const u32x2_t ones4 = (u32x2_t){Elem<ET>::kOnePair, Elem<ET>::kOnePair};
+    constexpr float kLog2e = 1.4426950408889634f;
+    float m_run = kNegClamp, f_run = kNegClamp;
+
+    const int64_t k_tok_b = P.k_token_stride * 2, v_tok_b = P.v_token_stride * 2;
+    const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
+    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 16 * pc);
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
+    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * 2;
+    auto tile_base = [&](const char *blk_base, int blk, int t, int64_t tok_b) -> const char * {
+        const bool past = P.zero_page && 16 * t >= ctx - blk * BS;
+        return past ? P.zero_page : blk_base + (int64_t)(16 * t) * tok_b;
+    };
+
+    bool any_bad = false;
+    for (int blk = blk_begin; blk < blk_end; ++blk) {
+        const int raw = bt_row[blk];
+        const bool bad = (unsigned)raw >= (unsigned)P.num_pool_blocks;
+        any_bad |= bad;
+        const int phys = bad ? 0 : raw;
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
+        const char *vb = v_head + (int64_t)phys * P.v_block_stride * 2;
+        const bool first = (blk == blk_begin);
+
+        // ---- QK over every tile of the block, GT tiles of K at a time ----
+        f32x4_t s[NT];
+#pragma unroll
+        for (int g = 0; g < NT; g += GT) {
+            u32x4_t kr[GT][KS];
+#pragma unroll
+            for (int t = 0; t < GT; ++t) {
+                const char *kt = tile_base(kb, blk, g + t, k_tok_b);
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk)
+                    kr[t][kk] = (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
+                                    ? *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk)
+                                    : (u32x4_t){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int t = 0; t < GT; ++t) {
+                f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) c = Elem<ET>::mma32(kr[t][kk], qv[kk], c);
+                s[g + t] = c;
             }
         }
-        return;
-    }
 
-    // ---- a piece of the tile: partial (O relative to m, plus m and l) ----
+        // ---- softmax prepare and the online-merge factor (as run_segment) ----
+        float sc = P.scale;
+        if (!(sc > 0.f)) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int row = 4 * qd + e;
-        if (row >= rows_here) continue;
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
+        const int blk0 = blk * BS;
+        const bool full = !bad && (blk0 + BS <= min_rowlen);
+        const int rvalid = bad ? 0 : rowlen - blk0;
+        if (!full) {
 #pragma unroll
-        for (int ds = 0; ds < DVS; ++ds) {
-            if (!(DV % 128 == 0 || 128 * ds + 8 * pc < DV)) continue;
-            float *dst = part_o + row * DV + 128 * ds + 8 * pc;
-            *reinterpret_cast<f32x4_t *>(dst) =
-                (f32x4_t){acc[ds][0][e], acc[ds][1][e], acc[ds][2][e], acc[ds][3][e]} * o_e[e];
-            *reinterpret_cast<f32x4_t *>(dst + 4) =
-                (f32x4_t){acc[ds][4][e], acc[ds][5][e], acc[ds][6][e], acc[ds][7][e]} * o_e[e];
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mb = fmaxf(mx * sc, kNegClamp);
+        const float mnew = first ? mb : fmaxf(m_run, mb);
+        const bool use = first || (mb >= mnew - kFrameGap);
+        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        const float mb2 = use ? mb * kLog2e : INFINITY;
+        const float sc2 = sc * kLog2e;
+        u32x2_t pa[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
+            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
+        }
+        m_run = mnew;
+        if (use) f_run = mb;
+        {
+            f32x4_t cv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
+            lacc *= cv;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
+
+        // ---- PV, GT tiles of V at a time; V rows past the context (or of an
+        // out-of-pool block) are zeroed ----
+        const int vvalid = bad ? 0 : min(BS, ctx - blk0);
+#pragma unroll
+        for (int g = 0; g < NT; g += GT) {
+            u32x4_t vr[GT][DVS][4];
+#pragma unroll
+            for (int t = 0; t < GT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const char *vt = tile_base(vb, blk, g + t, v_tok_b) + (int64_t)e * v_tok_b;
+                    const bool zero = 16 * (g + t) + 4 * qd + e >= vvalid;
+#pragma unroll
+                    for (int ds = 0; ds < DVS; ++ds) {
+                        u32x4_t x = (u32x4_t){0u, 0u, 0u, 0u};
+                        if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
+                            x = *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds);
+                        vr[t][ds][e] = zero ? (u32x4_t){0u, 0u, 0u, 0u} : x;
+                    }
+                }
+#pragma unroll
+            for (int t = 0; t < GT; ++t)
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int w = jj >> 1;
+                        constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                        const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                        const unsigned d0 = __builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel);
+                        const unsigned d1 = __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel);
+                        acc[ds][jj] = Elem<ET>::mma16(pa[g + t], (u32x2_t){d0, d1}, acc[ds][jj]);
+                    }
         }
     }
-    if (qd == 0) {
-        part_ml[pc] = m_run;
-        part_ml[16 + pc] = l_tot;
-    }
+    if (any_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
+    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run, 1.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -832,6 +1041,7 @@ template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typ
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
+    static_assert(!KV8 || BS * DK <= 16384, "fp8 caches: blocks that fit the registers");
     // single-tile bf16 workers with 128-dim heads stage K through LDS
     constexpr bool KLDS = MAXW == 1 && !KV8 && DK == 128;
     __shared__ __attribute__((aligned(16))) char klds[KLDS ? BS * 256 : 16];
@@ -870,9 +1080,13 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         // every wave of the group has a row tile: all run the same blocks, so
         // a per-block barrier among them is matched
         const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
-        if (rt < P.row_tiles)
-            run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml,
-                                                                     MAXW > 1 && full_group, klds);
+        if (rt < P.row_tiles) {
+            if constexpr (BS * DK > 16384 || BS * DV > 16384)  // a block's K or V exceeds the registers
+                run_segment_big<BS, DK, DV, OutT, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
+            else
+                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po,
+                                                                         pml, MAXW > 1 && full_group, klds);
+        }
         pos += seg;
         slot = 1;
         if (pos >= end) break;

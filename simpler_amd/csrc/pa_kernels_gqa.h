@@ -17,8 +17,8 @@ KernelPair gqa_pair() {
             pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, false, ET>, false, D == 128};
 }
 
-// Block sizes 16..128 and head dims 16..256; BS x D at most 16384 elements (a
-// block's K and V operands stay in registers).
+// Block sizes 16..128 and head dims 16..256 (a block with more than 16384
+// elements of K or V runs run_segment_big).
 template <int BS, typename OutT, typename ET>
 KernelPair gqa_by_dim(int d) {
     switch (d) {
@@ -26,9 +26,7 @@ KernelPair gqa_by_dim(int d) {
         case 32: return gqa_pair<BS, 32, OutT, ET>();
         case 64: return gqa_pair<BS, 64, OutT, ET>();
         case 128: return gqa_pair<BS, 128, OutT, ET>();
-        case 256:
-            if constexpr (BS <= 64) return gqa_pair<BS, 256, OutT, ET>();
-            return KernelPair{};
+        case 256: return gqa_pair<BS, 256, OutT, ET>();
         default: return KernelPair{};
     }
 }

@@ -71,8 +71,6 @@ def test_highperf_shapes_direct_entry(name, out_dtype, device):
 @pytest.mark.parametrize("bs", [16, 32, 64, 128])
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_fp16_block_sizes_and_head_dims(bs, d, device):
-    if bs * d > 16384:
-        pytest.skip("block_size*head_dim above the register-resident block limit")
     print(f"[case] fp16 bs={bs} d={d}", flush=True)
     case = make_custom_case(batch=3, num_heads=16, kv_heads=4, head_dim=d, block_size=bs,
                             context_lens=[1, 333, 2 * bs + 5], seed=100 + bs + d, dtype=torch.float16)

@@ -76,12 +76,38 @@ def test_cfg1_small(out_dtype, device):
 @pytest.mark.parametrize("bs", [16, 32, 64, 128])
 @pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
 def test_block_sizes_and_head_dims(bs, d, device):
-    if bs * d > 16384:
-        pytest.skip("block_size*head_dim above the register-resident block limit")
     print(f"[case] bs={bs} d={d}", flush=True)
     case = make_custom_case(batch=3, num_heads=8, kv_heads=2, head_dim=d, block_size=bs,
                             context_lens=[1, bs + 3, 5 * bs - 1], seed=100 + bs + d)
     assert_close(run_gpu(case, device), oracle_numpy(case), what=f"bs{bs}_d{d}")
+
+
+@pytest.mark.parametrize("workers,q_len,value_range", [(0, 1, None), (7, 4, None), (1000, 4, None),
+                                                       (37, 1, 8.0)])
+def test_blocks_larger_than_the_registers(workers, q_len, value_range, device):
+    # 128 tokens x 256 dims: K and V of a block are loaded in tile groups;
+    # causal rows across two row tiles, split segments, large score ranges
+    print(f"[case] bs=128 d=256 workers={workers} q_len={q_len} range={value_range}", flush=True)
+    case = make_custom_case(batch=3, num_heads=16, kv_heads=2, head_dim=256, block_size=128, q_len=q_len,
+                            causal=q_len > 1, context_lens=[q_len, 1000, 2049], seed=150 + workers + q_len,
+                            value_range=value_range)
+    assert_close(run_gpu(case, device, num_workers=workers), oracle_numpy(case), what=f"big w{workers}")
+
+
+def test_blocks_larger_than_the_registers_ignore_garbage_and_report_bad_blocks(device):
+    case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=256, block_size=128,
+                            context_lens=[300, 50], seed=710, pool_extra=2)
+    base = run_gpu(case, device)
+    for b, n in enumerate([300, 50]):
+        last = int(case.block_table[b, (n - 1) // 128])
+        case.value_cache[last, n % 128 :] = float("nan")
+        case.key_cache[last, n % 128 :] = float("inf")
+    np.testing.assert_array_equal(run_gpu(case, device), base)
+    case.block_table[0, 1] = 10_000
+    run_gpu(case, device)
+    with pytest.raises(pa.PagedAttentionError):
+        pa.check_errors(device)
+    pa.check_errors(device)
 
 
 @pytest.mark.parametrize("group", [1, 2, 4, 5, 8, 16, 32])
