@@ -41,7 +41,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--config", default=DEFAULT_CONFIG)
     p.add_argument("--tg-mode", default="graph", choices=["eager", "graph"],
                    help="--op taskgraph: launch tasks as submitted, or as one hipGraph per step")
-    p.add_argument("--op", default="decode", choices=["decode", "kv_append", "prelude", "taskgraph"],
+    p.add_argument("--op", default="decode", choices=["decode", "decode_append", "kv_append", "prelude", "taskgraph"],
                    help="decode (the headline path); kv_append / prelude: the cache-write step before it")
     p.add_argument("--tokens", type=int, default=32768,
                    help="--op kv_append: tokens written per call (32 = one decode step of bs=32)")
@@ -272,6 +272,82 @@ def bench_kv(args) -> int:
     return 0
 
 
+def bench_decode_append(args) -> int:
+    """The KV append fused into the decode (simpler_hip_pa_decode_append) on a
+    decode config, beside the same work as two steps: simpler_hip_kv_append at
+    the derived slots, then simpler_hip_pa_decode (and the decode alone)."""
+    import torch
+
+    from simpler_amd import kv_cache as kvc
+    from simpler_amd import paged_attention as pa
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, make_case
+
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    if cfg.mla or cfg.kv_format != "bf16":
+        print("bench.py: --op decode_append times bf16 GQA configs", file=sys.stderr)
+        return 2
+    case_cpu = make_case(cfg)
+    case = case_cpu.to(dev)
+    g = torch.Generator().manual_seed(20261211)
+    shape = (cfg.batch, cfg.q_len, cfg.kv_heads)
+    k_new = torch.randn(*shape, cfg.head_dim_k, generator=g).to(torch.bfloat16).to(dev)
+    v_new = torch.randn(*shape, cfg.head_dim_v, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(case.out_shape(), dtype=torch.bfloat16, device=dev)
+    pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
+                         case.scale, causal=cfg.causal, num_workers=args.workers)
+    pa.append_tensors(pargs, case.query, case.key_cache, case.value_cache, k_new, v_new)
+    pos = case.context_lens.long()[:, None] - cfg.q_len + torch.arange(cfg.q_len, device=dev)[None, :]
+    phys = case.block_table.long().gather(1, pos.clamp(min=0) // cfg.block_size)
+    slots = torch.where(pos >= 0, phys * cfg.block_size + pos % cfg.block_size, -1).to(torch.int32).reshape(-1)
+    aargs = kvc.append_args(k_new.reshape(-1, cfg.kv_heads, cfg.head_dim_k),
+                            v_new.reshape(-1, cfg.kv_heads, cfg.head_dim_v), slots, case.key_cache, case.value_cache)
+    stream = torch.cuda.current_stream(dev)
+    sid = stream.cuda_stream
+    variants = {
+        "fused": lambda: pa.launch(pargs, dev, sid, key_new=k_new, value_new=v_new),
+        "separate": lambda: (kvc.launch_append(aargs, stream=sid), pa.launch(pargs, dev, sid)),
+        "decode_only": lambda: pa.launch(pargs, dev, sid),
+    }
+    # the variants take turns (five rounds); each one's figure is its median round
+    runs = {name: [] for name in variants}
+    for rnd in range(5):
+        for name, call in variants.items():
+            for _ in range(args.warmup):
+                call()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                call()
+            e1.record(stream)
+            torch.cuda.synchronize(dev)
+            runs[name].append(e0.elapsed_time(e1) / args.steps * 1e3)
+            print(f"[bench] round {rnd} {name}: {runs[name][-1]:.2f} us/step", file=sys.stderr, flush=True)
+    us = {name: sorted(r)[len(r) // 2] for name, r in runs.items()}
+    pa.check_errors(dev)
+    # decode bytes plus the appended rows (read from key_new/value_new, written to the caches)
+    new_rows = cfg.batch * cfg.q_len * cfg.kv_heads * (cfg.head_dim_k + cfg.head_dim_v) * 2
+    nbytes = algorithmic_bytes(case_cpu, out_bytes=2) + 2 * new_rows
+    gbs = nbytes / (us["fused"] * 1e-6) / 1e9
+    line = {
+        "metric": f"decode with fused KV append GB/s [{cfg.name}]", "value": round(gbs, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us["fused"] / 1e3, 5),
+        "us_per_step": round(us["fused"], 2), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.description}; {cfg.q_len} new token(s) per sequence appended",
+                   "parallelism": "single GPU"},
+        "us_per_step_separate": round(us["separate"], 2), "us_per_step_decode_only": round(us["decode_only"], 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "pa_decode_kernel (append) + pa_merge_kernel", "kernel_us": round(us["fused"], 2),
+                     "algorithmic_bytes": nbytes},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def bench_taskgraph(args) -> int:
     """The reference's unfused paged-attention chain on the task-graph backend.
 
@@ -362,6 +438,8 @@ def main() -> int:
         return 2
     if args.op == "taskgraph":
         return bench_taskgraph(args)
+    if args.op == "decode_append":
+        return bench_decode_append(args)
     if args.op != "decode":
         return bench_kv(args)
 

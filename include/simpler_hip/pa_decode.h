@@ -135,7 +135,7 @@ int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *args, void *worksp
  * launch since the last check met an out-of-pool block_table entry (such
  * blocks are skipped, never dereferenced), else SIMPLER_HIP_ERR_BAD_LENGTH if
  * one read a context_lens entry below 0, above max_blocks_per_seq*block_size,
- * or (causal) below q_len (the kernels then use the length clamped into
+ * or (causal, or with the fused append) below q_len (the kernels then use the length clamped into
  * [0, max_blocks_per_seq*block_size]), else 0. Clears the flags. Synchronous. */
 int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *stream);
 
@@ -156,6 +156,35 @@ int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *s
  */
 #define SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES (80u << 20)
 int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stream);
+
+/*
+ * KV-cache append fused into the decode: writes each sequence's new tokens
+ * into the paged caches and attends over the context that includes them, in
+ * the decode's two launches. Replaces the reference's separate append (the
+ * slot_mapping scatter of simpler_setup/goldens/qwen3_14b_decode.py:106-115,
+ * 261-269, which its fused attention task runs as phase 0,
+ * examples/a2a3/tensormap_and_ringbuffer/qwen3_14b_decode/kernels/vendor/
+ * paged_attention_cce/kernel/fai_body.hpp:199-230) followed by the decode.
+ *
+ * key_new    [batch, q_len, num_kv_heads, head_dim_k], the caches' element
+ *            type (bf16 or fp16), contiguous, 16-byte aligned
+ * value_new  [batch, q_len, num_kv_heads, head_dim_v], same; NULL for MLA
+ *            (value_cache == key_cache: V is the first head_dim_v dims of the
+ *            K row written)
+ * The q_len new tokens of sequence b are its last positions: with len =
+ * context_lens[b] (which counts them), token j goes to position
+ * p = len - q_len + j, i.e. row p % block_size of block
+ * block_table[b][p / block_size] -- the slot the reference derives from the
+ * block table and seq_len (qwen3_14b_decode.py:106-115). Results and cache
+ * contents are those of simpler_hip_kv_append with that slot mapping followed
+ * by simpler_hip_pa_decode. q_len <= 16; bf16 and fp16 caches (not fp8).
+ * Same workspace as simpler_hip_pa_decode for these args. A length below
+ * q_len is reported by simpler_hip_pa_decode_check as BAD_LENGTH (only the
+ * new tokens at positions >= 0 are then written); new tokens in out-of-pool
+ * blocks are neither read nor written (BAD_BLOCK).
+ */
+int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *args, const void *key_new, const void *value_new,
+                                 void *workspace, size_t workspace_bytes, void *stream);
 
 /* Measurement helpers: name of the main kernel the args select, and the
  * number of worker wavefronts a launch uses. */

@@ -23,6 +23,8 @@ SOURCES = [
     CSRC / "pa_decode.hip",
     CSRC / "pa_kernels_gqa_bf16.hip",
     CSRC / "pa_kernels_gqa_f16.hip",
+    CSRC / "pa_kernels_gqa_bf16_append.hip",
+    CSRC / "pa_kernels_gqa_f16_append.hip",
     CSRC / "pa_kernels_fp8.hip",
     CSRC / "pa_kernels_mla.hip",
     CSRC / "pa_kernels_merge.hip",

@@ -27,6 +27,7 @@ using namespace pa;
 // ----------------------------------------------------------------------------
 
 constexpr int kZeroOffset = 128;  // workspace bytes [128, 256) are never written after init
+constexpr int kMaxAppendTokens = 16;  // fused append: new tokens per sequence (one per residue mod 16)
 constexpr size_t kMaxZeroPageBytes = 1 << 20;  // larger token strides read the padding tiles as they are
 
 struct Plan {
@@ -94,24 +95,31 @@ bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
 }
 
 // The main kernel(s) and the merge kernel a decode with these args runs;
-// main is null when the combination is not supported.
+// main is null when the combination is not supported. With `append`, ka holds
+// the fused-append variants of k (same launch shapes; the plan is made from k).
 struct Kernels {
     KernelPair k;
+    KernelPair ka;
     MergeFn merge;
 };
 
-Kernels pick_kernel(const SimplerHipPaDecodeArgs *a) {
+Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
     Kernels s{};
     const int bs = a->block_size, dk = a->head_dim_k, dv = a->head_dim_v, out = a->out_dtype;
+    const bool f16 = a->kv_format == SIMPLER_HIP_KV_FP16;
     if (a->kv_format == SIMPLER_HIP_KV_FP8_E4M3) {
-        if (dk == dv) s.k = pick_gqa_fp8(bs, dk, out);
+        if (dk == dv && !append) s.k = pick_gqa_fp8(bs, dk, out);  // no fused append for fp8 caches
     } else if (is_mla_shape(a)) {
-        if (v_is_k_prefix(a) && a->kv_format == SIMPLER_HIP_KV_BF16) s.k = pick_mla(bs, out);
+        if (v_is_k_prefix(a) && a->kv_format == SIMPLER_HIP_KV_BF16) {
+            s.k = pick_mla(bs, out, false);
+            if (append) s.ka = pick_mla(bs, out, true);
+        }
     } else if (dk == dv) {
-        s.k = a->kv_format == SIMPLER_HIP_KV_FP16 ? pick_gqa_f16(bs, dk, out) : pick_gqa_bf16(bs, dk, out);
+        s.k = f16 ? pick_gqa_f16(bs, dk, out) : pick_gqa_bf16(bs, dk, out);
+        if (append) s.ka = f16 ? pick_gqa_f16_append(bs, dk, out) : pick_gqa_bf16_append(bs, dk, out);
     }
     s.merge = pick_merge(dv, out);
-    if (!s.merge.fn) s.k.main = nullptr;
+    if (!s.merge.fn || (append && !s.ka.main)) s.k.main = nullptr;
     return s;
 }
 
@@ -299,14 +307,17 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
 
 namespace simpler_hip {
 namespace {
+// k_new / v_new: the fused append's new tokens (k_new null: plain decode).
 int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes, void *stream,
-                     int phases, unsigned *err_mirror) {
+                     int phases, unsigned *err_mirror, const void *k_new = nullptr, const void *v_new = nullptr) {
     if (phases & ~(SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE)) return SIMPLER_HIP_ERR_INVALID;
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
-    const Kernels s = pick_kernel(a);
+    const bool append = k_new != nullptr;
+    const Kernels s = pick_kernel(a, append);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    const Plan plan = make_plan(a, s.k);
+    Plan plan = make_plan(a, s.k);
+    if (append) plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : s.ka.main;
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
     if (a->batch == 0) return SIMPLER_HIP_OK;
 
@@ -348,6 +359,8 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     P.k_scale = a->k_scale;
     P.v_scale = a->v_scale;
     P.err_mirror = (phases & SIMPLER_HIP_PHASE_MERGE) ? err_mirror : nullptr;
+    P.k_new = (const uint16_t *)k_new;
+    P.v_new = (const uint16_t *)v_new;
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
@@ -374,6 +387,20 @@ int pa_decode_with_mirror(const SimplerHipPaDecodeArgs *a, void *workspace, size
 extern "C" int simpler_hip_pa_decode_phase(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes,
                                            void *stream, int phases) {
     return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream, phases, nullptr);
+}
+
+extern "C" int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *a, const void *key_new,
+                                            const void *value_new, void *workspace, size_t workspace_bytes,
+                                            void *stream) {
+    const int rc = validate(a);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    if (a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || a->q_len > kMaxAppendTokens) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    const bool mla = is_mla_shape(a) && v_is_k_prefix(a);
+    if (!key_new || ((uintptr_t)key_new & 15)) return SIMPLER_HIP_ERR_INVALID;
+    if (mla ? value_new != nullptr : (!value_new || ((uintptr_t)value_new & 15))) return SIMPLER_HIP_ERR_INVALID;
+    return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream,
+                                         SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr, key_new,
+                                         value_new);
 }
 
 // ---------------------------------------------------------------------------

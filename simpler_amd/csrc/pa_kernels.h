@@ -48,6 +48,13 @@
 // Within a segment, V of block i is issued first and K of block i+1 as soon
 // as K of block i is consumed (after QK(i), or once K(i) is staged in LDS), so
 // both streams are in flight during the math.
+//
+// Fused KV append (APPEND): the q_len new tokens of each sequence, given
+// beside the caches, are its last positions. The blocks holding them run
+// after the pipelined loop (unpipelined_blocks), where the new rows replace
+// the cache's rows in registers and row tile 0's wave writes them into the
+// caches (simpler_setup/goldens/qwen3_14b_decode.py:106-115,261-269 is the
+// append this replaces).
 
 #pragma once
 
@@ -111,6 +118,11 @@ struct KernelParams {
     float scale;
     int32_t causal;
     unsigned *err_mirror;  // host-visible copy of *error_flag written by the merge kernel, or null
+    // fused KV append: the q_len new tokens of each sequence (its positions
+    // len-q_len .. len-1), [batch, q_len, kv_heads, Dk] and [.., Dv]; v_new is
+    // null for MLA (V is a prefix of K). Null when not appending.
+    const uint16_t *k_new;
+    const uint16_t *v_new;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
@@ -266,13 +278,14 @@ constexpr unsigned kErrBadLength = 2u;  // a context_lens entry the kernels had 
 
 // One wave of the grid (wave 0 of workgroup 0) checks every raw length: below
 // 0, above what the block-table row holds, or (causal) shorter than the query.
-// The kernels run such a sequence with its length clamped by ctx_of; the flag
+// With a fused append, a length below q_len cannot hold the new tokens. The
+// kernels run such a sequence with its length clamped by ctx_of; the flag
 // turns that into an error for the caller, as the host-side table check does.
 __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
     if (blockIdx.x != 0 || threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     const int64_t cap = (int64_t)P.max_blocks * P.block_size;
-    const int lo = P.causal ? P.q_len : 0;
+    const int lo = (P.causal || P.k_new) ? P.q_len : 0;  // an appended context holds its new tokens
     bool bad = false;
     for (int b = lane; b < P.batch; b += 64) {
         const int len = P.context_lens[b];
@@ -448,6 +461,309 @@ __device__ __forceinline__ void finish_segment(const KernelParams &P, const int 
     }
 }
 
+// Fused KV append. The q_len (<= 16) new tokens of sequence b are its
+// positions ctx-q_len .. ctx-1. They are consecutive, so each residue of a
+// position mod 16 belongs to one new token at most, and a lane, whose K and V
+// operands always hold the same residues (register K: token pc of every
+// 16-token tile; V and row-staged K: tokens 4qd+e), needs the rows of at most
+// one new token per residue it holds, loaded once per segment. Every wave
+// that reads a block holding new tokens uses these rows in place of the
+// cache's (so what the cache holds there during the launch never matters),
+// and the wave of row tile 0 writes them into the cache.
+__device__ __forceinline__ int new_token_at(const int new0, const int ctx, const int r) {
+    const int p = new0 + ((r - new0) & 15);
+    return (p >= 0 && p < ctx) ? p : -1;
+}
+// 16-token tile of block blk that holds position p, or -1
+template <int BS>
+__device__ __forceinline__ int tile_of(const int p, const int blk) {
+    const int o = p - blk * BS;
+    return (p >= 0 && (unsigned)o < (unsigned)BS) ? (o >> 4) : -1;
+}
+
+// ---------------------------------------------------------------------------
+// KV blocks without cross-block prefetch, continuing a segment's state (A,
+// its row sums, m, f). Two users:
+//  * blocks whose K or V does not fit the registers as a whole (block_size x
+//    head_dim above 16384 elements, e.g. 128 tokens x 256 dims): the block's
+//    K and V are loaded in groups of GT 16-token tiles; QK runs over every
+//    tile of the block before the softmax, whose max is the whole block's
+//    (as the golden's), then PV group by group;
+//  * the fused append's blocks that hold new tokens (APPEND), at the end of
+//    a segment: the new rows are loaded here and replace the cache's rows in
+//    registers (see new_token_at), so the pipelined loop before them carries
+//    no extra registers.
+// Same lane layouts and arithmetic as run_segment's register path, so a
+// block gives the same bits either way. Blocks [lo, hi) of the segment that
+// starts at blk_begin.
+// ---------------------------------------------------------------------------
+
+template <int BS, int DK, int DV, typename ET, bool APPEND>
+__device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const int b, const int kvh, const int rt,
+                                                   const int ctx, const int blk_begin, const int lo, const int hi,
+                                                   const u32x4_t (&qv)[(DK + 31) / 32], const int rowlen,
+                                                   const int min_rowlen, f32x4_t (&acc)[(DV + 127) / 128][8],
+                                                   f32x4_t &lacc, float &m_run, float &f_run) {
+    constexpr int NT = BS / 16;            // 16-token tiles per KV block
+    constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
+    constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
+    // tiles per load group: at most 128 registers of K (KS x 4 per tile) and of V (DVS x 16 per tile)
+    constexpr int GK = 32 / KS > 0 ? 32 / KS : 1;
+    constexpr int GV = 8 / DVS > 0 ? 8 / DVS : 1;
+    constexpr int GT0 = GK < GV ? GK : GV;
+    constexpr int GT = GT0 < NT ? GT0 : NT;
+    static_assert(NT % GT == 0, "load groups divide the block");
+    const int lane = threadIdx.x & 63;
+    const int qd = lane >> 4;
+    const int pc = lane & 15;
+    const __attribute__((address_space(4))) int32_t *bt_row =
+        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
+    const u32x2_t ones4 = (u32x2_t){Elem<ET>::kOnePair, Elem<ET>::kOnePair};
+    constexpr float kLog2e = 1.4426950408889634f;
+
+    const int64_t k_tok_b = P.k_token_stride * 2, v_tok_b = P.v_token_stride * 2;
+    const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
+    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 16 * pc);
+    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
+    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * 2;
+    auto tile_base = [&](const char *blk_base, int blk, int t, int64_t tok_b) -> const char * {
+        const bool past = P.zero_page && 16 * t >= ctx - blk * BS;
+        return past ? P.zero_page : blk_base + (int64_t)(16 * t) * tok_b;
+    };
+
+    // fused append: register-K rows of the new token at residue pc, V rows of
+    // those at residues 4qd+e
+    const int new0 = ctx - P.q_len;
+    int pk = -1, pe[4] = {-1, -1, -1, -1};
+    u32x4_t knew[APPEND ? KS : 1], vnew[APPEND ? 4 : 1][DVS];
+    if constexpr (APPEND) {
+        const int64_t row0 = (int64_t)b * P.q_len - new0;  // k_new row of position p: row0 + p
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) knew[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+        pk = new_token_at(new0, ctx, pc);
+        if (pk >= 0) {
+            const uint16_t *kr = P.k_new + ((row0 + pk) * P.kv_heads + kvh) * DK;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                if (DK % 32 == 0 || 32 * kk + 8 * qd < DK) knew[kk] = ld16(kr + 32 * kk + 8 * qd);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            pe[e] = new_token_at(new0, ctx, 4 * qd + e);
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds) {
+                vnew[e][ds] = (u32x4_t){0u, 0u, 0u, 0u};
+                if (pe[e] >= 0 && (DV % 128 == 0 || 128 * ds + 8 * pc < DV))
+                    vnew[e][ds] = ld16(P.v_new + ((row0 + pe[e]) * P.kv_heads + kvh) * DV + 128 * ds + 8 * pc);
+            }
+        }
+    }
+
+    bool any_bad = false;
+    for (int blk = lo; blk < hi; ++blk) {
+        const int raw = bt_row[blk];
+        const bool bad = (unsigned)raw >= (unsigned)P.num_pool_blocks;
+        any_bad |= bad;
+        const int phys = bad ? 0 : raw;
+        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
+        const char *vb = v_head + (int64_t)phys * P.v_block_stride * 2;
+        const bool first = (blk == blk_begin);
+        const bool blk_new = APPEND && blk * BS + BS > new0;  // the block holds new tokens (wave-uniform)
+        const int tk = APPEND && blk_new ? tile_of<BS>(pk, blk) : -1;
+
+        // ---- QK over every tile of the block, GT tiles of K at a time ----
+        f32x4_t s[NT];
+#pragma unroll
+        for (int g = 0; g < NT; g += GT) {
+            u32x4_t kr[GT][KS];
+#pragma unroll
+            for (int t = 0; t < GT; ++t) {
+                const char *kt = tile_base(kb, blk, g + t, k_tok_b);
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk)
+                    kr[t][kk] = (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
+                                    ? *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk)
+                                    : (u32x4_t){0u, 0u, 0u, 0u};
+            }
+            if constexpr (APPEND) {
+                if (blk_new) {
+#pragma unroll
+                    for (int t = 0; t < GT; ++t)
+#pragma unroll
+                        for (int kk = 0; kk < KS; ++kk)
+                            if (g + t == tk) kr[t][kk] = knew[kk];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < GT; ++t) {
+                f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) c = Elem<ET>::mma32(kr[t][kk], qv[kk], c);
+                s[g + t] = c;
+            }
+        }
+
+        // ---- softmax prepare and the online-merge factor (as run_segment) ----
+        float sc = P.scale;
+        if (!(sc > 0.f)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] *= sc;
+            sc = 1.f;
+        }
+        const int blk0 = blk * BS;
+        const bool full = !bad && (blk0 + BS <= min_rowlen);
+        const int rvalid = bad ? 0 : rowlen - blk0;
+        if (!full) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mb = fmaxf(mx * sc, kNegClamp);
+        const float mnew = first ? mb : fmaxf(m_run, mb);
+        const bool use = first || (mb >= mnew - kFrameGap);
+        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
+        const float mb2 = use ? mb * kLog2e : INFINITY;
+        const float sc2 = sc * kLog2e;
+        u32x2_t pa[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
+            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
+        }
+        m_run = mnew;
+        if (use) f_run = mb;
+        {
+            f32x4_t cv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
+#pragma unroll
+            for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
+            lacc *= cv;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
+
+        // ---- PV, GT tiles of V at a time; V rows past the context (or of an
+        // out-of-pool block) are zeroed ----
+        const int vvalid = bad ? 0 : min(BS, ctx - blk0);
+#pragma unroll
+        for (int g = 0; g < NT; g += GT) {
+            u32x4_t vr[GT][DVS][4];
+#pragma unroll
+            for (int t = 0; t < GT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const char *vt = tile_base(vb, blk, g + t, v_tok_b) + (int64_t)e * v_tok_b;
+                    const bool zero = 16 * (g + t) + 4 * qd + e >= vvalid;
+#pragma unroll
+                    for (int ds = 0; ds < DVS; ++ds) {
+                        u32x4_t x = (u32x4_t){0u, 0u, 0u, 0u};
+                        if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
+                            x = *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds);
+                        if constexpr (APPEND) {
+                            if (blk_new && tile_of<BS>(pe[e], blk) == g + t) x = vnew[e][ds];
+                        }
+                        vr[t][ds][e] = zero ? (u32x4_t){0u, 0u, 0u, 0u} : x;
+                    }
+                }
+#pragma unroll
+            for (int t = 0; t < GT; ++t)
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int w = jj >> 1;
+                        constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                        const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                        const unsigned d0 = __builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel);
+                        const unsigned d1 = __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel);
+                        acc[ds][jj] = Elem<ET>::mma16(pa[g + t], (u32x2_t){d0, d1}, acc[ds][jj]);
+                    }
+        }
+        // the new tokens of this block into the caches (row tile 0's wave)
+        if constexpr (APPEND) {
+            if (blk_new && rt == 0 && !bad) {
+                char *kw = const_cast<char *>(kb), *vw = const_cast<char *>(vb);
+                if (tk >= 0) {
+#pragma unroll
+                    for (int kk = 0; kk < KS; ++kk)
+                        if (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
+                            *reinterpret_cast<u32x4_t *>(kw + (int64_t)(pk - blk0) * k_tok_b +
+                                                         2 * (32 * kk + 8 * qd)) = knew[kk];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (tile_of<BS>(pe[e], blk) < 0) continue;
+#pragma unroll
+                    for (int ds = 0; ds < DVS; ++ds)
+                        if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
+                            *reinterpret_cast<u32x4_t *>(vw + (int64_t)(pe[e] - blk0) * v_tok_b +
+                                                         2 * (128 * ds + 8 * pc)) = vnew[e][ds];
+                }
+            }
+        }
+    }
+    if (any_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
+}
+
+// Query operand (row pc of row tile rt, dims 32kk+8qd..) and the row's visible
+// length; 0 rows past the tile's valid rows.
+template <int DK>
+__device__ __forceinline__ void load_query(const KernelParams &P, const int b, const int kvh, const int rt,
+                                           const int ctx, u32x4_t (&qv)[(DK + 31) / 32], int &rowlen) {
+    constexpr int KS = (DK + 31) / 32;
+    const int lane = threadIdx.x & 63;
+    const int qd = lane >> 4, pc = lane & 15;
+    rowlen = 0;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
+    if (pc < min(16, P.rows - rt * 16)) {
+        const int r = rt * 16 + pc;
+        const int i = r / P.group, hh = r - i * P.group;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+            if (DK % 32 == 0 || 32 * kk + 8 * qd < DK) qv[kk] = ld16(qrow + 32 * kk + 8 * qd);
+        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+    }
+}
+
+// A segment of blocks too large for the registers (see unpipelined_blocks).
+template <int BS, int DK, int DV, typename OutT, typename ET, bool APPEND = false>
+__device__ __forceinline__ void run_segment_big(const KernelParams &P, const int b, const int kvh, const int rt,
+                                                const int ctx, const int nblk, const int blk_begin, const int blk_end,
+                                                float *const part_o, float *const part_ml) {
+    constexpr int KS = (DK + 31) / 32;
+    constexpr int DVS = (DV + 127) / 128;
+    u32x4_t qv[KS];
+    int rowlen = 0;
+    load_query<DK>(P, b, kvh, rt, ctx, qv, rowlen);
+    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
+    f32x4_t acc[DVS][8];
+#pragma unroll
+    for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegClamp, f_run = kNegClamp;
+    unpipelined_blocks<BS, DK, DV, ET, APPEND>(P, b, kvh, rt, ctx, blk_begin, blk_begin, blk_end, qv, rowlen,
+                                               min_rowlen, acc, lacc, m_run, f_run);
+    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run, 1.f);
+}
+
 // KV8: K and V caches hold E4M3FN bytes with one fp32 scale per (block, kv
 // head). They are widened to bf16 in registers (exact) right before the
 // MFMAs. The K scale folds into the softmax scale. The V scale is carried as
@@ -470,7 +786,8 @@ __device__ __forceinline__ void finish_segment(const KernelParams &P, const int 
 // ctx and nblk are sequence b's (clamped) context length and block count.
 // ET: the element type of the query and bf16/fp16 caches (fp8 caches widen
 // to bf16, so KV8 takes ET = bf16).
-template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16>
+template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16,
+          bool APPEND = false>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int ctx, const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
@@ -482,6 +799,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     static_assert(!KV8 || (DK % 64 == 0 && DV % 128 == 0), "fp8 caches: head dims multiple of 64 (K), 128 (V)");
     static_assert(!KLDS || (!KV8 && DK == 128), "K through LDS: 16-bit caches, DK = 128");
     static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
+    static_assert(!(KV8 && APPEND), "fused append: 16-bit caches");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -797,7 +1115,6 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     // would wait for K(i+1) as well.
     bool bad = false;
     int phys = checked(bt_row[blk_begin], bad);
-    load_k(kreg, phys, blk_begin);
     auto step = [&](const int blk, auto has_next) {
         constexpr bool NEXT = decltype(has_next)::value;
         const bool blk_bad = bad;
@@ -833,200 +1150,29 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         };
         compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k);
     };
-    for (int blk = blk_begin; blk + 1 < blk_end; ++blk) step(blk, std::true_type{});
-    step(blk_end - 1, std::false_type{});
+    // blocks [blk_begin, end), end > blk_begin, through the pipeline
+    auto pipeline = [&](const int end) {
+        load_k(kreg, phys, blk_begin);
+        for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{});
+        step(end - 1, std::false_type{});
+    };
+    if constexpr (APPEND) {
+        // Fused append: the blocks from the first one holding a new token on
+        // run after the pipeline, in unpipelined_blocks, which reads the new
+        // rows there. (Kept apart from the plain decode's path: a run-time
+        // condition around the pipeline's first load would loosen the
+        // compiler's wait counts in the loop.)
+        const int pipe_end = max(blk_begin, min(blk_end, ctx - P.q_len < 0 ? 0 : (ctx - P.q_len) / BS));
+        if (pipe_end > blk_begin) pipeline(pipe_end);
+        if (pipe_end < blk_end)
+            unpipelined_blocks<BS, DK, DV, ET, true>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
+                                                     min_rowlen, acc, lacc, m_run, f_run);
+    } else {
+        pipeline(blk_end);
+    }
 
     finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run,
                              vs_frame);
-}
-
-// ---------------------------------------------------------------------------
-// Blocks whose K or V does not fit the registers as a whole (block_size x
-// head_dim above 16384 elements, e.g. 128 tokens x 256 dims): the block's K
-// and V are loaded in groups of GT 16-token tiles. QK runs over every tile of
-// the block before the softmax, whose max is the whole block's (as the
-// golden's), then PV group by group. Same lane layouts and arithmetic as
-// run_segment's register path; loads are not prefetched across blocks.
-// ---------------------------------------------------------------------------
-
-template <int BS, int DK, int DV, typename OutT, typename ET>
-__device__ __forceinline__ void run_segment_big(const KernelParams &P, const int b, const int kvh, const int rt,
-                                                const int ctx, const int nblk, const int blk_begin, const int blk_end,
-                                                float *const part_o, float *const part_ml) {
-    constexpr int NT = BS / 16;            // 16-token tiles per KV block
-    constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
-    constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
-    // tiles per load group: at most 128 registers of K (KS x 4 per tile) and of V (DVS x 16 per tile)
-    constexpr int GK = 32 / KS > 0 ? 32 / KS : 1;
-    constexpr int GV = 8 / DVS > 0 ? 8 / DVS : 1;
-    constexpr int GT0 = GK < GV ? GK : GV;
-    constexpr int GT = GT0 < NT ? GT0 : NT;
-    static_assert(NT % GT == 0, "load groups divide the block");
-    const int lane = threadIdx.x & 63;
-    const int qd = lane >> 4;
-    const int pc = lane & 15;
-    const int rows_here = min(16, P.rows - rt * 16);
-
-    int rowlen = 0;
-    u32x4_t qv[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
-    if (pc < rows_here) {
-        const int r = rt * 16 + pc;
-        const int i = r / P.group, hh = r - i * P.group;
-        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-            if (DK % 32 == 0 || 32 * kk + 8 * qd < DK) qv[kk] = ld16(qrow + 32 * kk + 8 * qd);
-        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
-    }
-    const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
-    const __attribute__((address_space(4))) int32_t *bt_row =
-        (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
-
-    f32x4_t acc[DVS][8];
-#pragma unroll
-    for (int ds = 0; ds < DVS; ++ds)
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    const u32x2_t ones4 = (u32x2_t){Elem<ET>::kOnePair, Elem<ET>::kOnePair};
-    constexpr float kLog2e = 1.4426950408889634f;
-    float m_run = kNegClamp, f_run = kNegClamp;
-
-    const int64_t k_tok_b = P.k_token_stride * 2, v_tok_b = P.v_token_stride * 2;
-    const uint32_t k_lane = (uint32_t)(pc * k_tok_b + 16 * qd);
-    const uint32_t v_lane = (uint32_t)(4 * qd * v_tok_b + 16 * pc);
-    const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
-    const char *v_head = reinterpret_cast<const char *>(P.v) + (int64_t)kvh * P.v_head_stride * 2;
-    auto tile_base = [&](const char *blk_base, int blk, int t, int64_t tok_b) -> const char * {
-        const bool past = P.zero_page && 16 * t >= ctx - blk * BS;
-        return past ? P.zero_page : blk_base + (int64_t)(16 * t) * tok_b;
-    };
-
-    bool any_bad = false;
-    for (int blk = blk_begin; blk < blk_end; ++blk) {
-        const int raw = bt_row[blk];
-        const bool bad = (unsigned)raw >= (unsigned)P.num_pool_blocks;
-        any_bad |= bad;
-        const int phys = bad ? 0 : raw;
-        const char *kb = k_head + (int64_t)phys * P.k_block_stride * 2;
-        const char *vb = v_head + (int64_t)phys * P.v_block_stride * 2;
-        const bool first = (blk == blk_begin);
-
-        // ---- QK over every tile of the block, GT tiles of K at a time ----
-        f32x4_t s[NT];
-#pragma unroll
-        for (int g = 0; g < NT; g += GT) {
-            u32x4_t kr[GT][KS];
-#pragma unroll
-            for (int t = 0; t < GT; ++t) {
-                const char *kt = tile_base(kb, blk, g + t, k_tok_b);
-#pragma unroll
-                for (int kk = 0; kk < KS; ++kk)
-                    kr[t][kk] = (DK % 32 == 0 || 32 * kk + 8 * qd < DK)
-                                    ? *reinterpret_cast<const u32x4_t *>(kt + k_lane + 64 * kk)
-                                    : (u32x4_t){0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int t = 0; t < GT; ++t) {
-                f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < KS; ++kk) c = Elem<ET>::mma32(kr[t][kk], qv[kk], c);
-                s[g + t] = c;
-            }
-        }
-
-        // ---- softmax prepare and the online-merge factor (as run_segment) ----
-        float sc = P.scale;
-        if (!(sc > 0.f)) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) s[t] *= sc;
-            sc = 1.f;
-        }
-        const int blk0 = blk * BS;
-        const bool full = !bad && (blk0 + BS <= min_rowlen);
-        const int rvalid = bad ? 0 : rowlen - blk0;
-        if (!full) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mb = fmaxf(mx * sc, kNegClamp);
-        const float mnew = first ? mb : fmaxf(m_run, mb);
-        const bool use = first || (mb >= mnew - kFrameGap);
-        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
-        const float mb2 = use ? mb * kLog2e : INFINITY;
-        const float sc2 = sc * kLog2e;
-        u32x2_t pa[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float p[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
-            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
-        }
-        m_run = mnew;
-        if (use) f_run = mb;
-        {
-            f32x4_t cv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
-#pragma unroll
-            for (int ds = 0; ds < DVS; ++ds)
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
-            lacc *= cv;
-        }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
-
-        // ---- PV, GT tiles of V at a time; V rows past the context (or of an
-        // out-of-pool block) are zeroed ----
-        const int vvalid = bad ? 0 : min(BS, ctx - blk0);
-#pragma unroll
-        for (int g = 0; g < NT; g += GT) {
-            u32x4_t vr[GT][DVS][4];
-#pragma unroll
-            for (int t = 0; t < GT; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const char *vt = tile_base(vb, blk, g + t, v_tok_b) + (int64_t)e * v_tok_b;
-                    const bool zero = 16 * (g + t) + 4 * qd + e >= vvalid;
-#pragma unroll
-                    for (int ds = 0; ds < DVS; ++ds) {
-                        u32x4_t x = (u32x4_t){0u, 0u, 0u, 0u};
-                        if (DV % 128 == 0 || 128 * ds + 8 * pc < DV)
-                            x = *reinterpret_cast<const u32x4_t *>(vt + v_lane + 256 * ds);
-                        vr[t][ds][e] = zero ? (u32x4_t){0u, 0u, 0u, 0u} : x;
-                    }
-                }
-#pragma unroll
-            for (int t = 0; t < GT; ++t)
-#pragma unroll
-                for (int ds = 0; ds < DVS; ++ds)
-#pragma unroll
-                    for (int jj = 0; jj < 8; ++jj) {
-                        const int w = jj >> 1;
-                        constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
-                        const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
-                        const unsigned d0 = __builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel);
-                        const unsigned d1 = __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel);
-                        acc[ds][jj] = Elem<ET>::mma16(pa[g + t], (u32x2_t){d0, d1}, acc[ds][jj]);
-                    }
-        }
-    }
-    if (any_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
-    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run, 1.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1037,7 +1183,8 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
 // four sibling waves, one per row tile, walk the same KV blocks, so V is loaded
 // through the caches (the siblings hit each other's lines) rather than
 // streamed past them.
-template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16>
+template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16,
+          bool APPEND = false>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
@@ -1082,10 +1229,11 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
         const bool full_group = (rg + 1) * P.tiles_per_worker <= P.row_tiles;
         if (rt < P.row_tiles) {
             if constexpr (BS * DK > 16384 || BS * DV > 16384)  // a block's K or V exceeds the registers
-                run_segment_big<BS, DK, DV, OutT, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
+                run_segment_big<BS, DK, DV, OutT, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
             else
-                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po,
-                                                                         pml, MAXW > 1 && full_group, klds);
+                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk,
+                                                                                 blk + seg, po, pml,
+                                                                                 MAXW > 1 && full_group, klds);
         }
         pos += seg;
         slot = 1;
@@ -1358,7 +1506,7 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t num_re
                      __builtin_amdgcn_readfirstlane((int)num_records), 0x00020000};
 }
 
-template <int BS, int DK, int DV, typename OutT>
+template <int BS, int DK, int DV, typename OutT, bool APPEND = false>
 __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
                                                 const int groups, const int b, const int kvh, const int nblk,
                                                 const int blk_begin, const int blk_end, const int slot,
@@ -1400,6 +1548,23 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
     }
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - r0 / P.group) : ctx;
+
+    // ---- fused append: the new tokens' K rows (positions new0 .. ctx-1),
+    // 16-byte chunk c = threadIdx.x + 256u of the q_len x KC chunks in this
+    // thread's registers, patched into the LDS copy of their block once it is
+    // filled, and written to the cache by row group 0 at the segment's end ----
+    constexpr int NU = APPEND ? (16 * KC + 255) / 256 : 1;  // q_len <= 16
+    const int new0 = ctx - P.q_len;
+    u32x4_t knew[NU];
+    if constexpr (APPEND) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            knew[u] = (u32x4_t){0u, 0u, 0u, 0u};
+            const int c = (int)threadIdx.x + 256 * u, j = c / KC;
+            if (blk_end * BS > new0 && j < P.q_len && new0 + j >= 0)
+                knew[u] = ld16(P.k_new + ((int64_t)(b * P.q_len + j) * P.kv_heads + kvh) * DK + 8 * (c - j * KC));
+        }
+    }
 
     // Block-table entries are read through the scalar cache (constant
     // address space): the load is counted by lgkmcnt, so waiting for it never
@@ -1670,6 +1835,19 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
             __builtin_amdgcn_s_waitcnt(kWaitAll);
         __builtin_amdgcn_s_barrier();  // every wave's fill landed; the other buffer is free
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (APPEND) {
+            if (blk * BS + BS > new0) {  // the block holds new tokens (workgroup-uniform)
+                char *buf = even ? smem0 : smem1;
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    const int c = (int)threadIdx.x + 256 * u, j = c / KC;
+                    const int o = new0 + j - blk * BS;  // row of the token in this block
+                    if (j < P.q_len && new0 + j >= 0 && (unsigned)o < (unsigned)BS)
+                        lds_st16(buf, (uint32_t)(o * RB + 16 * (c - j * KC)), knew[u]);
+                }
+                lds_barrier();
+            }
+        }
         bool bad_next = false;
         if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
         if (blk + 2 < blk_end) prefetch(blk + 2);
@@ -1678,6 +1856,21 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         bad_cur = bad_next;
     }
     __syncthreads();  // the buffers are refilled by the next segment; pexch is free
+    if constexpr (APPEND) {  // the new tokens of this segment's blocks into the cache
+        if (rgrp == 0 && blk_end * BS > new0) {
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const int c = (int)threadIdx.x + 256 * u, j = c / KC;
+                const int p = new0 + j;
+                if (j >= P.q_len || p < 0 || p < blk_begin * BS || p >= blk_end * BS) continue;
+                bool bad = false;
+                const int phys = phys_of(p / BS, bad);
+                if (bad) continue;
+                char *row = const_cast<char *>(k_head) + (int64_t)phys * P.k_block_stride * 2 + (int64_t)(p % BS) * tok_b;
+                *reinterpret_cast<u32x4_t *>(row + 16 * (c - j * KC)) = knew[u];
+            }
+        }
+    }
 
     // ---- finish: O = e^{f-m} A, l = e^{f-m} L. The row factors live with the
     // row's wave; every wave holds a quarter of every row's dims ----
@@ -1720,7 +1913,7 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 // Worker workgroup = four waves = one row group of one work slice. The work
 // list holds (batch, kv head, KV block) entries; every row group of a slice
 // walks the same entries.
-template <int BS, int DK, int DV, typename OutT>
+template <int BS, int DK, int DV, typename OutT, bool APPEND = false>
 __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     using L = MlaLayout<DK>;
     __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
@@ -1750,8 +1943,8 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0, smem1,
-                                          sink, pexch);
+        run_mla_segment<BS, DK, DV, OutT, APPEND>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0,
+                                                  smem1, sink, pexch);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -1792,10 +1985,13 @@ struct MergeFn {
 // SIMPLER_HIP_DT_BFLOAT16 or SIMPLER_HIP_DT_FLOAT16 code), Dk == Dv.
 KernelPair pick_gqa_bf16(int bs, int d, int out_dtype);
 KernelPair pick_gqa_f16(int bs, int d, int out_dtype);
+// The same with the fused KV append (KernelParams::k_new / v_new).
+KernelPair pick_gqa_bf16_append(int bs, int d, int out_dtype);
+KernelPair pick_gqa_f16_append(int bs, int d, int out_dtype);
 // GQA decode with fp8 E4M3FN caches (bf16 query), Dk == Dv == 128.
 KernelPair pick_gqa_fp8(int bs, int d, int out_dtype);
-// MLA (Dk 576, Dv 512, V a prefix of K), bf16.
-KernelPair pick_mla(int bs, int out_dtype);
+// MLA (Dk 576, Dv 512, V a prefix of K), bf16, without or with the fused KV append.
+KernelPair pick_mla(int bs, int out_dtype, bool append);
 // The split merge for output width dv.
 MergeFn pick_merge(int dv, int out_dtype);
 

@@ -5,8 +5,8 @@ namespace simpler_hip {
 namespace pa {
 
 KernelPair pick_gqa_f16(int bs, int d, int out_dtype) {
-    if (out_dtype == SIMPLER_HIP_DT_FLOAT32) return gqa_by_block<float, _Float16>(bs, d);
-    if (out_dtype == SIMPLER_HIP_DT_FLOAT16) return gqa_by_block<_Float16, _Float16>(bs, d);
+    if (out_dtype == SIMPLER_HIP_DT_FLOAT32) return gqa_by_block<float, _Float16, false>(bs, d);
+    if (out_dtype == SIMPLER_HIP_DT_FLOAT16) return gqa_by_block<_Float16, _Float16, false>(bs, d);
     return KernelPair{};
 }
 

@@ -190,11 +190,14 @@ PHASE_MAIN, PHASE_MERGE = 1, 2
 
 
 def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = None,
-           phases: int = PHASE_MAIN | PHASE_MERGE) -> None:
+           phases: int = PHASE_MAIN | PHASE_MERGE, key_new: torch.Tensor | None = None,
+           value_new: torch.Tensor | None = None) -> None:
     """Enqueue one decode on ``stream`` (default: torch's current stream).
 
     ``phases`` selects the main kernel, the merge kernel or both (the default);
-    a merge must follow a main launch with the same args.
+    a merge must follow a main launch with the same args. With ``key_new``
+    (checked by ``append_tensors``) the decode runs with the fused KV append
+    (``simpler_hip_pa_decode_append``, both phases).
     """
     lib = _lib.lib()
     if stream is None:
@@ -203,12 +206,45 @@ def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = N
     if need == 0:
         raise PagedAttentionError(-1)
     ws = _WORKSPACE.get(device, need, stream)
+    if key_new is not None:
+        if phases != PHASE_MAIN | PHASE_MERGE:
+            raise ValueError("the fused append runs both phases")
+        rc = lib.simpler_hip_pa_decode_append(ctypes.byref(args), key_new.data_ptr(),
+                                              value_new.data_ptr() if value_new is not None else None,
+                                              ws.data_ptr(), ws.numel(), stream)
+        if rc != 0:
+            raise PagedAttentionError(rc, "simpler_hip_pa_decode_append")
+        return
     if phases == PHASE_MAIN | PHASE_MERGE:
         rc = lib.simpler_hip_pa_decode(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream)
     else:
         rc = lib.simpler_hip_pa_decode_phase(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream, phases)
     if rc != 0:
         raise PagedAttentionError(rc)
+
+
+def append_tensors(args: _lib.PaDecodeArgs, query: torch.Tensor, key_cache: torch.Tensor,
+                   value_cache: torch.Tensor, key_new: torch.Tensor, value_new: torch.Tensor | None) -> None:
+    """Check the new tokens of a fused append against decode ``args``:
+    ``key_new`` ``[B, q_len, Hkv, Dk]`` (or ``[B, Hkv, Dk]`` for q_len 1) and
+    ``value_new`` ``[..., Dv]`` contiguous, of the caches' dtype; ``value_new`` is
+    ``None`` exactly when ``value_cache`` is a view of ``key_cache`` (MLA)."""
+    kv_dtype = key_cache.dtype
+    q_len = args.q_len
+    mla = value_cache.data_ptr() == key_cache.data_ptr()
+    for name, t, d in (("key_new", key_new, args.head_dim_k), ("value_new", value_new, args.head_dim_v)):
+        if t is None:
+            if name == "value_new" and mla:
+                continue
+            raise ValueError(f"{name} is required")
+        if name == "value_new" and mla:
+            raise ValueError("value_new must be None when value_cache is a view of key_cache (MLA)")
+        _check(t, name, kv_dtype, (3, 4))
+        shape = (args.batch, q_len, args.num_kv_heads, d) if t.dim() == 4 else (args.batch, args.num_kv_heads, d)
+        if t.dim() == 3 and q_len != 1:
+            raise ValueError(f"{name} must be [batch, q_len, kv_heads, dim] for q_len > 1")
+        if tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {shape} tensor, got {tuple(t.shape)}")
 
 
 def paged_attention_decode(
@@ -244,6 +280,43 @@ def paged_attention_decode(
         causal=causal, num_workers=num_workers, k_scale=k_scale, v_scale=v_scale,
     )
     launch(args, query.device)
+    return out
+
+
+def paged_attention_decode_append(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    key_new: torch.Tensor,
+    value_new: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    scale: float | None = None,
+    *,
+    causal: bool = False,
+    out_dtype: torch.dtype = torch.float32,
+    num_workers: int = 0,
+) -> torch.Tensor:
+    """KV-cache append fused into the decode (``simpler_hip_pa_decode_append``).
+
+    The ``q_len`` new tokens of sequence ``b`` are its last positions
+    ``context_lens[b] - q_len .. context_lens[b] - 1`` (the lengths count them):
+    their K/V (``key_new``/``value_new``, ``[B, q_len, Hkv, D]``) are written to
+    the caches at ``block_table[b, p // block_size]``, row ``p % block_size``, and
+    the decode attends over them, as ``kv_append`` with that slot mapping
+    followed by ``paged_attention_decode`` would. ``value_new`` is ``None`` for
+    MLA (V is a prefix of the K row). bf16 or fp16; q_len <= 16.
+    """
+    if scale is None:
+        scale = 1.0 / math.sqrt(query.shape[-1])
+    if out is None:
+        shape = (*query.shape[:-1], value_cache.shape[-1])
+        out = torch.empty(shape, dtype=out_dtype, device=query.device)
+    args = make_args(query, key_cache, value_cache, block_table, context_lens, out, scale, causal=causal,
+                     num_workers=num_workers)
+    append_tensors(args, query, key_cache, value_cache, key_new, value_new)
+    launch(args, query.device, key_new=key_new, value_new=value_new)
     return out
 
 

@@ -240,6 +240,23 @@ def test_mla_dispatch_and_plan():
         assert lib.simpler_hip_pa_decode(ctypes.byref(bad), ctypes.c_void_p(0x100000), 1 << 30, None) == -2
 
 
+def test_fused_append_validates_on_the_host():
+    lib = _lib.lib()
+    k, v = ctypes.c_void_p(0x7000), ctypes.c_void_p(0x8000)
+
+    def call(a, kn, vn, ws_bytes=1 << 30):
+        return lib.simpler_hip_pa_decode_append(ctypes.byref(a), kn, vn, ctypes.c_void_p(0x100000), ws_bytes, None)
+
+    assert call(_args(), None, v) == -1  # key_new is required
+    assert call(_args(), k, None) == -1  # and value_new for separate caches
+    assert call(_args(), ctypes.c_void_p(0x7008), v) == -1  # 16-byte aligned rows
+    assert call(_mla_args(), k, v) == -1  # MLA: V is the K prefix, no value_new
+    assert call(_args(q_len=17, num_heads=8, causal=1), k, v) == -2  # more than 16 new tokens
+    assert call(_args(kv_format=1, k_scale=0x9000, v_scale=0xA000), k, v) == -2  # no fused append for fp8
+    assert call(_args(), k, v, ws_bytes=16) == -4  # the decode's workspace rule
+    assert call(_mla_args(), k, None, ws_bytes=16) == -4
+
+
 def test_worker_plan():
     # without a device the launcher assumes an MI355X (256 CUs). 128-dim bf16 heads
     # read K in whole rows through LDS: one worker per SIMD

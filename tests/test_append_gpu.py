@@ -1,0 +1,183 @@
+"""KV-cache append fused into the decode (simpler_hip_pa_decode_append), on the GPU.
+
+The reference appends the current token's K/V into the paged pool at a slot
+derived from the block table and the sequence length
+(simpler_setup/goldens/qwen3_14b_decode.py:106-115,261-269) and then runs the
+decode over the context that includes it. Each case here runs the fused entry
+on caches whose new-token rows hold NaN, and checks:
+
+* the caches afterwards equal the oracle's append (``oracle/kv_oracle.py``,
+  slots from ``new_token_slots``) bit for bit;
+* the output equals, bit for bit, the plain decode run on those appended
+  caches (the same kernels reading the rows from the cache), and is within
+  the decode tolerance of the oracle.
+
+Shapes cover each kernel path: K staged through LDS (D = 128, one row tile),
+K in registers (D = 64), blocks larger than the registers (BS = 128,
+D = 256), sibling row-tile waves (causal q_len 8), fp16, MLA (576/512, two
+64-row groups), several worker counts, new tokens across a block boundary.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle
+from simpler_amd import paged_attention as pa
+from simpler_amd.workloads import DecodeCase, make_custom_case
+from tests.pa_helpers import assert_close, oracle_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def new_tokens(case: DecodeCase, seed: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    c = case.config
+    gen = torch.Generator("cpu").manual_seed(seed)
+    dt = case.key_cache.dtype
+    shape = (c.batch, c.q_len, c.kv_heads)
+    k = torch.randn((*shape, c.head_dim_k), generator=gen).to(dt)
+    v = None if c.mla else torch.randn((*shape, c.head_dim_v), generator=gen).to(dt)
+    return k, v
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def oracle_appended(case: DecodeCase, k_new: torch.Tensor, v_new: torch.Tensor | None) -> DecodeCase:
+    """The case with the new tokens written by the oracle's append."""
+    c = case.config
+    slots = kv_oracle.new_token_slots(case.block_table.numpy(), case.context_lens.numpy(), c.block_size, c.q_len)
+    kb, vb = kv_oracle.kv_append(u16(case.key_cache), None if c.mla else u16(case.value_cache),
+                                 u16(k_new).reshape(-1, c.kv_heads, c.head_dim_k),
+                                 None if c.mla else u16(v_new).reshape(-1, c.kv_heads, c.head_dim_v),
+                                 slots.reshape(-1))
+    to_t = lambda a: torch.from_numpy(a.view(np.int16)).view(case.key_cache.dtype)  # noqa: E731
+    key = to_t(kb)
+    value = key[..., : c.head_dim_v] if c.mla else to_t(vb)
+    return DecodeCase(c, case.seed, case.query, key, value, case.block_table, case.context_lens, case.scale)
+
+
+def poison_new_rows(case: DecodeCase) -> None:
+    """NaN in the cache rows the new tokens go to: the fused path must not read them."""
+    c = case.config
+    for b, n in enumerate(case.context_lens.tolist()):
+        for p in range(max(n - c.q_len, 0), n):
+            blk = int(case.block_table[b, p // c.block_size])
+            case.key_cache[blk, p % c.block_size] = float("nan")
+            if not c.mla:
+                case.value_cache[blk, p % c.block_size] = float("nan")
+
+
+def run_decode(case: DecodeCase, device, num_workers: int = 0, k_new=None, v_new=None):
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    if k_new is None:
+        pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out,
+                                  case.scale, causal=case.config.causal, num_workers=num_workers)
+    else:
+        pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens,
+                                         k_new.to(device), None if v_new is None else v_new.to(device), out,
+                                         case.scale, causal=case.config.causal, num_workers=num_workers)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    return out.cpu().numpy(), d.key_cache.cpu(), d.value_cache.cpu()
+
+
+CASES = {
+    # K through LDS (D = 128, one row tile), the headline kernel
+    "gqa_d128": dict(batch=4, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                     context_lens=[1, 128, 129, 3000]),
+    # K in registers
+    "gqa_d64_bs16": dict(batch=4, num_heads=16, kv_heads=4, head_dim=64, block_size=16, context_lens=[1, 16, 17, 300]),
+    "gqa_d16_bs64": dict(batch=2, num_heads=16, kv_heads=1, head_dim=16, block_size=64, context_lens=[33, 640]),
+    # blocks larger than the registers
+    "gqa_bs128_d256": dict(batch=3, num_heads=16, kv_heads=2, head_dim=256, block_size=128,
+                           context_lens=[1, 1000, 2049]),
+    # sibling row-tile waves; new tokens 122..129 straddle blocks 0 and 1
+    "verify_q8": dict(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, q_len=8, causal=True,
+                      context_lens=[8, 130, 2000]),
+    # 16 new tokens, one row tile per kv head, straddling 16-token blocks
+    "verify_q16": dict(batch=2, num_heads=2, kv_heads=2, head_dim=64, block_size=16, q_len=16, causal=True,
+                       context_lens=[16, 40]),
+    "fp16_d128": dict(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, context_lens=[5, 129, 900],
+                      dtype=torch.float16),
+    "mla_q1": dict(batch=3, num_heads=128, kv_heads=1, head_dim=576, head_dim_v=512, block_size=64, mla=True,
+                   context_lens=[1, 64, 700]),
+    "mla_q4": dict(batch=2, num_heads=16, kv_heads=1, head_dim=576, head_dim_v=512, block_size=32, mla=True,
+                   q_len=4, causal=True, context_lens=[4, 34]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+@pytest.mark.parametrize("workers", [0, 7])
+def test_fused_append_equals_append_then_decode(name, workers, device):
+    print(f"[case] append {name} workers={workers}", flush=True)
+    seed = 900 + sorted(CASES).index(name)
+    case = make_custom_case(seed=seed, **CASES[name])
+    k_new, v_new = new_tokens(case, seed + 1)
+    want = oracle_appended(case, k_new, v_new)
+    poison_new_rows(case)
+    got, key_after, value_after = run_decode(case, device, workers, k_new, v_new)
+    # caches: exactly the oracle's append
+    np.testing.assert_array_equal(u16(key_after), u16(want.key_cache))
+    if not case.config.mla:
+        np.testing.assert_array_equal(u16(value_after), u16(want.value_cache))
+    # output: the plain decode on the appended caches, bit for bit, and the oracle
+    plain, _, _ = run_decode(want, device, workers)
+    np.testing.assert_array_equal(got, plain)
+    assert_close(got, oracle_numpy(want), what=f"append {name}")
+
+
+@pytest.mark.parametrize("workers", [1, 1000])
+def test_fused_append_worker_counts_at_qwen3_shape(workers, device):
+    # 1 worker walks every block of every sequence; 1000 cut the new-token
+    # blocks into one-block pieces
+    print(f"[case] append qwen3 shape workers={workers}", flush=True)
+    case = make_custom_case(batch=8, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                            context_lens=[1, 127, 128, 129, 1000, 2047, 4096, 8191], seed=950)
+    k_new, v_new = new_tokens(case, 951)
+    want = oracle_appended(case, k_new, v_new)
+    poison_new_rows(case)
+    got, key_after, value_after = run_decode(case, device, workers, k_new, v_new)
+    np.testing.assert_array_equal(u16(key_after), u16(want.key_cache))
+    np.testing.assert_array_equal(u16(value_after), u16(want.value_cache))
+    plain, _, _ = run_decode(want, device, workers)
+    np.testing.assert_array_equal(got, plain)
+
+
+def test_fused_append_out_of_pool_block_is_reported_and_not_written(device):
+    case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
+                            context_lens=[300, 50], seed=960)
+    k_new, v_new = new_tokens(case, 961)
+    case.block_table[0, 2] = 10_000  # the block of sequence 0's new token (position 299)
+    d = case.to(device)
+    before = d.key_cache.clone(), d.value_cache.clone()
+    pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens,
+                                     k_new.to(device), v_new.to(device), scale=case.scale)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError):
+        pa.check_errors(device)
+    # only sequence 1's new token was written
+    changed = (d.key_cache != before[0]).any(dim=(2, 3)).nonzero().tolist()
+    blk1 = int(case.block_table[1, 0])
+    assert changed == [[blk1, 49]]
+    assert (d.value_cache != before[1]).any(dim=(2, 3)).nonzero().tolist() == [[blk1, 49]]
+    pa.check_errors(device)
+
+
+def test_fused_append_length_shorter_than_the_new_tokens_is_reported(device):
+    case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128, q_len=4,
+                            causal=True, context_lens=[300, 50], seed=970)
+    k_new, v_new = new_tokens(case, 971)
+    d = case.to(device)
+    lens = d.context_lens.clone()
+    lens[1] = 2  # below q_len
+    pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, lens, k_new.to(device),
+                                     v_new.to(device), scale=case.scale, causal=True)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError):
+        pa.check_errors(device)
+    pa.check_errors(device)

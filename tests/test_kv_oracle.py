@@ -27,6 +27,24 @@ def test_slot_of_matches_reference_identity_paging():
     np.testing.assert_array_equal(ko.slot_of(table, seq_lens, 128), expect)
 
 
+def test_new_token_slots_extend_the_reference_slot():
+    seq_lens = np.array([1, 3, 128, 129, 3500], dtype=np.int32)
+    table, expect = _identity_paging(5, 43, seq_lens, 128)
+    # one new token: the reference's current-token slot
+    np.testing.assert_array_equal(ko.new_token_slots(table, seq_lens, 128, 1)[:, 0], expect)
+    # four: positions len-4 .. len-1 under identity paging (page b*43 + pos//128), -1 below position 0
+    got = ko.new_token_slots(table, seq_lens, 128, 4)
+    for b, n in enumerate(seq_lens.tolist()):
+        for j in range(4):
+            p = n - 4 + j
+            assert got[b, j] == ((b * 43 + p // 128) * 128 + p % 128 if p >= 0 else -1)
+    # a shuffled table: each slot's block is the table entry of the position's logical block
+    rng = np.random.default_rng(3)
+    shuffled = rng.permutation(5 * 43).astype(np.int32).reshape(5, 43)
+    got = ko.new_token_slots(shuffled, seq_lens, 128, 2)
+    assert got[3, 0] == shuffled[3, 0] * 128 + 127 and got[3, 1] == shuffled[3, 1] * 128
+
+
 def test_append_writes_exactly_the_slots():
     rng = np.random.default_rng(1)
     nblk, bs, hkv, d = 12, 16, 3, 8
