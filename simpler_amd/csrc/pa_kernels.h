@@ -304,6 +304,20 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
 // interleave heads within a row).
 __device__ __forceinline__ int lane_tiles(const KernelParams &P) { return P.kv_heads * P.row_groups / P.lanes; }
 
+// Which tiles a list takes rotates with the batch: list u runs tile group
+// (u + b) mod lanes of batch b. Every list (and so every worker) then meets
+// every kv head, whose K/V streams run at different speeds depending on how
+// their rows map onto memory channels, instead of one list per head setting
+// the kernel's end. Neighbouring lists still read the heads of the same token
+// rows together.
+__device__ __forceinline__ int list_tile0(const KernelParams &P, int list, int b) {
+    return ((list + b) % P.lanes) * lane_tiles(P);
+}
+// The list that ran tile group g of batch b.
+__device__ __forceinline__ int list_of_tile(const KernelParams &P, int g, int b) {
+    return ((g - b) % P.lanes + P.lanes) % P.lanes;
+}
+
 // Wave-level scan over the batch for one list. Work of batch b = blocks_of(b)
 // * lane_tiles. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
 // before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
@@ -1216,7 +1230,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        const int jt = list * tpb + j;  // tile of the batch
+        const int jt = list_tile0(P, list, b) + j;  // tile of the batch
         const int kvh = jt / P.row_groups, rg = jt - kvh * P.row_groups;
         const int rt = rg * P.tiles_per_worker + wave;  // this wave's row tile
         // A worker touches at most two tiles partially: the first and the last
@@ -1278,7 +1292,7 @@ __global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const Ker
     const int kvh = jr / P.row_tiles, rt = jr - kvh * P.row_tiles;
     const int rg = rt / P.tiles_per_worker, wave = rt - rg * P.tiles_per_worker;
     const int jt = kvh * P.row_groups + rg;  // tile of the batch in the work lists
-    const int list = jt / lane_tiles(P), j = jt - list * lane_tiles(P);
+    const int list = list_of_tile(P, jt / lane_tiles(P), b), j = jt - (jt / lane_tiles(P)) * lane_tiles(P);
     const int rows_here = min(16, P.rows - rt * 16);
     int prefix = 0;
     const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
