@@ -207,19 +207,23 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
         const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && p.main == k.main);
         const int per_cu = one_per_simd ? kWorkersPerSimdCu : kWorkersPerCu;
         p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu);
-        // bf16 caches: one work list per tile of a batch when the worker count
-        // allows it, so the kv heads' workers walk the same blocks side by
-        // side (cfg3-like long contexts: 167.7 us against 173.4 us; the
-        // Qwen3-8B bs=32 shape and the verify shape: within 0.5%). fp8 caches,
-        // whose heads are single 128-byte lines of a 1 KB token row, measured
-        // 4% slower with it and keep one list.
+        // Work lists (the tiles of a batch shared out among them, rotating with
+        // the batch). 16-bit caches: one list per tile of a batch when the
+        // worker count allows it, so the kv heads' workers walk the same blocks
+        // side by side (cfg3-like long contexts: 167.7 us against 173.4 us
+        // with one list, and 176 with two tiles per list). fp8 caches, whose
+        // heads are single 128-byte lines of a 1 KB token row: four lists
+        // (60.5 us against 61.4 with one list and 62.4 with one per tile on
+        // the Qwen3-8B bs=32 shape).
         const int tpb = a->num_kv_heads * p.row_groups;
-        if (tpb > 1 && a->kv_format != SIMPLER_HIP_KV_FP8_E4M3) {
+        const bool fp8 = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3;
+        const int want_lanes = fp8 ? (tpb % 4 == 0 ? 4 : 1) : tpb;
+        if (want_lanes > 1) {
             if (a->num_workers > 0) {
-                if (p.workers % tpb == 0) p.lanes = tpb;
-            } else if (p.workers >= 4 * tpb) {
-                p.workers -= p.workers % tpb;
-                p.lanes = tpb;
+                if (p.workers % want_lanes == 0) p.lanes = want_lanes;
+            } else if (p.workers >= 4 * want_lanes) {
+                p.workers -= p.workers % want_lanes;
+                p.lanes = want_lanes;
             }
         }
         p.grid = p.workers;
