@@ -181,3 +181,53 @@ def test_fused_append_length_shorter_than_the_new_tokens_is_reported(device):
     with pytest.raises(pa.PagedAttentionError):
         pa.check_errors(device)
     pa.check_errors(device)
+
+
+@pytest.mark.parametrize("name", ["gqa_d128", "verify_q8", "mla_q1"])
+def test_fused_append_replays_from_a_hip_graph(name, device):
+    # The fused append allocates nothing once its workspace is sized, so a
+    # caller can capture it. Between replays, eager work changes the new
+    # tokens and poisons their cache rows again; every replay must write the
+    # new rows and match the plain decode on the appended caches.
+    print(f"[case] append hip graph replays {name}", flush=True)
+    seed = 980 + sorted(CASES).index(name)
+    case = make_custom_case(seed=seed, **CASES[name])
+    news = [new_tokens(case, seed + 1), new_tokens(case, seed + 2)]
+    wants = [oracle_appended(case, k, v) for k, v in news]
+    plains = [run_decode(w, device)[0] for w in wants]
+    poison_new_rows(case)
+    d = case.to(device)
+    k_dev = news[0][0].to(device)
+    v_dev = None if case.config.mla else news[0][1].to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+
+    def step():
+        pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens,
+                                         k_dev, v_dev, out, case.scale, causal=case.config.causal)
+
+    side = torch.cuda.Stream(device)
+    with torch.cuda.stream(side):
+        step()  # sizes and zeroes the capture stream's workspace outside the capture
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step()
+    torch.cuda.synchronize(device)
+    poisoned_k, poisoned_v = case.key_cache.to(device), case.value_cache.to(device)
+    for i in range(4):
+        k = i % 2
+        k_dev.copy_(news[k][0].to(device))
+        if v_dev is not None:
+            v_dev.copy_(news[k][1].to(device))
+        d.key_cache.copy_(poisoned_k)
+        if not case.config.mla:
+            d.value_cache.copy_(poisoned_v)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        np.testing.assert_array_equal(u16(d.key_cache.cpu()), u16(wants[k].key_cache))
+        if not case.config.mla:
+            np.testing.assert_array_equal(u16(d.value_cache.cpu()), u16(wants[k].value_cache))
+        np.testing.assert_array_equal(out.cpu().numpy(), plains[k])
+    pa.check_errors(device)
