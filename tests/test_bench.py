@@ -1,0 +1,53 @@
+"""bench.py's contract: one JSON line with the headline metric, the roofline and
+the CPU baseline; more than one GPU is refused with a message."""
+
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def run_bench(*args: str, timeout: int = 240) -> subprocess.CompletedProcess:
+    return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True, text=True,
+                          timeout=timeout, cwd=ROOT)
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    res = run_bench("--gpus", "2", "--steps", "1", "--warmup", "0")
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr
+    assert res.stdout.strip() == ""
+
+
+@pytest.mark.gpu
+def test_default_line_carries_the_contract(device, capsys, monkeypatch):
+    # in this process (the test process already holds the GPU: no child process)
+    print("[case] bench.py default config, short run", flush=True)
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "5", "--warmup", "2", "--cpu-seconds", "1"])
+    assert bench.main() == 0
+    out = capsys.readouterr().out
+    lines = [l for l in out.splitlines() if l.startswith("{")]
+    assert len(lines) == 1
+    line = json.loads(lines[0])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+                "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in line, key
+    assert line["n_gpus"] == 1 and line["steps"] == 5 and line["warmup"] == 2
+    assert line["unit"] == "GB/s" and line["higher_is_better"] is True and line["dtype"] == "bf16"
+    assert line["config"]["workload"].startswith("cfg2_qwen3_8b")
+    roof = line["roofline"]
+    assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
+    assert 0 < roof["frac"] < 1 and abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    # the step's throughput (both kernels) is below the main kernel's alone
+    assert 0 < line["value"] <= roof["achieved"]
+    cpu = line["cpu_baseline"]
+    assert cpu["kind"] in ("port", "reference") and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
