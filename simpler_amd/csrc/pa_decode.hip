@@ -37,6 +37,7 @@ struct Plan {
     int tiles_per_worker;
     int row_groups;
     int threads;  // per worker workgroup
+    size_t lds;   // dynamic LDS per workgroup (sibling waves' K buffers)
     int groups;   // workgroups per worker (MLA row groups), else 1
     int lanes;    // work lists (KernelParams::lanes)
     int64_t grid;
@@ -132,12 +133,13 @@ Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
 // four (one per SIMD).
 // Without a device (host-only builds and tests) an MI355X is assumed:
 // 256 CUs.
-int wave_slots(KernelFn fn, int threads, int want_per_cu) {
+int wave_slots(KernelFn fn, int threads, int want_per_cu, size_t lds = 0) {
     struct Entry {
         KernelFn fn;
         int device;
         int threads;
         int want;
+        size_t lds;
         int slots;
     };
     static std::mutex mu;
@@ -146,7 +148,8 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu) {
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     std::lock_guard<std::mutex> lk(mu);
     for (const Entry &e : cache)
-        if (e.fn == fn && e.device == dev && e.threads == threads && e.want == want_per_cu) return e.slots;
+        if (e.fn == fn && e.device == dev && e.threads == threads && e.want == want_per_cu && e.lds == lds)
+            return e.slots;
     // kWorkersPerCu workgroups per CU, or as many as fit (a 4-wave workgroup
     // fills a CU at one wave per SIMD). Two 2-wave workers per CU measured
     // 195.5 us on the speculative-verify shape against 213.9 us with one.
@@ -161,13 +164,13 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn),
-                                                         threads, 0) == hipSuccess &&
+                                                         threads, lds) == hipSuccess &&
             n > 0 && n < per_cu)
             per_cu = n;
     }
     (void)hipGetLastError();
     const int slots = cus * per_cu;
-    cache.push_back({fn, dev, threads, want_per_cu, slots});
+    cache.push_back({fn, dev, threads, want_per_cu, lds, slots});
     return slots;
 }
 
@@ -198,6 +201,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
         p.tiles_per_worker = p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker;
         p.threads = 64 * p.tiles_per_worker;
         p.main = p.tiles_per_worker > 1 ? k.main_multi : k.main;
+        if (k.klds && p.tiles_per_worker > 1) p.lds = (size_t)p.tiles_per_worker * a->block_size * 256;
         p.groups = 1;
         p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
         // One worker per SIMD when K is read in whole rows (through LDS) and for
@@ -206,7 +210,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
         // four.
         const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && p.main == k.main);
         const int per_cu = one_per_simd ? kWorkersPerSimdCu : kWorkersPerCu;
-        p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu);
+        p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu, p.lds);
         // Work lists (the tiles of a batch shared out among them, rotating with
         // the batch). 16-bit caches: one list per tile of a batch when the
         // worker count allows it, so the kv heads' workers walk the same blocks
@@ -368,7 +372,7 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
-        hipLaunchKernelGGL(plan.main, dim3((unsigned)plan.grid), dim3((unsigned)plan.threads), 0,
+        hipLaunchKernelGGL(plan.main, dim3((unsigned)plan.grid), dim3((unsigned)plan.threads), (unsigned)plan.lds,
                            (hipStream_t)stream, P);
         if (hipGetLastError() != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
     }

@@ -788,11 +788,13 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
 // lane group qd holds dims 16·qd + 64·(kk/2) + 8·(kk%2) .. +7, and Q is loaded
 // in the same order.
 //
-// KLDS (bf16, DK = 128): K is read like V, as whole 256-byte token rows (lane
-// (qd, pc) reads 16-byte chunk pc of token 4qd+e of each 16-token tile, so
-// one instruction covers four full rows), with non-temporal loads, and is
-// rearranged into the QK operand layout through this wave's BS x 256-byte LDS
-// buffer `klds`. Chunk c of token T sits at slot c ^ (T & 15) of the token's
+// KLDS (16-bit caches, DK = 128): K is read like V, as whole 256-byte token
+// rows (lane (qd, pc) reads 16-byte chunk pc of token 4qd+e of each 16-token
+// tile, so one instruction covers four full rows; a compute unit's load path
+// moves such rows about four times faster than the half-line reads of the
+// register layout), with non-temporal loads (plain loads for sibling waves),
+// and is rearranged into the QK operand layout through this wave's
+// BS x 256-byte LDS buffer `klds`. Chunk c of token T sits at slot c ^ (T & 15) of the token's
 // LDS row, so the row writes and the operand reads each touch 16 distinct
 // 16-byte slots per 16 lanes. The K registers are free once a block is in
 // LDS, so the next block's K is issued before this block's QK.
@@ -1203,12 +1205,16 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
     static_assert(!KV8 || BS * DK <= 16384, "fp8 caches: blocks that fit the registers");
-    // single-tile bf16 workers with 128-dim heads stage K through LDS
-    constexpr bool KLDS = MAXW == 1 && !KV8 && DK == 128;
-    __shared__ __attribute__((aligned(16))) char klds[KLDS ? BS * 256 : 16];
+    // 16-bit caches with 128-dim heads stage K through LDS, BS x 256 bytes per
+    // wave: a static buffer for single-wave workers, the launch's dynamic LDS
+    // (one buffer per sibling wave of the workgroup) otherwise
+    constexpr bool KLDS = !KV8 && DK == 128;
+    __shared__ __attribute__((aligned(16))) char klds1[(KLDS && MAXW == 1) ? BS * 256 : 16];
+    extern __shared__ __attribute__((aligned(16))) char klds_waves[];
     flag_bad_lengths(P);
     const int w = blockIdx.x;
     const int wave = MAXW == 1 ? 0 : (int)(threadIdx.x >> 6);
+    char *const klds = MAXW == 1 ? klds1 : klds_waves + wave * (BS * 256);
     const int tpb = lane_tiles(P);
     const int list = w % P.lanes;
     int start = 0, end = 0, b = 0, prefix = 0;
@@ -1987,7 +1993,7 @@ struct KernelPair {
     KernelFn main;        // one wave per worker (MLA: the four-wave LDS kernel); null if unsupported
     KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     bool mla;
-    bool klds;  // `main` stages K through LDS (full-row K reads)
+    bool klds;  // stages K through LDS (full-row K reads); main_multi in dynamic LDS, BS x 256 B per wave
 };
 
 struct MergeFn {
