@@ -920,10 +920,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             }
         }
     };
-    auto load_v = [&](auto &vdst, auto &vrawdst, int phys, int blk) {
+    auto load_v_tile = [&](auto &vdst, auto &vrawdst, int phys, int blk, int t) {
         const char *vb = v_head + (int64_t)phys * P.v_block_stride * ESZ;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const char *vt = tile_base(vb, blk, t, v_tok_b) + (int64_t)e * v_tok_b;
@@ -941,12 +939,16 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 }
             }
     };
+    auto load_v = [&](auto &vdst, auto &vrawdst, int phys, int blk) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) load_v_tile(vdst, vrawdst, phys, blk, t);
+    };
 
     // One KV block: QK on kr (or the LDS copy), softmax, PV on vr / vrw.
     // before_qk and after_qk place the single-buffer pipeline's loads of the
     // next block's K.
     auto compute_block = [&](const int blk, const int phys_b, const bool blk_bad, auto &kr, auto &vr, auto &vrw,
-                             auto &&before_qk, auto &&after_qk) {
+                             auto &&before_qk, auto &&after_qk, auto &&after_pv_tile) {
         const bool first = (blk == blk_begin);
         if (blk_bad && lane == 0) atomicOr(P.error_flag, kErrBadBlock);
         float sc = P.scale, vs = 1.f;
@@ -1083,7 +1085,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (KV8 && v_zero) break;  // wave-uniform: the block adds nothing
+          if (!(KV8 && v_zero)) {  // wave-uniform: a zero-scale block adds nothing
             u32x4_t vt4[DVS][4];       // 8 bf16 dims of tokens 16t + 4qd + e
 #pragma unroll
             for (int ds = 0; ds < DVS; ++ds)
@@ -1118,17 +1120,25 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                     const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
                     acc[ds][jj] = Elem<ET>::mma16(pa[t], (u32x2_t){d0, d1}, acc[ds][jj]);
                 }
+          }
+            after_pv_tile(t);
         }
     };
 
     // Per block i: V(i) is issued first, then QK(i) consumes K(i) (issued
     // during block i-1), then K(i+1) is issued (with K staged through LDS: as
-    // soon as K(i) is in LDS, before QK(i)), then softmax and PV(i). The
-    // scheduling barriers keep the compiler from sinking loads past the math,
-    // which would serialise the memory latency. The segment's last block is
-    // peeled off (no K(i+1)): with the prefetch under a run-time condition the
-    // compiler's wait counts would have to cover the path without it, so PV(i)
-    // would wait for K(i+1) as well.
+    // soon as K(i) is in LDS, before QK(i)), then softmax and PV(i). fp8
+    // caches (kRefillV) issue V(i+1) earlier instead: as PV(i) finishes with
+    // V(i)'s token tile t, V(i+1)'s tile t goes into the same registers, so V
+    // stays in flight through the math without a second register set (fp8
+    // cfg2 shape 58.8 against 59.5-59.7 us; neutral for 16-bit caches and
+    // 1.3% slower for sibling waves). The scheduling barriers keep the
+    // compiler from sinking loads past the math, which would serialise the
+    // memory latency. The segment's last block is peeled off (no K(i+1),
+    // V(i+1)): with the prefetch under a run-time condition the compiler's
+    // wait counts would have to cover the path without it, so PV(i) would wait
+    // for K(i+1) as well.
+    constexpr bool kRefillV = KV8;
     bool bad = false;
     int phys = checked(bt_row[blk_begin], bad);
     auto step = [&](const int blk, auto has_next) {
@@ -1140,7 +1150,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
         // block's loads together lets the caches serve the second request.
         if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
-        load_v(vreg, vraw, phys_b, blk);
+        if constexpr (!kRefillV) load_v(vreg, vraw, phys_b, blk);
         auto stage_k_and_prefetch = [&] {
             if constexpr (KLDS) {
                 // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
@@ -1164,11 +1174,15 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                 load_k(kreg, phys, blk + 1);
             }
         };
-        compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k);
+        auto refill_v = [&](int t) {  // after PV(i) of token tile t; phys is block i+1's by then
+            if constexpr (kRefillV && NEXT) load_v_tile(vreg, vraw, phys, blk + 1, t);
+        };
+        compute_block(blk, phys_b, blk_bad, kreg, vreg, vraw, stage_k_and_prefetch, prefetch_k, refill_v);
     };
     // blocks [blk_begin, end), end > blk_begin, through the pipeline
     auto pipeline = [&](const int end) {
         load_k(kreg, phys, blk_begin);
+        if constexpr (kRefillV) load_v(vreg, vraw, phys, blk_begin);
         for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{});
         step(end - 1, std::false_type{});
     };
