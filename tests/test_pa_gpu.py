@@ -139,6 +139,25 @@ def test_row_tiles_share_a_worker(heads, q_len, workers, device):
     assert_close(run_gpu(case, device, num_workers=workers), oracle_numpy(case), what=f"rowtiles{heads}x{q_len}")
 
 
+@pytest.mark.parametrize("bs,heads,q_len,dtype,workers", [(128, 64, 1, torch.bfloat16, 0),
+                                                          (128, 16, 3, torch.bfloat16, 0),
+                                                          (16, 64, 1, torch.bfloat16, 7),
+                                                          (128, 40, 2, torch.float16, 0),
+                                                          (32, 32, 1, torch.float16, 333)])
+def test_sibling_waves_stage_k_through_lds(bs, heads, q_len, dtype, workers, device):
+    # 128-dim heads with several row tiles per kv head: every sibling wave of a
+    # workgroup stages K in its own BS x 256 bytes of the launch's dynamic LDS
+    # (four waves x 32 KB at BS = 128). 64 rows -> 4 tiles, 48 -> 3, 80 -> 5
+    # (a second row group with one live wave), 32 -> 2.
+    print(f"[case] sibling K through LDS bs={bs} rows={heads * q_len} {dtype} workers={workers}", flush=True)
+    case = make_custom_case(batch=3, num_heads=heads, kv_heads=1, head_dim=128, block_size=bs, q_len=q_len,
+                            causal=q_len > 1, context_lens=[q_len, 3 * bs + 5, 2000], seed=330 + heads + bs,
+                            dtype=dtype)
+    got = run_gpu(case, device, num_workers=workers)
+    pa.check_errors(device)
+    assert_close(got, oracle_numpy(case), what=f"sibling-klds bs{bs} rows{heads * q_len}")
+
+
 def test_causal_fully_masked_last_block(device):
     # prefix ends on a block boundary: rows 0..q_len-2 see nothing of the last block
     case = make_custom_case(batch=1, num_heads=4, kv_heads=1, head_dim=64, block_size=16, q_len=4, causal=True,
