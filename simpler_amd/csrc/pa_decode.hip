@@ -174,7 +174,9 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu, size_t lds = 0) {
     return slots;
 }
 
-Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: the main kernels of pick_kernel
+// k: the main kernels of pick_kernel; allow_pair false: no two-tile waves
+// (the fused append runs two-tile shapes as sibling waves).
+Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, bool allow_pair = true) {
     Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
@@ -197,18 +199,20 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
         p.grid = (int64_t)p.workers * p.groups;
     } else {
         // Row tiles of one kv head run as sibling waves of one worker workgroup
-        // (up to four), so K/V of a block is fetched once for all of them.
-        p.tiles_per_worker = p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker;
-        p.threads = 64 * p.tiles_per_worker;
-        p.main = p.tiles_per_worker > 1 ? k.main_multi : k.main;
-        if (k.klds && p.tiles_per_worker > 1) p.lds = (size_t)p.tiles_per_worker * a->block_size * 256;
+        // (up to four), so K/V of a block is fetched once for all of them;
+        // two row tiles with K through LDS run in one wave instead.
+        const bool pair = allow_pair && k.main_pair && p.row_tiles == 2;
+        p.tiles_per_worker = pair ? 2 : (p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker);
+        p.threads = pair ? 64 : 64 * p.tiles_per_worker;
+        p.main = pair ? k.main_pair : p.tiles_per_worker > 1 ? k.main_multi : k.main;
+        if (!pair && k.klds && p.tiles_per_worker > 1) p.lds = (size_t)p.tiles_per_worker * a->block_size * 256;
         p.groups = 1;
         p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
         // One worker per SIMD when K is read in whole rows (through LDS) and for
         // fp8 caches; two per CU when K is read in half lines, whose plain
         // loads rely on the L1 merging the two halves and evict each other at
         // four.
-        const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && p.main == k.main);
+        const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && (p.main == k.main || pair));
         const int per_cu = one_per_simd ? kWorkersPerSimdCu : kWorkersPerCu;
         p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu, p.lds);
         // Work lists (the tiles of a batch shared out among them, rotating with
@@ -324,7 +328,7 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     const bool append = k_new != nullptr;
     const Kernels s = pick_kernel(a, append);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    Plan plan = make_plan(a, s.k);
+    Plan plan = make_plan(a, s.k, !append);
     if (append) plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : s.ka.main;
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
     if (a->batch == 0) return SIMPLER_HIP_OK;

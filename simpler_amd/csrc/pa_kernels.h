@@ -803,7 +803,7 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
 // ET: the element type of the query and bf16/fp16 caches (fp8 caches widen
 // to bf16, so KV8 takes ET = bf16).
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16,
-          bool APPEND = false>
+          bool APPEND = false, int RTW = 1>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int ctx, const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
@@ -816,29 +816,35 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     static_assert(!KLDS || (!KV8 && DK == 128), "K through LDS: 16-bit caches, DK = 128");
     static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
     static_assert(!(KV8 && APPEND), "fused append: 16-bit caches");
+    static_assert(RTW == 1 || (KLDS && !APPEND), "two row tiles per wave: K through LDS, no fused append");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
-    const int rows_here = min(16, P.rows - rt * 16);
 
-    // ---- Q^T operand (row pc, dims 32kk+8qd..) and this row's visible length ----
-    int rowlen = 0;
-    u32x4_t qv[KS];
+    // ---- Q^T operand (row pc, dims 32kk+8qd..) and this row's visible
+    // length, for each of the wave's RTW row tiles rt, rt+1, .. ----
+    int rowlen[RTW];
+    u32x4_t qv[RTW][KS];
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
-    if (pc < rows_here) {
-        const int r = rt * 16 + pc;
-        const int i = r / P.group, hh = r - i * P.group;
-        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
+    for (int r = 0; r < RTW; ++r) {
+        rowlen[r] = 0;
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-            const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
-            if (DK % 32 == 0 || dim < DK) qv[kk] = ld16(qrow + dim);
+        for (int kk = 0; kk < KS; ++kk) qv[r][kk] = (u32x4_t){0u, 0u, 0u, 0u};
+        if (pc < min(16, P.rows - (rt + r) * 16)) {
+            const int row = (rt + r) * 16 + pc;
+            const int i = row / P.group, hh = row - i * P.group;
+            const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
+                if (DK % 32 == 0 || dim < DK) qv[r][kk] = ld16(qrow + dim);
+            }
+            rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
         }
-        rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
     }
-    // shortest visible length over the valid rows of this tile (wave-uniform):
-    // blocks that end at or before it need no masking.
+    // shortest visible length over the valid rows of the wave's tiles
+    // (wave-uniform; the first tile's first row): blocks that end at or before
+    // it need no masking.
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
 
     // Block-table entries are read through the scalar cache (constant address
@@ -848,17 +854,23 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     const __attribute__((address_space(4))) int32_t *bt_row =
         (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
 
-    f32x4_t acc[DVS][8];
-#pragma unroll
-    for (int ds = 0; ds < DVS; ++ds)
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[RTW][DVS][8];
     // Row sums of the rounded p on the matrix unit (P x ones), kept in A's
     // frame: every lane holds rows 4qd+e like A's columns.
-    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t lacc[RTW];
+    float m_run[RTW], f_run[RTW];
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+#pragma unroll
+        for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) acc[r][ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        lacc[r] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        m_run[r] = kNegClamp;
+        f_run[r] = kNegClamp;
+    }
     const u32x2_t ones4 = (u32x2_t){Elem<ET>::kOnePair, Elem<ET>::kOnePair};  // 1.0 of the element type
     constexpr float kLog2e = 1.4426950408889634f;
-    float m_run = kNegClamp, f_run = kNegClamp;
 
     // bf16: the operands themselves; fp8: the raw bytes (half the registers)
     u32x4_t kreg[NT][KV8 ? KS / 2 : KS];
@@ -961,105 +973,112 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         __builtin_amdgcn_sched_barrier(0);
         before_qk();
 
-        // ---- QK: S^T tiles ----
-        f32x4_t s[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-                u32x4_t kop;
-                if constexpr (KV8) {
-                    const u32x4_t raw = kr[t][kk >> 1];
-                    kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
-                } else if constexpr (KLDS) {
-                    kop = lds_ld16(klds, t * 4096 + kr_off[kk]);
-                } else {
-                    kop = kr[t][kk];
-                }
-                c = Elem<ET>::mma32(kop, qv[kk], c);
-            }
-            s[t] = c;
-        }
-
-        __builtin_amdgcn_sched_barrier(0);
-        after_qk();
-        __builtin_amdgcn_sched_barrier(0);
-
-        // ---- softmax prepare: mask, block max of s*scale (golden :145-165).
-        // For scale > 0 the max of the scaled scores is the scaled max, so the
-        // scale folds into the exponent below; otherwise scale first ----
-        if (!(sc > 0.f)) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) s[t] *= sc;
-            sc = 1.f;
-        }
         const int blk0 = blk * BS;
         const bool full = !blk_bad && (blk0 + BS <= min_rowlen);
-        const int rvalid = blk_bad ? 0 : rowlen - blk0;  // tokens of this block visible to row pc
-        // one wave-uniform branch around the masking (per-element selects
-        // would run on every block)
-        if (!full) {
+        const bool v_zero = KV8 && vs == 0.f;  // this block's V is zero: nothing to add
+        // For scale > 0 the max of the scaled scores is the scaled max, so the
+        // scale folds into the exponent below; otherwise scores are scaled first.
+        const bool prescale = !(sc > 0.f);
+        const float scl = prescale ? 1.f : sc;
+        u32x2_t pa[RTW][NT];
+        // row tile by row tile (one tile's scores live at a time; a second
+        // tile reads K from LDS again)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            // ---- QK: S^T tiles ----
+            f32x4_t s[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) {
+                    u32x4_t kop;
+                    if constexpr (KV8) {
+                        const u32x4_t raw = kr[t][kk >> 1];
+                        kop = (kk & 1) ? fp8x8_to_bf16x8(raw[2], raw[3]) : fp8x8_to_bf16x8(raw[0], raw[1]);
+                    } else if constexpr (KLDS) {
+                        kop = lds_ld16(klds, t * 4096 + kr_off[kk]);
+                    } else {
+                        kop = kr[t][kk];
+                    }
+                    c = Elem<ET>::mma32(kop, qv[r][kk], c);
+                }
+                s[t] = c;
+            }
+            if (r == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                after_qk();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+
+            // ---- softmax prepare: mask, block max of s*scale (golden :145-165) ----
+            if (prescale) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) s[t] *= sc;
+            }
+            const int rvalid = blk_bad ? 0 : rowlen[r] - blk0;  // tokens of this block visible to row pc
+            // one wave-uniform branch around the masking (per-element selects
+            // would run on every block)
+            if (!full) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+            }
+            float mx = -INFINITY;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mb = fmaxf(mx * sc, kNegClamp);
+                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mb = fmaxf(mx * scl, kNegClamp);
 
-        // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
-        const float mnew = first ? mb : fmaxf(m_run, mb);
-        const bool use = first || (mb >= mnew - kFrameGap);
-        const float cfe = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);  // e^{f - m_blk}
-        float cf = cfe;
-        const bool v_zero = KV8 && vs == 0.f;  // this block's V is zero: nothing to add
-        if (KV8 && use && !v_zero) {            // move this row's A into the block's V-scale frame
-            cf *= vs_frame / vs;
-            vs_frame = vs;
-        }
-
-        // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e -
-        // m_blk*log2e)); a skipped block (use false) gives p = 0 ----
-        const float mb2 = use ? mb * kLog2e : INFINITY;
-        const float sc2 = sc * kLog2e;
-        u32x2_t pa[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float p[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
-            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
-        }
-        m_run = mnew;
-        if (use) f_run = mb;
-
-        // ---- rescale A (and its row sums) to the new frame (rows 4qd+e live
-        // in lane 4qd+e's factors) ----
-        {
-            f32x4_t cv, cl;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                cv[e] = __shfl(cf, 4 * qd + e, 64);
-                cl[e] = KV8 ? __shfl(cfe, 4 * qd + e, 64) : cv[e];
+            // ---- online merge coefficients (aiv_online_update.cpp:183-207) ----
+            const float mnew = first ? mb : fmaxf(m_run[r], mb);
+            const bool use = first || (mb >= mnew - kFrameGap);
+            const float cfe = first ? 0.f : (use ? __expf(f_run[r] - mb) : 1.f);  // e^{f - m_blk}
+            float cf = cfe;
+            if (KV8 && use && !v_zero) {  // move this row's A into the block's V-scale frame
+                cf *= vs_frame / vs;
+                vs_frame = vs;
             }
+
+            // ---- p = bf16(exp(s*scale - m_blk)) = bf16(exp2(s*scale*log2e -
+            // m_blk*log2e)); a skipped block (use false) gives p = 0 ----
+            const float mb2 = use ? mb * kLog2e : INFINITY;
+            const float sc2 = scl * kLog2e;
 #pragma unroll
-            for (int ds = 0; ds < DVS; ++ds)
+            for (int t = 0; t < NT; ++t) {
+                float p[4];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
-            lacc *= cl;
+                for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
+                pa[r][t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
+            }
+            m_run[r] = mnew;
+            if (use) f_run[r] = mb;
+
+            // ---- rescale A (and its row sums) to the new frame (rows 4qd+e
+            // live in lane 4qd+e's factors) ----
+            {
+                f32x4_t cv, cl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    cv[e] = __shfl(cf, 4 * qd + e, 64);
+                    cl[e] = KV8 ? __shfl(cfe, 4 * qd + e, 64) : cv[e];
+                }
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) acc[r][ds][jj] *= cv;
+                lacc[r] *= cl;
+            }
+            // row sums of the rounded p (every column of P x ones is the
+            // sum), also for a block whose V adds nothing
+#pragma unroll
+            for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
         }
-        // row sums of the rounded p (every column of P x ones is the sum),
-        // also for a block whose V adds nothing
-#pragma unroll
-        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
 
         // ---- PV: A += P * V ----
         const int vvalid = (blk_bad || v_zero) ? 0 : min(BS, ctx - blk0);  // tokens with defined V
@@ -1118,7 +1137,9 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                     const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
                     const unsigned d0 = __builtin_amdgcn_perm(a1, a0, sel);
                     const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
-                    acc[ds][jj] = Elem<ET>::mma16(pa[t], (u32x2_t){d0, d1}, acc[ds][jj]);
+#pragma unroll
+                    for (int r = 0; r < RTW; ++r)
+                        acc[r][ds][jj] = Elem<ET>::mma16(pa[r][t], (u32x2_t){d0, d1}, acc[r][ds][jj]);
                 }
           }
             after_pv_tile(t);
@@ -1195,14 +1216,17 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const int pipe_end = max(blk_begin, min(blk_end, ctx - P.q_len < 0 ? 0 : (ctx - P.q_len) / BS));
         if (pipe_end > blk_begin) pipeline(pipe_end);
         if (pipe_end < blk_end)
-            unpipelined_blocks<BS, DK, DV, ET, true>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
-                                                     min_rowlen, acc, lacc, m_run, f_run);
+            unpipelined_blocks<BS, DK, DV, ET, true>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv[0],
+                                                     rowlen[0], min_rowlen, acc[0], lacc[0], m_run[0], f_run[0]);
     } else {
         pipeline(blk_end);
     }
 
-    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run,
-                             vs_frame);
+    // tile rt + r's pieces sit r pieces-of-a-worker-wave further on (two slots each)
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+        finish_segment<DV, OutT>(P, b, kvh, rt + r, nblk, blk_begin, blk_end, part_o + r * (2 * 16 * DV),
+                                 part_ml + r * (2 * 32), acc[r], lacc[r], m_run[r], f_run[r], vs_frame);
 }
 
 // ---------------------------------------------------------------------------
@@ -1213,8 +1237,10 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 // four sibling waves, one per row tile, walk the same KV blocks, so V is loaded
 // through the caches (the siblings hit each other's lines) rather than
 // streamed past them.
+// RTW = 2 (with MAXW = 1): one wave runs both row tiles of a row group,
+// every K and V operand feeding the two tiles' MFMAs.
 template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16,
-          bool APPEND = false>
+          bool APPEND = false, int RTW = 1>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
@@ -1265,9 +1291,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
             if constexpr (BS * DK > 16384 || BS * DV > 16384)  // a block's K or V exceeds the registers
                 run_segment_big<BS, DK, DV, OutT, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
             else
-                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk,
-                                                                                 blk + seg, po, pml,
-                                                                                 MAXW > 1 && full_group, klds);
+                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND, RTW>(
+                    P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml, MAXW > 1 && full_group, klds);
         }
         pos += seg;
         slot = 1;
@@ -2008,6 +2033,7 @@ struct KernelPair {
     KernelFn main_multi;  // up to kMaxWavesPerWorker waves per worker
     bool mla;
     bool klds;  // stages K through LDS (full-row K reads); main_multi in dynamic LDS, BS x 256 B per wave
+    KernelFn main_pair = nullptr;  // one wave per worker running two row tiles (K through LDS), or null
 };
 
 struct MergeFn {

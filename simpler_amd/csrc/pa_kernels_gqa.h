@@ -13,8 +13,10 @@ namespace {
 
 template <int BS, int D, typename OutT, typename ET, bool APPEND>
 KernelPair gqa_pair() {
-    return {pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND>,
-            pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, false, ET, APPEND>, false, D == 128};
+    KernelPair k{pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND>,
+                 pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, false, ET, APPEND>, false, D == 128};
+    if constexpr (D == 128 && !APPEND) k.main_pair = pa_decode_kernel<BS, D, D, OutT, 1, false, ET, false, 2>;
+    return k;
 }
 
 // Block sizes 16..128 and head dims 16..256 (a block with more than 16384
