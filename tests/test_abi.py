@@ -273,10 +273,12 @@ def test_worker_plan():
     zero_page = 16 * 2048 + 512
     assert ws(num_workers=7) == 256 + zero_page + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
     assert ws(num_workers=1) == 256 + zero_page + 256 + 2 * 16 * 128 * 4
-    # q_len 8 x group 4 = 32 rows = 2 row tiles: a worker is a 2-wave workgroup
-    # and keeps two partial slots per wave
-    assert pa.plan(_args(q_len=8, causal=1)) == 512
+    # q_len 8 x group 4 = 32 rows = 2 row tiles: with 128-dim heads one wave runs
+    # both (one worker per SIMD), two partial slots per row tile
+    assert pa.plan(_args(q_len=8, causal=1)) == 1024
     assert ws(q_len=8, causal=1, num_workers=7) == 256 + zero_page + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
+    # other head dims: a 2-wave workgroup (sibling waves), two per CU
+    assert pa.plan(_args(q_len=8, causal=1, head_dim_k=64, head_dim_v=64, k_head_stride=64, v_head_stride=64)) == 512
     # token strides too large for a 1 MB zero page: padding tiles are read as they are
     assert ws(num_workers=7, k_token_stride=1 << 15, v_token_stride=1 << 15, k_block_stride=1 << 22,
               v_block_stride=1 << 22) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
