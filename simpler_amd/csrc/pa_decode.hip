@@ -208,12 +208,18 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, bool allow_
         if (!pair && k.klds && p.tiles_per_worker > 1) p.lds = (size_t)p.tiles_per_worker * a->block_size * 256;
         p.groups = 1;
         p.row_groups = (p.row_tiles + p.tiles_per_worker - 1) / p.tiles_per_worker;
-        // One worker per SIMD when K is read in whole rows (through LDS) and for
-        // fp8 caches; two per CU when K is read in half lines, whose plain
-        // loads rely on the L1 merging the two halves and evict each other at
-        // four.
-        const bool one_per_simd = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3 || (k.klds && (p.main == k.main || pair));
-        const int per_cu = one_per_simd ? kWorkersPerSimdCu : kWorkersPerCu;
+        // One worker per SIMD when K is read in whole rows (through LDS); three
+        // per CU for fp8 caches and for two-tile waves, whose blocks take
+        // twice the math per byte (same-box medians at 768 against 1024
+        // workers: fp8 57.4 against 58.7 us, the verify shape 134.2 against
+        // 142.9; the single-tile kernel 108.2 against 108.9 on cfg2 but 165.5
+        // against 164.5 on cfg3, so it keeps four); two per CU when K is read
+        // in half lines, whose plain loads rely on the L1 merging the two
+        // halves and evict each other at four.
+        const bool fp8_kv = a->kv_format == SIMPLER_HIP_KV_FP8_E4M3;
+        const int per_cu = (fp8_kv || pair) ? kWorkersThreePerCu
+                           : (k.klds && p.main == k.main) ? kWorkersPerSimdCu
+                                                          : kWorkersPerCu;
         p.workers = a->num_workers > 0 ? a->num_workers : wave_slots(p.main, p.threads, per_cu, p.lds);
         // Work lists (the tiles of a batch shared out among them, rotating with
         // the batch). 16-bit caches: one list per tile of a batch when the

@@ -90,7 +90,8 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 constexpr float kNegClamp = -1e30f;  // goldens/paged_attention.py:160 clamp
 constexpr float kFrameGap = 40.f;
 constexpr int kWorkersPerCu = 2;       // default worker workgroups per compute unit (half-line K reads)
-constexpr int kWorkersPerSimdCu = 4;   // one worker per SIMD: full-row K reads and fp8 caches (see make_plan)
+constexpr int kWorkersPerSimdCu = 4;   // one worker per SIMD: full-row K reads (see make_plan)
+constexpr int kWorkersThreePerCu = 3;  // fp8 caches and two-tile waves: three single-wave workers per CU
 constexpr int kMaxWavesPerWorker = 4;  // row tiles per worker workgroup (256 threads)
 
 struct KernelParams {

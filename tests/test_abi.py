@@ -274,8 +274,8 @@ def test_worker_plan():
     assert ws(num_workers=7) == 256 + zero_page + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
     assert ws(num_workers=1) == 256 + zero_page + 256 + 2 * 16 * 128 * 4
     # q_len 8 x group 4 = 32 rows = 2 row tiles: with 128-dim heads one wave runs
-    # both (one worker per SIMD), two partial slots per row tile
-    assert pa.plan(_args(q_len=8, causal=1)) == 1024
+    # both (three workers per CU), two partial slots per row tile
+    assert pa.plan(_args(q_len=8, causal=1)) == 768
     assert ws(q_len=8, causal=1, num_workers=7) == 256 + zero_page + 7 * 2 * 2 * 32 * 4 + 7 * 2 * 2 * 16 * 128 * 4
     # other head dims: a 2-wave workgroup (sibling waves), two per CU
     assert pa.plan(_args(q_len=8, causal=1, head_dim_k=64, head_dim_v=64, k_head_stride=64, v_head_stride=64)) == 512
@@ -284,6 +284,8 @@ def test_worker_plan():
               v_block_stride=1 << 22) == 256 + 7 * 2 * 32 * 4 + 7 * 2 * 16 * 128 * 4
     # 25 row tiles: 4-wave workgroups, one per CU, in 7 work lists (row groups)
     assert pa.plan(_args(num_heads=80, num_kv_heads=1, q_len=5, causal=1)) == 252
+    # fp8 caches: three single-wave workers per CU, in four work lists
+    assert pa.plan(_args(kv_format=1, k_scale=0x7000, v_scale=0x7100)) == 768
 
 
 def test_work_list_must_fit_32_bit_indices():
