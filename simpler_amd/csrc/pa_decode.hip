@@ -174,9 +174,7 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu, size_t lds = 0) {
     return slots;
 }
 
-// k: the main kernels of pick_kernel; allow_pair false: no two-tile waves
-// (the fused append runs two-tile shapes as sibling waves).
-Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, bool allow_pair = true) {
+Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: the main kernels of pick_kernel
     Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
@@ -201,7 +199,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, bool allow_
         // Row tiles of one kv head run as sibling waves of one worker workgroup
         // (up to four), so K/V of a block is fetched once for all of them;
         // two row tiles with K through LDS run in one wave instead.
-        const bool pair = allow_pair && k.main_pair && p.row_tiles == 2;
+        const bool pair = k.main_pair && p.row_tiles == 2;
         p.tiles_per_worker = pair ? 2 : (p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker);
         p.threads = pair ? 64 : 64 * p.tiles_per_worker;
         p.main = pair ? k.main_pair : p.tiles_per_worker > 1 ? k.main_multi : k.main;
@@ -334,8 +332,9 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     const bool append = k_new != nullptr;
     const Kernels s = pick_kernel(a, append);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    Plan plan = make_plan(a, s.k, !append);
-    if (append) plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : s.ka.main;
+    Plan plan = make_plan(a, s.k);
+    if (append)
+        plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : plan.main == s.k.main_pair ? s.ka.main_pair : s.ka.main;
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
     if (a->batch == 0) return SIMPLER_HIP_OK;
 

@@ -513,17 +513,20 @@ __device__ __forceinline__ int tile_of(const int p, const int blk) {
 // starts at blk_begin.
 // ---------------------------------------------------------------------------
 
-template <int BS, int DK, int DV, typename ET, bool APPEND>
+// RTW row tiles rt, rt+1, .. of one wave (each K and V operand feeds every
+// tile's MFMAs); min_rowlen is the first tile's (the shortest).
+template <int BS, int DK, int DV, typename ET, bool APPEND, int RTW = 1>
 __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const int b, const int kvh, const int rt,
                                                    const int ctx, const int blk_begin, const int lo, const int hi,
-                                                   const u32x4_t (&qv)[(DK + 31) / 32], const int rowlen,
-                                                   const int min_rowlen, f32x4_t (&acc)[(DV + 127) / 128][8],
-                                                   f32x4_t &lacc, float &m_run, float &f_run) {
+                                                   const u32x4_t (&qv)[RTW][(DK + 31) / 32], const int (&rowlen)[RTW],
+                                                   const int min_rowlen, f32x4_t (&acc)[RTW][(DV + 127) / 128][8],
+                                                   f32x4_t (&lacc)[RTW], float (&m_run)[RTW], float (&f_run)[RTW]) {
     constexpr int NT = BS / 16;            // 16-token tiles per KV block
     constexpr int KS = (DK + 31) / 32;     // 32-dim k-steps of QK
     constexpr int DVS = (DV + 127) / 128;  // 128-dim column sets of PV
-    // tiles per load group: at most 128 registers of K (KS x 4 per tile) and of V (DVS x 16 per tile)
-    constexpr int GK = 32 / KS > 0 ? 32 / KS : 1;
+    // tiles per load group: at most 128 / RTW registers of K (KS x 4 per tile)
+    // and 128 of V (DVS x 16 per tile)
+    constexpr int GK = 32 / KS / RTW > 0 ? 32 / KS / RTW : 1;
     constexpr int GV = 8 / DVS > 0 ? 8 / DVS : 1;
     constexpr int GT0 = GK < GV ? GK : GV;
     constexpr int GT = GT0 < NT ? GT0 : NT;
@@ -587,7 +590,7 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
         const int tk = APPEND && blk_new ? tile_of<BS>(pk, blk) : -1;
 
         // ---- QK over every tile of the block, GT tiles of K at a time ----
-        f32x4_t s[NT];
+        f32x4_t s[RTW][NT];
 #pragma unroll
         for (int g = 0; g < NT; g += GT) {
             u32x4_t kr[GT][KS];
@@ -610,66 +613,72 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
                 }
             }
 #pragma unroll
-            for (int t = 0; t < GT; ++t) {
-                f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < GT; ++t)
 #pragma unroll
-                for (int kk = 0; kk < KS; ++kk) c = Elem<ET>::mma32(kr[t][kk], qv[kk], c);
-                s[g + t] = c;
-            }
+                for (int r = 0; r < RTW; ++r) {
+                    f32x4_t c = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < KS; ++kk) c = Elem<ET>::mma32(kr[t][kk], qv[r][kk], c);
+                    s[r][g + t] = c;
+                }
         }
 
         // ---- softmax prepare and the online-merge factor (as run_segment) ----
-        float sc = P.scale;
-        if (!(sc > 0.f)) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) s[t] *= sc;
-            sc = 1.f;
-        }
+        const float scale = P.scale;
+        const bool prescale = !(scale > 0.f);
+        const float sc = prescale ? 1.f : scale;
         const int blk0 = blk * BS;
         const bool full = !bad && (blk0 + BS <= min_rowlen);
-        const int rvalid = bad ? 0 : rowlen - blk0;
-        if (!full) {
+        u32x2_t pa[RTW][NT];
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            if (prescale) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) s[r][t] *= scale;
+            }
+            const int rvalid = bad ? 0 : rowlen[r] - blk0;
+            if (!full) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * t + 4 * qd + e >= rvalid) s[r][t][e] = -INFINITY;
+            }
+            float mx = -INFINITY;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (16 * t + 4 * qd + e >= rvalid) s[t][e] = -INFINITY;
+                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[r][t][e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mb = fmaxf(mx * sc, kNegClamp);
+            const float mnew = first ? mb : fmaxf(m_run[r], mb);
+            const bool use = first || (mb >= mnew - kFrameGap);
+            const float cf = first ? 0.f : (use ? __expf(f_run[r] - mb) : 1.f);
+            const float mb2 = use ? mb * kLog2e : INFINITY;
+            const float sc2 = sc * kLog2e;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float p[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r][t][e], sc2, -mb2));
+                pa[r][t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
+            }
+            m_run[r] = mnew;
+            if (use) f_run[r] = mb;
+            {
+                f32x4_t cv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) acc[r][ds][jj] *= cv;
+                lacc[r] *= cv;
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mb = fmaxf(mx * sc, kNegClamp);
-        const float mnew = first ? mb : fmaxf(m_run, mb);
-        const bool use = first || (mb >= mnew - kFrameGap);
-        const float cf = first ? 0.f : (use ? __expf(f_run - mb) : 1.f);
-        const float mb2 = use ? mb * kLog2e : INFINITY;
-        const float sc2 = sc * kLog2e;
-        u32x2_t pa[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float p[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][e], sc2, -mb2));
-            pa[t] = (u32x2_t){Elem<ET>::pack2(p[0], p[1]), Elem<ET>::pack2(p[2], p[3])};
-        }
-        m_run = mnew;
-        if (use) f_run = mb;
-        {
-            f32x4_t cv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) cv[e] = __shfl(cf, 4 * qd + e, 64);
-#pragma unroll
-            for (int ds = 0; ds < DVS; ++ds)
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) acc[ds][jj] *= cv;
-            lacc *= cv;
-        }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) lacc = Elem<ET>::mma16(pa[t], ones4, lacc);
 
         // ---- PV, GT tiles of V at a time; V rows past the context (or of an
         // out-of-pool block) are zeroed ----
@@ -705,7 +714,9 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
                         const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
                         const unsigned d0 = __builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel);
                         const unsigned d1 = __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel);
-                        acc[ds][jj] = Elem<ET>::mma16(pa[g + t], (u32x2_t){d0, d1}, acc[ds][jj]);
+#pragma unroll
+                        for (int r = 0; r < RTW; ++r)
+                            acc[r][ds][jj] = Elem<ET>::mma16(pa[r][g + t], (u32x2_t){d0, d1}, acc[r][ds][jj]);
                     }
         }
         // the new tokens of this block into the caches (row tile 0's wave)
@@ -763,20 +774,21 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
                                                 float *const part_o, float *const part_ml) {
     constexpr int KS = (DK + 31) / 32;
     constexpr int DVS = (DV + 127) / 128;
-    u32x4_t qv[KS];
-    int rowlen = 0;
-    load_query<DK>(P, b, kvh, rt, ctx, qv, rowlen);
+    u32x4_t qv[1][KS];
+    int rowlen[1] = {0};
+    load_query<DK>(P, b, kvh, rt, ctx, qv[0], rowlen[0]);
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - (rt * 16) / P.group) : ctx;
-    f32x4_t acc[DVS][8];
+    f32x4_t acc[1][DVS][8];
 #pragma unroll
     for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) acc[ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegClamp, f_run = kNegClamp;
+        for (int jj = 0; jj < 8; ++jj) acc[0][ds][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    f32x4_t lacc[1] = {(f32x4_t){0.f, 0.f, 0.f, 0.f}};
+    float m_run[1] = {kNegClamp}, f_run[1] = {kNegClamp};
     unpipelined_blocks<BS, DK, DV, ET, APPEND>(P, b, kvh, rt, ctx, blk_begin, blk_begin, blk_end, qv, rowlen,
                                                min_rowlen, acc, lacc, m_run, f_run);
-    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc, lacc, m_run, f_run, 1.f);
+    finish_segment<DV, OutT>(P, b, kvh, rt, nblk, blk_begin, blk_end, part_o, part_ml, acc[0], lacc[0], m_run[0],
+                             f_run[0], 1.f);
 }
 
 // KV8: K and V caches hold E4M3FN bytes with one fp32 scale per (block, kv
@@ -817,7 +829,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     static_assert(!KLDS || (!KV8 && DK == 128), "K through LDS: 16-bit caches, DK = 128");
     static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
     static_assert(!(KV8 && APPEND), "fused append: 16-bit caches");
-    static_assert(RTW == 1 || (KLDS && !APPEND), "two row tiles per wave: K through LDS, no fused append");
+    static_assert(RTW == 1 || KLDS, "two row tiles per wave: K through LDS");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -1217,8 +1229,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         const int pipe_end = max(blk_begin, min(blk_end, ctx - P.q_len < 0 ? 0 : (ctx - P.q_len) / BS));
         if (pipe_end > blk_begin) pipeline(pipe_end);
         if (pipe_end < blk_end)
-            unpipelined_blocks<BS, DK, DV, ET, true>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv[0],
-                                                     rowlen[0], min_rowlen, acc[0], lacc[0], m_run[0], f_run[0]);
+            unpipelined_blocks<BS, DK, DV, ET, true, RTW>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
+                                                          min_rowlen, acc, lacc, m_run, f_run);
     } else {
         pipeline(blk_end);
     }

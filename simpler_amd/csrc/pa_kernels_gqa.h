@@ -15,7 +15,7 @@ template <int BS, int D, typename OutT, typename ET, bool APPEND>
 KernelPair gqa_pair() {
     KernelPair k{pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND>,
                  pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, false, ET, APPEND>, false, D == 128};
-    if constexpr (D == 128 && !APPEND) k.main_pair = pa_decode_kernel<BS, D, D, OutT, 1, false, ET, false, 2>;
+    if constexpr (D == 128) k.main_pair = pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND, 2>;
     return k;
 }
 
