@@ -26,9 +26,10 @@
 // (tile, KV block) pairs, tile = (batch, kv head, row tile), in that order
 // (optionally as one list per tile of a batch; see lane_tiles).
 // A row is one (query token, head in the GQA group) pair; 16 rows per tile
-// (MFMA N). The main kernel launches one worker (a wavefront, or sibling
-// wavefronts for several row tiles) per slot of the GPU (CUs x workers per CU
-// at this kernel's occupancy) and gives each an equal contiguous slice of that
+// (MFMA N). The main kernel launches one worker (a wavefront; a wavefront
+// running two row tiles of a kv head; or sibling wavefronts for several row
+// tiles) per slot of the GPU (CUs x workers per CU at this kernel's
+// occupancy) and gives each an equal contiguous slice of that
 // list, computed on the device from context_lens, so ragged lengths cost no
 // imbalance and no tail. A tile that
 // lies inside one slice is finished (normalised and stored) by that wave; a
