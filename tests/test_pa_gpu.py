@@ -143,12 +143,15 @@ def test_row_tiles_share_a_worker(heads, q_len, workers, device):
                                                           (128, 16, 3, torch.bfloat16, 0),
                                                           (16, 64, 1, torch.bfloat16, 7),
                                                           (128, 40, 2, torch.float16, 0),
-                                                          (32, 32, 1, torch.float16, 333)])
+                                                          (32, 32, 1, torch.float16, 333),
+                                                          (128, 6, 4, torch.bfloat16, 0),
+                                                          (64, 6, 4, torch.float16, 5)])
 def test_sibling_waves_stage_k_through_lds(bs, heads, q_len, dtype, workers, device):
     # 128-dim heads with several row tiles per kv head: every sibling wave of a
     # workgroup stages K in its own BS x 256 bytes of the launch's dynamic LDS
     # (four waves x 32 KB at BS = 128). 64 rows -> 4 tiles, 48 -> 3, 80 -> 5
-    # (a second row group with one live wave), 32 -> 2.
+    # (a second row group with one live wave); 32 rows -> 2 tiles and 24 -> 2
+    # (the second one partial) run in one wave (the two-tile kernel).
     print(f"[case] sibling K through LDS bs={bs} rows={heads * q_len} {dtype} workers={workers}", flush=True)
     case = make_custom_case(batch=3, num_heads=heads, kv_heads=1, head_dim=128, block_size=bs, q_len=q_len,
                             causal=q_len > 1, context_lens=[q_len, 3 * bs + 5, 2000], seed=330 + heads + bs,
