@@ -186,6 +186,45 @@ int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stre
 int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *args, const void *key_new, const void *value_new,
                                  void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * The decode prelude fused into the decode as well: the query and the new
+ * tokens' K/V are computed inside the decode's launches from the fp32
+ * projections, as simpler_hip_qk_norm_rope_append (include/simpler_hip/
+ * kv_cache.h) computes them -- q/k = RoPE(RMSnorm(proj * inv_rms) * weight),
+ * half-split RoPE, v = proj * inv_rms, all rounded to bf16 -- and the new K/V
+ * are written into the caches and attended over as in
+ * simpler_hip_pa_decode_append. Replaces the reference's prelude + append +
+ * attention of one decode layer (simpler_setup/goldens/qwen3_14b_decode.py
+ * :207-226, 261-269, then the paged attention; in the reference the prelude
+ * and the cache write are phase 0 of the fused attention task,
+ * paged_attention_cce/kernel/fai_body.hpp:199-230). Results and cache contents
+ * equal, bit for bit, simpler_hip_qk_norm_rope_append per token (position
+ * context_lens[b] - q_len + i, slot from the block table) followed by
+ * simpler_hip_pa_decode on its query.
+ *
+ * args: as for simpler_hip_pa_decode_append, with bf16 caches (kv_format
+ * BF16), head_dim_k = head_dim_v = 128, a GQA cache (not MLA), q_len <= 16;
+ * args->query is not read (it may be NULL).
+ * A sequence whose length is below q_len or above max_position is reported by
+ * simpler_hip_pa_decode_check as BAD_LENGTH; its tokens outside the RoPE table
+ * get a zero query row and neither replace nor write cache rows.
+ */
+typedef struct SimplerHipDecodePreludeArgs {
+    const float *q_proj;        /* [batch, q_len, num_heads, 128] fp32 */
+    const float *k_proj;        /* [batch, q_len, num_kv_heads, 128] fp32 */
+    const float *v_proj;        /* [batch, q_len, num_kv_heads, 128] fp32 */
+    const float *inv_rms;       /* [batch, q_len] fp32: rsqrt(mean(h^2) + eps) of the hidden state */
+    const float *q_norm_weight; /* [128] fp32 */
+    const float *k_norm_weight; /* [128] fp32 */
+    const float *rope_cos;      /* [max_position, 128] fp32 */
+    const float *rope_sin;      /* [max_position, 128] fp32 */
+    int32_t max_position;
+    float eps;
+} SimplerHipDecodePreludeArgs;
+
+int simpler_hip_pa_decode_prelude(const SimplerHipPaDecodeArgs *args, const SimplerHipDecodePreludeArgs *prelude,
+                                  void *workspace, size_t workspace_bytes, void *stream);
+
 /* Measurement helpers: name of the main kernel the args select, and the
  * number of worker wavefronts a launch uses. */
 const char *simpler_hip_pa_decode_kernel_name(const SimplerHipPaDecodeArgs *args);

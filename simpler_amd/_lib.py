@@ -94,6 +94,17 @@ class QkNormRopeAppendArgs(ctypes.Structure):
     ]
 
 
+class DecodePreludeArgs(ctypes.Structure):
+    """Mirror of ``SimplerHipDecodePreludeArgs`` (include/simpler_hip/pa_decode.h)."""
+
+    _fields_ = [
+        *[(n, ctypes.c_void_p) for n in ("q_proj", "k_proj", "v_proj", "inv_rms", "q_norm_weight", "k_norm_weight",
+                                          "rope_cos", "rope_sin")],
+        ("max_position", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
 # Every symbol the public headers declare, with its ctypes signature.
 _VP, _SZ, _I32, _U32, _U64, _I = (
     ctypes.c_void_p,
@@ -113,6 +124,7 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_pa_decode_check": (_I, [_VP, _SZ, _VP]),
     "simpler_hip_pa_decode_noalloc": (_I, [_ARGS_P, _VP]),
     "simpler_hip_pa_decode_append": (_I, [_ARGS_P, _VP, _VP, _VP, _SZ, _VP]),
+    "simpler_hip_pa_decode_prelude": (_I, [_ARGS_P, ctypes.POINTER(DecodePreludeArgs), _VP, _SZ, _VP]),
     "simpler_hip_pa_decode_kernel_name": (ctypes.c_char_p, [_ARGS_P]),
     "simpler_hip_pa_decode_plan": (_I, [_ARGS_P, ctypes.POINTER(_I32)]),
     # include/simpler_hip/kv_cache.h

@@ -323,13 +323,15 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
 
 namespace simpler_hip {
 namespace {
-// k_new / v_new: the fused append's new tokens (k_new null: plain decode).
+// k_new / v_new: the fused append's new tokens; pre: the fused prelude, whose
+// projections give the query and the new tokens (both null: plain decode).
 int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes, void *stream,
-                     int phases, unsigned *err_mirror, const void *k_new = nullptr, const void *v_new = nullptr) {
+                     int phases, unsigned *err_mirror, const void *k_new = nullptr, const void *v_new = nullptr,
+                     const SimplerHipDecodePreludeArgs *pre = nullptr) {
     if (phases & ~(SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE)) return SIMPLER_HIP_ERR_INVALID;
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
-    const bool append = k_new != nullptr;
+    const bool append = k_new != nullptr || pre != nullptr;
     const Kernels s = pick_kernel(a, append);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
     Plan plan = make_plan(a, s.k);
@@ -378,6 +380,18 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     P.err_mirror = (phases & SIMPLER_HIP_PHASE_MERGE) ? err_mirror : nullptr;
     P.k_new = (const uint16_t *)k_new;
     P.v_new = (const uint16_t *)v_new;
+    if (pre) {
+        P.pre_q = pre->q_proj;
+        P.pre_k = pre->k_proj;
+        P.pre_v = pre->v_proj;
+        P.pre_inv_rms = pre->inv_rms;
+        P.pre_qw = pre->q_norm_weight;
+        P.pre_kw = pre->k_norm_weight;
+        P.pre_cos = pre->rope_cos;
+        P.pre_sin = pre->rope_sin;
+        P.pre_max_pos = pre->max_position;
+        P.pre_eps = pre->eps;
+    }
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
@@ -418,6 +432,27 @@ extern "C" int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *a, con
     return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream,
                                          SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr, key_new,
                                          value_new);
+}
+
+extern "C" int simpler_hip_pa_decode_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre,
+                                             void *workspace, size_t workspace_bytes, void *stream) {
+    if (!a || !pre) return SIMPLER_HIP_ERR_INVALID;
+    // the query comes from q_proj: validate the rest with q_proj standing in for it
+    SimplerHipPaDecodeArgs args = *a;
+    args.query = pre->q_proj;
+    const int rc = validate(&args);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    if (args.kv_format != SIMPLER_HIP_KV_BF16 || args.head_dim_k != 128 || args.head_dim_v != 128 ||
+        args.q_len > kMaxAppendTokens || (is_mla_shape(&args) && v_is_k_prefix(&args)))
+        return SIMPLER_HIP_ERR_UNSUPPORTED;
+    const void *ptrs[8] = {pre->q_proj,        pre->k_proj,        pre->v_proj,   pre->inv_rms,
+                           pre->q_norm_weight, pre->k_norm_weight, pre->rope_cos, pre->rope_sin};
+    for (const void *p : ptrs)
+        if (!p || ((uintptr_t)p & 15)) return SIMPLER_HIP_ERR_INVALID;
+    if (pre->max_position < 1 || !(pre->eps >= 0.f)) return SIMPLER_HIP_ERR_INVALID;
+    return simpler_hip::pa_decode_launch(&args, workspace, workspace_bytes, stream,
+                                         SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr, nullptr, nullptr,
+                                         pre);
 }
 
 // ---------------------------------------------------------------------------

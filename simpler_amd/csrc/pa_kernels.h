@@ -125,9 +125,20 @@ struct KernelParams {
     // null for MLA (V is a prefix of K). Null when not appending.
     const uint16_t *k_new;
     const uint16_t *v_new;
+    // fused decode prelude (bf16, 128-dim heads, with the fused append): the
+    // query and the new tokens' K/V come from fp32 projections
+    // [batch, q_len, heads, 128] as q/k = RoPE(RMSnorm(proj * inv_rms) * w),
+    // v = proj * inv_rms; pre_q null otherwise
+    const float *pre_q, *pre_k, *pre_v;
+    const float *pre_inv_rms;       // [batch, q_len]
+    const float *pre_qw, *pre_kw;   // [128] norm weights
+    const float *pre_cos, *pre_sin; // [max_position, 128]
+    int32_t pre_max_pos;
+    float pre_eps;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
+
 
 // V rows are read as whole 128-byte lines exactly once: non-temporal loads
 // keep them from displacing useful lines (measured ~11% more read bandwidth on
@@ -160,6 +171,78 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
     // fp32 -> bf16 round-to-nearest-even (gfx950: v_cvt_pk_bf16_f32)
     const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
     return __builtin_bit_cast(unsigned, h);
+}
+
+// One 128-dim q or k head row of the fused prelude, in the QK operand layout:
+// lane (pc, qd) gets dims 32kk + 8qd .. +7 (kk = 0..3) of its row, the four
+// lanes qd of a row holding it all (every lane of the wave calls this; `src`
+// is read only where `valid`). x = src * inv_rms, r = 1 / sqrt(mean(x^2) +
+// eps), y = x * r * w, half-split RoPE at the row's position (dim d pairs
+// with d + 64: k-steps kk and kk + 2 of the same lane), rounded to bf16; zero
+// where the position is outside the table. The arithmetic is the standalone
+// prelude kernel's (qk_norm_rope_append_kernel in kv_cache.hip): no fused
+// multiply-adds, correctly rounded division and square root, and the sum of
+// squares added in its order (leaf i = x_i^2 + x_{i+64}^2, then an xor tree
+// over i with steps 32, 16, 8, 4, 2, 1), so both produce the same bits.
+__device__ __forceinline__ void prelude_qk_row(const float *src, const float ir, const float *w, const float *cosr,
+                                               const float *sinr, const float eps, const bool pos_ok,
+                                               const bool valid, u32x4_t (&out)[4]) {
+#pragma clang fp contract(off)
+    const int qd = (threadIdx.x & 63) >> 4;
+    float x[4][8];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        f32x4_t a = (f32x4_t){0.f, 0.f, 0.f, 0.f}, c = a;
+        if (valid) {
+            a = *reinterpret_cast<const f32x4_t *>(src + 32 * kk + 8 * qd);
+            c = *reinterpret_cast<const f32x4_t *>(src + 32 * kk + 8 * qd + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[kk][j] = a[j] * ir;
+            x[kk][4 + j] = c[j] * ir;
+        }
+    }
+    // leaves i = 32kk + 8qd + j (kk = 0, 1), then the tree's steps 32 (kk), 16
+    // (qd bit 1: lane ^ 32), 8 (qd bit 0: lane ^ 16), 4, 2, 1 (j)
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float l0 = x[0][j] * x[0][j] + x[2][j] * x[2][j];
+        const float l1 = x[1][j] * x[1][j] + x[3][j] * x[3][j];
+        t[j] = l0 + l1;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = t[j] + __shfl_xor(t[j], 32, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = t[j] + __shfl_xor(t[j], 16, 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = t[j] + t[j + 4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) t[j] = t[j] + t[j + 2];
+    const float ss = t[0] + t[1];
+    const float r = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, 128.f) + eps));
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        unsigned lo_w[4], hi_w[4];
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2) {
+            float ol[2], oh[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * j2 + h;
+                const int i = 32 * kk + 8 * qd + j;  // dim of the low half; its pair is i + 64
+                const float zl = (x[kk][j] * r) * w[i];
+                const float zh = (x[kk + 2][j] * r) * w[i + 64];
+                ol[h] = pos_ok ? zl * cosr[i] - zh * sinr[i] : 0.f;
+                oh[h] = pos_ok ? zh * cosr[i + 64] + zl * sinr[i + 64] : 0.f;
+            }
+            lo_w[j2] = pack_bf16x2(ol[0], ol[1]);
+            hi_w[j2] = pack_bf16x2(oh[0], oh[1]);
+        }
+        out[kk] = (u32x4_t){lo_w[0], lo_w[1], lo_w[2], lo_w[3]};
+        out[kk + 2] = (u32x4_t){hi_w[0], hi_w[1], hi_w[2], hi_w[3]};
+    }
 }
 
 // The 16-bit element type of the query and the caches: its MFMA forms and
@@ -287,11 +370,13 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
     if (blockIdx.x != 0 || threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     const int64_t cap = (int64_t)P.max_blocks * P.block_size;
-    const int lo = (P.causal || P.k_new) ? P.q_len : 0;  // an appended context holds its new tokens
+    const bool appending = P.k_new || P.pre_k;
+    const int lo = (P.causal || appending) ? P.q_len : 0;  // an appended context holds its new tokens
     bool bad = false;
     for (int b = lane; b < P.batch; b += 64) {
         const int len = P.context_lens[b];
         bad |= len < lo || (int64_t)len > cap;
+        bad |= P.pre_k && len > P.pre_max_pos;  // the prelude's positions len-q_len .. len-1 need RoPE rows
     }
     if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
 }
@@ -555,7 +640,44 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
     const int new0 = ctx - P.q_len;
     int pk = -1, pe[4] = {-1, -1, -1, -1};
     u32x4_t knew[APPEND ? KS : 1], vnew[APPEND ? 4 : 1][DVS];
-    if constexpr (APPEND) {
+    bool prelude = false;
+    if constexpr (APPEND && DK == 128 && DV == 128) {
+        // fused prelude: the new rows from the fp32 projections (every lane
+        // takes part in the K row's norm); positions outside the RoPE table
+        // are neither substituted nor written
+        if (P.pre_k) {
+            prelude = true;
+            const int64_t row0 = (int64_t)b * P.q_len - new0;  // projection row of position p: row0 + p
+            pk = new_token_at(new0, ctx, pc);
+            const bool kvalid = pk >= 0, kpos_ok = kvalid && pk < P.pre_max_pos;
+            const int64_t kc = (int64_t)(kpos_ok ? pk : 0) * 128;
+            u32x4_t k4[4];
+            prelude_qk_row(P.pre_k + ((row0 + (kvalid ? pk : new0)) * P.kv_heads + kvh) * 128,
+                           kvalid ? P.pre_inv_rms[row0 + pk] : 0.f, P.pre_kw, P.pre_cos + kc, P.pre_sin + kc,
+                           P.pre_eps, kpos_ok, kvalid, k4);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) knew[kk] = k4[kk < 4 ? kk : 0];
+            if (!kpos_ok) pk = -1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                pe[e] = new_token_at(new0, ctx, 4 * qd + e);
+                if (pe[e] >= P.pre_max_pos) pe[e] = -1;
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds) {
+                    vnew[e][ds] = (u32x4_t){0u, 0u, 0u, 0u};
+                    if (pe[e] >= 0) {
+                        const float ir = P.pre_inv_rms[row0 + pe[e]];
+                        const float *vs = P.pre_v + ((row0 + pe[e]) * P.kv_heads + kvh) * 128 + 128 * ds + 8 * pc;
+                        const f32x4_t a = *reinterpret_cast<const f32x4_t *>(vs);
+                        const f32x4_t c = *reinterpret_cast<const f32x4_t *>(vs + 4);
+                        vnew[e][ds] = (u32x4_t){pack_bf16x2(a[0] * ir, a[1] * ir), pack_bf16x2(a[2] * ir, a[3] * ir),
+                                                pack_bf16x2(c[0] * ir, c[1] * ir), pack_bf16x2(c[2] * ir, c[3] * ir)};
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (APPEND) if (!prelude) {
         const int64_t row0 = (int64_t)b * P.q_len - new0;  // k_new row of position p: row0 + p
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) knew[kk] = (u32x4_t){0u, 0u, 0u, 0u};
@@ -844,6 +966,25 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         rowlen[r] = 0;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) qv[r][kk] = (u32x4_t){0u, 0u, 0u, 0u};
+        if constexpr (APPEND && KLDS) {
+            if (P.pre_q) {  // fused prelude: the row from q_proj (every lane takes part)
+                const bool valid = pc < min(16, P.rows - (rt + r) * 16);
+                const int row = (rt + r) * 16 + pc;
+                const int i = valid ? row / P.group : 0, hh = valid ? row - i * P.group : 0;
+                const int pos = ctx - P.q_len + i;
+                const bool pos_ok = pos >= 0 && pos < P.pre_max_pos;
+                const int64_t tok = (int64_t)b * P.q_len + i;
+                const float ir = valid ? P.pre_inv_rms[tok] : 0.f;
+                const int64_t cs = (int64_t)(pos_ok ? pos : 0) * 128;
+                u32x4_t q4[4];
+                prelude_qk_row(P.pre_q + (tok * P.num_heads + kvh * P.group + hh) * 128, ir, P.pre_qw,
+                               P.pre_cos + cs, P.pre_sin + cs, P.pre_eps, pos_ok, valid, q4);
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) qv[r][kk] = q4[kk < 4 ? kk : 0];
+                if (valid) rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+                continue;
+            }
+        }
         if (pc < min(16, P.rows - (rt + r) * 16)) {
             const int row = (rt + r) * 16 + pc;
             const int i = row / P.group, hh = row - i * P.group;

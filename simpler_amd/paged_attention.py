@@ -320,6 +320,90 @@ def paged_attention_decode_append(
     return out
 
 
+def paged_attention_decode_prelude(
+    q_proj: torch.Tensor,
+    k_proj: torch.Tensor,
+    v_proj: torch.Tensor,
+    inv_rms: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    out: torch.Tensor | None = None,
+    scale: float | None = None,
+    *,
+    eps: float = 1e-6,
+    causal: bool = False,
+    out_dtype: torch.dtype = torch.float32,
+    num_workers: int = 0,
+) -> torch.Tensor:
+    """Decode prelude, KV append and decode in the decode's launches
+    (``simpler_hip_pa_decode_prelude``).
+
+    From the fp32 projections ``q_proj`` ``[B, (q_len,) Hq, 128]`` and ``k_proj``
+    / ``v_proj`` ``[B, (q_len,) Hkv, 128]``: q and k are RoPE(RMSnorm(proj *
+    inv_rms) * weight) at the new tokens' positions ``context_lens[b] - q_len + i``
+    (``rope_cos``/``rope_sin`` ``[max_position, 128]``, half-split), v = v_proj *
+    inv_rms (``inv_rms`` ``[B]`` or ``[B, q_len]``), all rounded to bf16, as
+    ``kv_cache.qk_norm_rope_append`` computes them; the new K/V go into the bf16
+    caches and the decode attends over them (see ``paged_attention_decode_append``).
+    """
+    q4 = q_proj.dim() == 4
+    q_len = q_proj.shape[1] if q4 else 1
+    batch, hq, d = q_proj.shape[0], q_proj.shape[-2], q_proj.shape[-1]
+    hkv = key_cache.shape[2]
+    kv_shape = (batch, q_len, hkv, d) if q4 else (batch, hkv, d)
+    for name, t, shape in (("q_proj", q_proj, tuple(q_proj.shape)), ("k_proj", k_proj, kv_shape),
+                           ("v_proj", v_proj, kv_shape)):
+        _check(t, name, torch.float32, (3, 4))
+        if tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 {shape} tensor, got {tuple(t.shape)}")
+    if inv_rms.numel() != batch * q_len or inv_rms.dtype != torch.float32 or not inv_rms.is_contiguous():
+        raise ValueError("inv_rms must be a contiguous float32 [batch] or [batch, q_len] tensor")
+    for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _check(t, name, torch.float32, (1,))
+        if tuple(t.shape) != (d,) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 [{d}] tensor")
+    for name, t in (("rope_cos", rope_cos), ("rope_sin", rope_sin)):
+        _check(t, name, torch.float32, (2,))
+        if t.shape[1] != d or not t.is_contiguous() or t.shape != rope_cos.shape:
+            raise ValueError(f"{name} must be a contiguous float32 [max_position, {d}] tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        shape = (batch, q_len, hq, value_cache.shape[-1]) if q4 else (batch, hq, value_cache.shape[-1])
+        out = torch.empty(shape, dtype=out_dtype, device=q_proj.device)
+    # the decode args take their query shape from q_proj (the query itself is
+    # computed in the kernel; this bf16 view over q_proj's storage is not read)
+    query_shape = torch.empty(0, dtype=torch.bfloat16, device=q_proj.device).set_(
+        q_proj.untyped_storage(), q_proj.storage_offset() * 2, tuple(q_proj.shape),
+        tuple(torch.empty(q_proj.shape, device="meta").stride()))
+    args = make_args(query_shape, key_cache, value_cache, block_table, context_lens, out, scale, causal=causal,
+                     num_workers=num_workers)
+    pre = _lib.DecodePreludeArgs()
+    pre.q_proj, pre.k_proj, pre.v_proj = q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr()
+    pre.inv_rms = inv_rms.data_ptr()
+    pre.q_norm_weight, pre.k_norm_weight = q_norm_weight.data_ptr(), k_norm_weight.data_ptr()
+    pre.rope_cos, pre.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
+    pre.max_position = rope_cos.shape[0]
+    pre.eps = float(eps)
+    lib = _lib.lib()
+    device = q_proj.device
+    stream = torch.cuda.current_stream(device).cuda_stream
+    need = lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(args))
+    if need == 0:
+        raise PagedAttentionError(-1)
+    ws = _WORKSPACE.get(device, need, stream)
+    rc = lib.simpler_hip_pa_decode_prelude(ctypes.byref(args), ctypes.byref(pre), ws.data_ptr(), ws.numel(), stream)
+    if rc != 0:
+        raise PagedAttentionError(rc, "simpler_hip_pa_decode_prelude")
+    return out
+
+
 def check_errors(device: torch.device | None = None) -> None:
     """Synchronise and raise if a launch on the current stream met an out-of-pool
     block_table entry (rc -6) or a context length it had to clamp (rc -7)."""

@@ -257,6 +257,36 @@ def test_fused_append_validates_on_the_host():
     assert call(_mla_args(), k, None, ws_bytes=16) == -4
 
 
+def test_fused_prelude_validates_on_the_host():
+    lib = _lib.lib()
+
+    def pre(**kw):
+        p = _lib.DecodePreludeArgs()
+        for i, n in enumerate(("q_proj", "k_proj", "v_proj", "inv_rms", "q_norm_weight", "k_norm_weight", "rope_cos",
+                               "rope_sin")):
+            setattr(p, n, 0x10000 + 0x1000 * i)
+        p.max_position, p.eps = 8192, 1e-6
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+    def call(a, p, ws_bytes=1 << 30):
+        return lib.simpler_hip_pa_decode_prelude(ctypes.byref(a), ctypes.byref(p) if p is not None else None,
+                                                 ctypes.c_void_p(0x100000), ws_bytes, None)
+
+    assert call(_args(), None) == -1
+    assert call(_args(), pre(k_proj=0)) == -1  # every projection is required
+    assert call(_args(), pre(rope_sin=0x20008)) == -1  # 16-byte aligned
+    assert call(_args(), pre(max_position=0)) == -1
+    assert call(_args(), pre(eps=-1.0)) == -1
+    assert call(_args(query=0), pre(), ws_bytes=16) == -4  # the query is not read: only the workspace rule fails
+    assert call(_args(head_dim_k=64, head_dim_v=64, k_head_stride=64, v_head_stride=64), pre()) == -2  # 128 only
+    assert call(_args(kv_format=1, k_scale=0x9000, v_scale=0xA000), pre()) == -2  # bf16 caches only
+    assert call(_args(kv_format=2), pre()) == -2
+    assert call(_args(q_len=17, num_heads=8, causal=1), pre()) == -2  # at most 16 new tokens
+    assert call(_mla_args(), pre()) == -2
+
+
 def test_worker_plan():
     # without a device the launcher assumes an MI355X (256 CUs). 128-dim bf16 heads
     # read K in whole rows through LDS: one worker per SIMD

@@ -1,0 +1,127 @@
+"""The decode prelude fused into the decode (``simpler_hip_pa_decode_prelude``) on the GPU.
+
+Checked bit for bit against the chain it replaces, on the same inputs: the
+standalone prelude ``simpler_hip_qk_norm_rope_append`` (one call over every new
+token, at position ``len - q_len + i`` and the slot its block-table entry gives)
+followed by ``simpler_hip_pa_decode`` on the query it wrote. That prelude is
+itself pinned against the oracle (tests/test_kv_cache_gpu.py), the decode
+likewise (tests/test_pa_gpu.py). The output and both caches must be equal.
+Shapes: one row tile (q_len 1, the Qwen3-8B head layout), causal q_len 4 with
+16-token blocks and a forced worker count, two row tiles in one wave (q_len 8),
+four tiles as sibling waves (q_len 16), and lengths past the RoPE table
+(reported as BAD_LENGTH, those tokens' query rows zero and their cache rows
+untouched, as the standalone prelude leaves them).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as ko
+from simpler_amd import kv_cache as kvc
+from simpler_amd import paged_attention as pa
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _inputs(batch, hq, hkv, bs, lens, q_len, seed, rope_len=None):
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s, std=1.0, bias=0.0: torch.empty(s).normal_(0.0, std, generator=g) + bias  # noqa: E731
+    max_blocks = max(1, math.ceil(max(lens) / bs)) + 1
+    pool = batch * max_blocks
+    table = torch.randperm(pool, generator=g).to(torch.int32).reshape(batch, max_blocks)
+    cos, sin = ko.rope_tables(rope_len or max_blocks * bs, D)
+    return dict(
+        q_proj=rn(batch, q_len, hq, D, std=0.5), k_proj=rn(batch, q_len, hkv, D, std=0.5),
+        v_proj=rn(batch, q_len, hkv, D, std=0.5), inv_rms=rn(batch, q_len, std=0.2, bias=1.0).abs(),
+        q_norm_weight=rn(D, std=0.1, bias=1.0), k_norm_weight=rn(D, std=0.1, bias=1.0),
+        rope_cos=torch.from_numpy(cos), rope_sin=torch.from_numpy(sin), block_table=table,
+        context_lens=torch.tensor(lens, dtype=torch.int32),
+        key_cache=rn(pool, bs, hkv, D, std=0.5).to(torch.bfloat16),
+        value_cache=rn(pool, bs, hkv, D, std=0.5).to(torch.bfloat16))
+
+
+def _chain(x, hq, q_len, bs, scale, workers):
+    """Standalone prelude over every new token, then the plain decode."""
+    batch = x["q_proj"].shape[0]
+    hkv = x["k_proj"].shape[2]
+    lens = x["context_lens"].cpu().long()
+    pos = lens[:, None] - q_len + torch.arange(q_len)[None, :]  # [batch, q_len]
+    table = x["block_table"].cpu().long()
+    slot = table.gather(1, (pos // bs).clamp(min=0)) * bs + pos % bs
+    slot = torch.where(pos >= 0, slot, torch.full_like(slot, -1))
+    dev = x["q_proj"].device
+    tok = batch * q_len
+    q_out = kvc.qk_norm_rope_append(
+        x["q_proj"].reshape(tok, hq * D), x["k_proj"].reshape(tok, hkv * D), x["v_proj"].reshape(tok, hkv * D),
+        x["inv_rms"].reshape(tok), x["q_norm_weight"], x["k_norm_weight"], x["rope_cos"], x["rope_sin"],
+        (pos + 1).reshape(tok).to(torch.int32).to(dev), slot.reshape(tok).to(torch.int32).to(dev), x["key_cache"],
+        x["value_cache"], num_heads=hq, error_count=torch.zeros(1, dtype=torch.int32, device=dev))
+    query = q_out.reshape(batch, q_len, hq, D) if q_len > 1 else q_out
+    return pa.paged_attention_decode(query, x["key_cache"], x["value_cache"], x["block_table"], x["context_lens"],
+                                     scale=scale, causal=q_len > 1, num_workers=workers)
+
+
+def _fused(x, q_len, scale, workers):
+    q_proj = x["q_proj"] if q_len > 1 else x["q_proj"][:, 0]
+    k_proj = x["k_proj"] if q_len > 1 else x["k_proj"][:, 0]
+    v_proj = x["v_proj"] if q_len > 1 else x["v_proj"][:, 0]
+    return pa.paged_attention_decode_prelude(
+        q_proj.contiguous(), k_proj.contiguous(), v_proj.contiguous(), x["inv_rms"], x["q_norm_weight"],
+        x["k_norm_weight"], x["rope_cos"], x["rope_sin"], x["key_cache"], x["value_cache"], x["block_table"],
+        x["context_lens"], scale=scale, eps=kvc.EPS, causal=q_len > 1, num_workers=workers)
+
+
+CASES = {
+    # name: (batch, hq, hkv, block_size, lens, q_len, workers)
+    "q1_qwen3_heads": (4, 32, 8, 128, [1, 129, 700, 2000], 1, 0),
+    "q4_bs16_w7": (3, 16, 4, 16, [4, 40, 300], 4, 7),
+    "q8_two_tiles": (3, 32, 8, 128, [8, 130, 2000], 8, 0),
+    "q8_two_tiles_w333": (2, 32, 8, 128, [700, 1500], 8, 333),
+    "q16_siblings": (2, 32, 8, 64, [16, 500], 16, 0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_fused_prelude_equals_prelude_then_decode(name, device):
+    batch, hq, hkv, bs, lens, q_len, workers = CASES[name]
+    print(f"[case] fused prelude {name}", flush=True)
+    x = _inputs(batch, hq, hkv, bs, lens, q_len, seed=960 + len(name))
+    a = {n: t.to(device) for n, t in x.items()}
+    b = {n: (t.clone() if n in ("key_cache", "value_cache") else t) for n, t in a.items()}
+    scale = 1.0 / math.sqrt(D)
+    want = _chain(a, hq, q_len, bs, scale, workers)
+    got = _fused(b, q_len, scale, workers)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert torch.equal(got, want), f"{name}: output differs from prelude then decode"
+    assert torch.equal(b["key_cache"], a["key_cache"]), f"{name}: key cache differs"
+    assert torch.equal(b["value_cache"], a["value_cache"]), f"{name}: value cache differs"
+    assert torch.isfinite(got).all()
+
+
+def test_fused_prelude_positions_past_the_rope_table(device):
+    # sequence 1's new tokens sit at positions 36..39 of a 32-row RoPE table
+    print("[case] fused prelude past the RoPE table", flush=True)
+    q_len = 4
+    x = _inputs(2, 16, 4, 16, [5, 40], q_len, seed=990, rope_len=32)
+    a = {n: t.to(device) for n, t in x.items()}
+    b = {n: (t.clone() if n in ("key_cache", "value_cache") else t) for n, t in a.items()}
+    scale = 1.0 / math.sqrt(D)
+    want = _chain(a, 16, q_len, 16, scale, 0)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)  # the plain decode sees valid lengths
+    got = _fused(b, q_len, scale, 0)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    assert torch.equal(got, want)
+    assert torch.equal(b["key_cache"], a["key_cache"]) and torch.equal(b["value_cache"], a["value_cache"])
+    np.testing.assert_array_equal(got[1].float().cpu().numpy(), want[1].float().cpu().numpy())
