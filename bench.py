@@ -41,7 +41,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--config", default=DEFAULT_CONFIG)
     p.add_argument("--tg-mode", default="graph", choices=["eager", "graph"],
                    help="--op taskgraph: launch tasks as submitted, or as one hipGraph per step")
-    p.add_argument("--op", default="decode", choices=["decode", "decode_append", "kv_append", "prelude", "taskgraph"],
+    p.add_argument("--op", default="decode",
+                   choices=["decode", "decode_append", "decode_prelude", "kv_append", "prelude", "taskgraph"],
                    help="decode (the headline path); kv_append / prelude: the cache-write step before it")
     p.add_argument("--tokens", type=int, default=32768,
                    help="--op kv_append: tokens written per call (32 = one decode step of bs=32)")
@@ -272,6 +273,93 @@ def bench_kv(args) -> int:
     return 0
 
 
+def bench_decode_prelude(args) -> int:
+    """The decode prelude (q/k RMS norm + RoPE, v scaling) and the KV append
+    fused into the decode (simpler_hip_pa_decode_prelude) on a bf16 GQA config
+    with 128-dim heads, beside the same work as two steps:
+    simpler_hip_qk_norm_rope_append over the new tokens, then
+    simpler_hip_pa_decode on its query (and the decode alone)."""
+    import torch
+
+    from simpler_amd import kv_cache as kvc
+    from simpler_amd import paged_attention as pa
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, make_case, rope_tables
+
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    if cfg.mla or cfg.kv_format != "bf16" or cfg.head_dim_k != 128 or cfg.head_dim_v != 128:
+        print("bench.py: --op decode_prelude times bf16 GQA configs with 128-dim heads", file=sys.stderr)
+        return 2
+    case_cpu = make_case(cfg)
+    case = case_cpu.to(dev)
+    g = torch.Generator().manual_seed(20261212)
+    b, ql, hq, hkv, d = cfg.batch, cfg.q_len, cfg.num_heads, cfg.kv_heads, cfg.head_dim_k
+    rn = lambda *shape, std=0.5: (torch.randn(*shape, generator=g) * std).to(dev)  # noqa: E731
+    q_proj, k_proj, v_proj = rn(b, ql, hq, d), rn(b, ql, hkv, d), rn(b, ql, hkv, d)
+    inv_rms = (1.0 + torch.rand(b, ql, generator=g) * 0.2).to(dev)
+    q_w, k_w = (1.0 + rn(d, std=0.1)), (1.0 + rn(d, std=0.1))
+    cos, sin = (t.to(dev) for t in rope_tables(int(case_cpu.context_lens.max()) + 1, d))
+    qp = lambda t: t if ql > 1 else t[:, 0].contiguous()  # noqa: E731
+    out = torch.empty(case.out_shape(), dtype=torch.bfloat16, device=dev)
+    fargs, pre = pa.prelude_args(qp(q_proj), qp(k_proj), qp(v_proj), inv_rms, q_w, k_w, cos, sin, case.key_cache,
+                                 case.value_cache, case.block_table, case.context_lens, out, case.scale,
+                                 eps=kvc.EPS, causal=cfg.causal, num_workers=args.workers)
+    # the two-step form: the standalone prelude over every new token, then the decode on its query
+    pos = case.context_lens.long()[:, None] - ql + torch.arange(ql, device=dev)[None, :]
+    phys = case.block_table.long().gather(1, pos.clamp(min=0) // cfg.block_size)
+    slots = torch.where(pos >= 0, phys * cfg.block_size + pos % cfg.block_size, -1).to(torch.int32).reshape(-1)
+    q_out = torch.empty(b * ql, hq, d, dtype=torch.bfloat16, device=dev)
+    sargs = kvc.prelude_args(q_proj.reshape(b * ql, hq * d), k_proj.reshape(b * ql, hkv * d),
+                             v_proj.reshape(b * ql, hkv * d), inv_rms.reshape(-1), q_w, k_w, cos, sin,
+                             (pos + 1).reshape(-1).to(torch.int32), slots, case.key_cache, case.value_cache, hq, q_out)
+    query = q_out.reshape(b, ql, hq, d) if ql > 1 else q_out
+    dargs = pa.make_args(query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
+                         case.scale, causal=cfg.causal, num_workers=args.workers)
+    stream = torch.cuda.current_stream(dev)
+    sid = stream.cuda_stream
+    variants = {
+        "fused": lambda: pa.launch(fargs, dev, sid, prelude=pre),
+        "separate": lambda: (kvc.launch_prelude(sargs, stream=sid), pa.launch(dargs, dev, sid)),
+        "decode_only": lambda: pa.launch(dargs, dev, sid),
+    }
+    runs = {name: [] for name in variants}
+    for rnd in range(5):
+        for name, call in variants.items():
+            for _ in range(args.warmup):
+                call()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                call()
+            e1.record(stream)
+            torch.cuda.synchronize(dev)
+            runs[name].append(e0.elapsed_time(e1) / args.steps * 1e3)
+            print(f"[bench] round {rnd} {name}: {runs[name][-1]:.2f} us/step", file=sys.stderr, flush=True)
+    us = {name: sorted(r)[len(r) // 2] for name, r in runs.items()}
+    pa.check_errors(dev)
+    # decode bytes plus the projections read (fp32 q, k, v) and the new K/V rows written
+    proj = b * ql * (hq + 2 * hkv) * d * 4
+    nbytes = algorithmic_bytes(case_cpu, out_bytes=2) + proj + b * ql * hkv * 2 * d * 2
+    gbs = nbytes / (us["fused"] * 1e-6) / 1e9
+    line = {
+        "metric": f"decode with fused prelude and KV append GB/s [{cfg.name}]", "value": round(gbs, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us["fused"] / 1e3, 5), "us_per_step": round(us["fused"], 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.description}; q/k RMS norm + RoPE and the append of {ql} new "
+                               "token(s) per sequence fused into the decode", "parallelism": "single GPU"},
+        "us_per_step_separate": round(us["separate"], 2), "us_per_step_decode_only": round(us["decode_only"], 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "pa_decode_kernel (prelude + append) + pa_merge_kernel",
+                     "kernel_us": round(us["fused"], 2), "algorithmic_bytes": nbytes},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def bench_decode_append(args) -> int:
     """The KV append fused into the decode (simpler_hip_pa_decode_append) on a
     decode config, beside the same work as two steps: simpler_hip_kv_append at
@@ -440,6 +528,8 @@ def main() -> int:
         return bench_taskgraph(args)
     if args.op == "decode_append":
         return bench_decode_append(args)
+    if args.op == "decode_prelude":
+        return bench_decode_prelude(args)
     if args.op != "decode":
         return bench_kv(args)
 

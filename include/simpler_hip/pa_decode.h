@@ -204,7 +204,10 @@ int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *args, const void 
  *
  * args: as for simpler_hip_pa_decode_append, with bf16 caches (kv_format
  * BF16), head_dim_k = head_dim_v = 128, a GQA cache (not MLA), q_len <= 16;
- * args->query is not read (it may be NULL).
+ * args->query is not read (it may be NULL). Workspace: what
+ * simpler_hip_pa_decode_workspace_size gives for these args suffices (two row
+ * tiles per kv head run as sibling waves here, which needs no more partial
+ * slots than the plain decode's two-tile wave).
  * A sequence whose length is below q_len or above max_position is reported by
  * simpler_hip_pa_decode_check as BAD_LENGTH; its tokens outside the RoPE table
  * get a zero query row and neither replace nor write cache rows.

@@ -97,14 +97,15 @@ bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
 
 // The main kernel(s) and the merge kernel a decode with these args runs;
 // main is null when the combination is not supported. With `append`, ka holds
-// the fused-append variants of k (same launch shapes; the plan is made from k).
+// the fused-append variants of k (same launch shapes; the plan is made from k);
+// with `prelude` too, the variants that also run the fused decode prelude.
 struct Kernels {
     KernelPair k;
     KernelPair ka;
     MergeFn merge;
 };
 
-Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
+Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false, bool prelude = false) {
     Kernels s{};
     const int bs = a->block_size, dk = a->head_dim_k, dv = a->head_dim_v, out = a->out_dtype;
     const bool f16 = a->kv_format == SIMPLER_HIP_KV_FP16;
@@ -117,7 +118,8 @@ Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
         }
     } else if (dk == dv) {
         s.k = f16 ? pick_gqa_f16(bs, dk, out) : pick_gqa_bf16(bs, dk, out);
-        if (append) s.ka = f16 ? pick_gqa_f16_append(bs, dk, out) : pick_gqa_bf16_append(bs, dk, out);
+        if (prelude) s.ka = f16 ? KernelPair{} : pick_gqa_bf16_prelude(bs, dk, out);
+        else if (append) s.ka = f16 ? pick_gqa_f16_append(bs, dk, out) : pick_gqa_bf16_append(bs, dk, out);
     }
     s.merge = pick_merge(dv, out);
     if (!s.merge.fn || (append && !s.ka.main)) s.k.main = nullptr;
@@ -174,7 +176,10 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu, size_t lds = 0) {
     return slots;
 }
 
-Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: the main kernels of pick_kernel
+// k: the main kernels of pick_kernel. allow_pair = false keeps two row tiles
+// as sibling waves (the fused prelude: its two-tile wave needs more registers
+// than the wave has).
+Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, const bool allow_pair = true) {
     Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
@@ -199,7 +204,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
         // Row tiles of one kv head run as sibling waves of one worker workgroup
         // (up to four), so K/V of a block is fetched once for all of them;
         // two row tiles with K through LDS run in one wave instead.
-        const bool pair = k.main_pair && p.row_tiles == 2;
+        const bool pair = allow_pair && k.main_pair && p.row_tiles == 2;
         p.tiles_per_worker = pair ? 2 : (p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker);
         p.threads = pair ? 64 : 64 * p.tiles_per_worker;
         p.main = pair ? k.main_pair : p.tiles_per_worker > 1 ? k.main_multi : k.main;
@@ -332,9 +337,9 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
     const bool append = k_new != nullptr || pre != nullptr;
-    const Kernels s = pick_kernel(a, append);
+    const Kernels s = pick_kernel(a, append, pre != nullptr);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    Plan plan = make_plan(a, s.k);
+    Plan plan = make_plan(a, s.k, pre == nullptr);
     if (append)
         plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : plan.main == s.k.main_pair ? s.ka.main_pair : s.ka.main;
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;

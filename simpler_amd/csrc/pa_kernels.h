@@ -226,19 +226,27 @@ __device__ __forceinline__ void prelude_qk_row(const float *src, const float ir,
     for (int kk = 0; kk < 2; ++kk) {
         unsigned lo_w[4], hi_w[4];
 #pragma unroll
-        for (int j2 = 0; j2 < 4; ++j2) {
-            float ol[2], oh[2];
+        for (int q4 = 0; q4 < 2; ++q4) {  // dims i = 32kk + 8qd + 4q4 .. +3 (16-byte loads of the tables)
+            const int i0 = 32 * kk + 8 * qd + 4 * q4;
+            const f32x4_t wl = *reinterpret_cast<const f32x4_t *>(w + i0);
+            const f32x4_t wh = *reinterpret_cast<const f32x4_t *>(w + i0 + 64);
+            const f32x4_t cl = *reinterpret_cast<const f32x4_t *>(cosr + i0);
+            const f32x4_t ch = *reinterpret_cast<const f32x4_t *>(cosr + i0 + 64);
+            const f32x4_t sl = *reinterpret_cast<const f32x4_t *>(sinr + i0);
+            const f32x4_t sh = *reinterpret_cast<const f32x4_t *>(sinr + i0 + 64);
+            float ol[4], oh[4];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = 2 * j2 + h;
-                const int i = 32 * kk + 8 * qd + j;  // dim of the low half; its pair is i + 64
-                const float zl = (x[kk][j] * r) * w[i];
-                const float zh = (x[kk + 2][j] * r) * w[i + 64];
-                ol[h] = pos_ok ? zl * cosr[i] - zh * sinr[i] : 0.f;
-                oh[h] = pos_ok ? zh * cosr[i + 64] + zl * sinr[i + 64] : 0.f;
+            for (int e = 0; e < 4; ++e) {
+                const int j = 4 * q4 + e;
+                const float zl = (x[kk][j] * r) * wl[e];
+                const float zh = (x[kk + 2][j] * r) * wh[e];
+                ol[e] = pos_ok ? zl * cl[e] - zh * sl[e] : 0.f;
+                oh[e] = pos_ok ? zh * ch[e] + zl * sh[e] : 0.f;
             }
-            lo_w[j2] = pack_bf16x2(ol[0], ol[1]);
-            hi_w[j2] = pack_bf16x2(oh[0], oh[1]);
+            lo_w[2 * q4] = pack_bf16x2(ol[0], ol[1]);
+            lo_w[2 * q4 + 1] = pack_bf16x2(ol[2], ol[3]);
+            hi_w[2 * q4] = pack_bf16x2(oh[0], oh[1]);
+            hi_w[2 * q4 + 1] = pack_bf16x2(oh[2], oh[3]);
         }
         out[kk] = (u32x4_t){lo_w[0], lo_w[1], lo_w[2], lo_w[3]};
         out[kk + 2] = (u32x4_t){hi_w[0], hi_w[1], hi_w[2], hi_w[3]};
@@ -600,8 +608,9 @@ __device__ __forceinline__ int tile_of(const int p, const int blk) {
 // ---------------------------------------------------------------------------
 
 // RTW row tiles rt, rt+1, .. of one wave (each K and V operand feeds every
-// tile's MFMAs); min_rowlen is the first tile's (the shortest).
-template <int BS, int DK, int DV, typename ET, bool APPEND, int RTW = 1>
+// tile's MFMAs); min_rowlen is the first tile's (the shortest). PRE: the
+// fused prelude (with APPEND), whose new rows come from the fp32 projections.
+template <int BS, int DK, int DV, typename ET, bool APPEND, int RTW = 1, bool PRE = false>
 __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const int b, const int kvh, const int rt,
                                                    const int ctx, const int blk_begin, const int lo, const int hi,
                                                    const u32x4_t (&qv)[RTW][(DK + 31) / 32], const int (&rowlen)[RTW],
@@ -640,13 +649,13 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
     const int new0 = ctx - P.q_len;
     int pk = -1, pe[4] = {-1, -1, -1, -1};
     u32x4_t knew[APPEND ? KS : 1], vnew[APPEND ? 4 : 1][DVS];
-    bool prelude = false;
-    if constexpr (APPEND && DK == 128 && DV == 128) {
-        // fused prelude: the new rows from the fp32 projections (every lane
-        // takes part in the K row's norm); positions outside the RoPE table
-        // are neither substituted nor written
-        if (P.pre_k) {
-            prelude = true;
+    static_assert(!PRE || (APPEND && DK == 128 && DV == 128), "fused prelude: with the append, 128-dim heads");
+    // fused prelude: the new rows from the fp32 projections (every lane takes
+    // part in the K row's norm); positions outside the RoPE table are neither
+    // substituted nor written. (Computing them once the first K loads are
+    // out measured no faster and needs more registers.)
+    if constexpr (PRE) {
+        {
             const int64_t row0 = (int64_t)b * P.q_len - new0;  // projection row of position p: row0 + p
             pk = new_token_at(new0, ctx, pc);
             const bool kvalid = pk >= 0, kpos_ok = kvalid && pk < P.pre_max_pos;
@@ -677,7 +686,7 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
             }
         }
     }
-    if constexpr (APPEND) if (!prelude) {
+    if constexpr (APPEND && !PRE) {
         const int64_t row0 = (int64_t)b * P.q_len - new0;  // k_new row of position p: row0 + p
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) knew[kk] = (u32x4_t){0u, 0u, 0u, 0u};
@@ -939,7 +948,7 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
 // ET: the element type of the query and bf16/fp16 caches (fp8 caches widen
 // to bf16, so KV8 takes ET = bf16).
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16,
-          bool APPEND = false, int RTW = 1>
+          bool APPEND = false, int RTW = 1, bool PRE = false>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int ctx, const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
@@ -953,6 +962,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
     static_assert(!(KV8 && APPEND), "fused append: 16-bit caches");
     static_assert(RTW == 1 || KLDS, "two row tiles per wave: K through LDS");
+    static_assert(!PRE || (APPEND && KLDS && RTW == 1), "fused prelude: with the append, K through LDS, one tile");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -966,8 +976,26 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         rowlen[r] = 0;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) qv[r][kk] = (u32x4_t){0u, 0u, 0u, 0u};
-        if constexpr (APPEND && KLDS) {
-            if (P.pre_q) {  // fused prelude: the row from q_proj (every lane takes part)
+        if constexpr (PRE) continue;  // fused prelude: computed by prep_q once the first loads are out
+        if (pc < min(16, P.rows - (rt + r) * 16)) {
+            const int row = (rt + r) * 16 + pc;
+            const int i = row / P.group, hh = row - i * P.group;
+            const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
+                if (DK % 32 == 0 || dim < DK) qv[r][kk] = ld16(qrow + dim);
+            }
+            rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
+        }
+    }
+    // Fused prelude: the query rows from q_proj (every lane takes part in a
+    // row's norm). Called after the segment's first K/V loads are issued, so
+    // its loads' latency overlaps theirs.
+    auto prep_q = [&] {
+        if constexpr (PRE) {
+#pragma unroll
+            for (int r = 0; r < RTW; ++r) {
                 const bool valid = pc < min(16, P.rows - (rt + r) * 16);
                 const int row = (rt + r) * 16 + pc;
                 const int i = valid ? row / P.group : 0, hh = valid ? row - i * P.group : 0;
@@ -981,22 +1009,10 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                                P.pre_cos + cs, P.pre_sin + cs, P.pre_eps, pos_ok, valid, q4);
 #pragma unroll
                 for (int kk = 0; kk < KS; ++kk) qv[r][kk] = q4[kk < 4 ? kk : 0];
-                if (valid) rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
-                continue;
+                rowlen[r] = valid ? (P.causal ? ctx - (P.q_len - 1 - i) : ctx) : 0;
             }
         }
-        if (pc < min(16, P.rows - (rt + r) * 16)) {
-            const int row = (rt + r) * 16 + pc;
-            const int i = row / P.group, hh = row - i * P.group;
-            const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK;
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-                const int dim = KV8 ? 16 * qd + 64 * (kk >> 1) + 8 * (kk & 1) : 32 * kk + 8 * qd;
-                if (DK % 32 == 0 || dim < DK) qv[r][kk] = ld16(qrow + dim);
-            }
-            rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
-        }
-    }
+    };
     // shortest visible length over the valid rows of the wave's tiles
     // (wave-uniform; the first tile's first row): blocks that end at or before
     // it need no masking.
@@ -1317,8 +1333,9 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     constexpr bool kRefillV = KV8;
     bool bad = false;
     int phys = checked(bt_row[blk_begin], bad);
-    auto step = [&](const int blk, auto has_next) {
+    auto step = [&](const int blk, auto has_next, auto v_issued) {
         constexpr bool NEXT = decltype(has_next)::value;
+        constexpr bool V_ISSUED = decltype(v_issued)::value;  // V(blk) already issued by the caller
         const bool blk_bad = bad;
         const int phys_b = phys;
         const int raw_next = NEXT ? bt_row[blk + 1] : 0;  // in flight during this block's loads
@@ -1326,7 +1343,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
         // block's loads together lets the caches serve the second request.
         if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
-        if constexpr (!kRefillV) load_v(vreg, vraw, phys_b, blk);
+        if constexpr (!kRefillV && !V_ISSUED) load_v(vreg, vraw, phys_b, blk);
         auto stage_k_and_prefetch = [&] {
             if constexpr (KLDS) {
                 // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
@@ -1359,8 +1376,22 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     auto pipeline = [&](const int end) {
         load_k(kreg, phys, blk_begin);
         if constexpr (kRefillV) load_v(vreg, vraw, phys, blk_begin);
-        for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{});
-        step(end - 1, std::false_type{});
+        if constexpr (PRE) {
+            // the first block's V goes out with its K, then the prelude's
+            // query (its loads complete behind them), then the first step
+            load_v(vreg, vraw, phys, blk_begin);
+            prep_q();
+            if (end - blk_begin > 1) {
+                step(blk_begin, std::true_type{}, std::true_type{});
+                for (int blk = blk_begin + 1; blk + 1 < end; ++blk) step(blk, std::true_type{}, std::false_type{});
+                step(end - 1, std::false_type{}, std::false_type{});
+            } else {
+                step(blk_begin, std::false_type{}, std::true_type{});
+            }
+        } else {
+            for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{}, std::false_type{});
+            step(end - 1, std::false_type{}, std::false_type{});
+        }
     };
     if constexpr (APPEND) {
         // Fused append: the blocks from the first one holding a new token on
@@ -1370,8 +1401,9 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // compiler's wait counts in the loop.)
         const int pipe_end = max(blk_begin, min(blk_end, ctx - P.q_len < 0 ? 0 : (ctx - P.q_len) / BS));
         if (pipe_end > blk_begin) pipeline(pipe_end);
+        else if constexpr (PRE) prep_q();  // no pipelined block: the query is needed by the tail alone
         if (pipe_end < blk_end)
-            unpipelined_blocks<BS, DK, DV, ET, true, RTW>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
+            unpipelined_blocks<BS, DK, DV, ET, true, RTW, PRE>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
                                                           min_rowlen, acc, lacc, m_run, f_run);
     } else {
         pipeline(blk_end);
@@ -1395,7 +1427,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 // RTW = 2 (with MAXW = 1): one wave runs both row tiles of a row group,
 // every K and V operand feeding the two tiles' MFMAs.
 template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16,
-          bool APPEND = false, int RTW = 1>
+          bool APPEND = false, int RTW = 1, bool PRE = false>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
@@ -1446,7 +1478,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
             if constexpr (BS * DK > 16384 || BS * DV > 16384)  // a block's K or V exceeds the registers
                 run_segment_big<BS, DK, DV, OutT, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
             else
-                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND, RTW>(
+                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND, RTW, PRE>(
                     P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml, MAXW > 1 && full_group, klds);
         }
         pos += seg;
@@ -2203,6 +2235,9 @@ KernelPair pick_gqa_f16(int bs, int d, int out_dtype);
 // The same with the fused KV append (KernelParams::k_new / v_new).
 KernelPair pick_gqa_bf16_append(int bs, int d, int out_dtype);
 KernelPair pick_gqa_f16_append(int bs, int d, int out_dtype);
+// The fused append with the fused decode prelude (KernelParams::pre_*): bf16
+// caches, Dk == Dv == 128.
+KernelPair pick_gqa_bf16_prelude(int bs, int d, int out_dtype);
 // GQA decode with fp8 E4M3FN caches (bf16 query), Dk == Dv == 128.
 KernelPair pick_gqa_fp8(int bs, int d, int out_dtype);
 // MLA (Dk 576, Dv 512, V a prefix of K), bf16, without or with the fused KV append.

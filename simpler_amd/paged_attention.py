@@ -191,13 +191,15 @@ PHASE_MAIN, PHASE_MERGE = 1, 2
 
 def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = None,
            phases: int = PHASE_MAIN | PHASE_MERGE, key_new: torch.Tensor | None = None,
-           value_new: torch.Tensor | None = None) -> None:
+           value_new: torch.Tensor | None = None, prelude: _lib.DecodePreludeArgs | None = None) -> None:
     """Enqueue one decode on ``stream`` (default: torch's current stream).
 
     ``phases`` selects the main kernel, the merge kernel or both (the default);
     a merge must follow a main launch with the same args. With ``key_new``
     (checked by ``append_tensors``) the decode runs with the fused KV append
-    (``simpler_hip_pa_decode_append``, both phases).
+    (``simpler_hip_pa_decode_append``, both phases); with ``prelude`` (from
+    ``prelude_args``) with the fused prelude and append
+    (``simpler_hip_pa_decode_prelude``, both phases).
     """
     lib = _lib.lib()
     if stream is None:
@@ -206,6 +208,14 @@ def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = N
     if need == 0:
         raise PagedAttentionError(-1)
     ws = _WORKSPACE.get(device, need, stream)
+    if prelude is not None:
+        if phases != PHASE_MAIN | PHASE_MERGE:
+            raise ValueError("the fused prelude runs both phases")
+        rc = lib.simpler_hip_pa_decode_prelude(ctypes.byref(args), ctypes.byref(prelude), ws.data_ptr(), ws.numel(),
+                                               stream)
+        if rc != 0:
+            raise PagedAttentionError(rc, "simpler_hip_pa_decode_prelude")
+        return
     if key_new is not None:
         if phases != PHASE_MAIN | PHASE_MERGE:
             raise ValueError("the fused append runs both phases")
@@ -353,6 +363,29 @@ def paged_attention_decode_prelude(
     caches and the decode attends over them (see ``paged_attention_decode_append``).
     """
     q4 = q_proj.dim() == 4
+    batch, hq, d = q_proj.shape[0], q_proj.shape[-2], q_proj.shape[-1]
+    q_len = q_proj.shape[1] if q4 else 1
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        shape = (batch, q_len, hq, value_cache.shape[-1]) if q4 else (batch, hq, value_cache.shape[-1])
+        out = torch.empty(shape, dtype=out_dtype, device=q_proj.device)
+    args, pre = prelude_args(q_proj, k_proj, v_proj, inv_rms, q_norm_weight, k_norm_weight, rope_cos, rope_sin,
+                             key_cache, value_cache, block_table, context_lens, out, scale, eps=eps, causal=causal,
+                             num_workers=num_workers)
+    launch(args, q_proj.device, prelude=pre)
+    return out
+
+
+def prelude_args(q_proj: torch.Tensor, k_proj: torch.Tensor, v_proj: torch.Tensor, inv_rms: torch.Tensor,
+                 q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, rope_cos: torch.Tensor,
+                 rope_sin: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                 block_table: torch.Tensor, context_lens: torch.Tensor, out: torch.Tensor, scale: float, *,
+                 eps: float = 1e-6, causal: bool = False,
+                 num_workers: int = 0) -> tuple[_lib.PaDecodeArgs, _lib.DecodePreludeArgs]:
+    """The C decode args and prelude args of ``paged_attention_decode_prelude``,
+    for repeated ``launch(args, device, prelude=pre)``; checks the tensors."""
+    q4 = q_proj.dim() == 4
     q_len = q_proj.shape[1] if q4 else 1
     batch, hq, d = q_proj.shape[0], q_proj.shape[-2], q_proj.shape[-1]
     hkv = key_cache.shape[2]
@@ -372,11 +405,6 @@ def paged_attention_decode_prelude(
         _check(t, name, torch.float32, (2,))
         if t.shape[1] != d or not t.is_contiguous() or t.shape != rope_cos.shape:
             raise ValueError(f"{name} must be a contiguous float32 [max_position, {d}] tensor")
-    if scale is None:
-        scale = 1.0 / math.sqrt(d)
-    if out is None:
-        shape = (batch, q_len, hq, value_cache.shape[-1]) if q4 else (batch, hq, value_cache.shape[-1])
-        out = torch.empty(shape, dtype=out_dtype, device=q_proj.device)
     # the decode args take their query shape from q_proj (the query itself is
     # computed in the kernel; this bf16 view over q_proj's storage is not read)
     query_shape = torch.empty(0, dtype=torch.bfloat16, device=q_proj.device).set_(
@@ -391,17 +419,7 @@ def paged_attention_decode_prelude(
     pre.rope_cos, pre.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
     pre.max_position = rope_cos.shape[0]
     pre.eps = float(eps)
-    lib = _lib.lib()
-    device = q_proj.device
-    stream = torch.cuda.current_stream(device).cuda_stream
-    need = lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(args))
-    if need == 0:
-        raise PagedAttentionError(-1)
-    ws = _WORKSPACE.get(device, need, stream)
-    rc = lib.simpler_hip_pa_decode_prelude(ctypes.byref(args), ctypes.byref(pre), ws.data_ptr(), ws.numel(), stream)
-    if rc != 0:
-        raise PagedAttentionError(rc, "simpler_hip_pa_decode_prelude")
-    return out
+    return args, pre
 
 
 def check_errors(device: torch.device | None = None) -> None:
