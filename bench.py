@@ -274,10 +274,11 @@ def bench_kv(args) -> int:
 
 
 def bench_decode_prelude(args) -> int:
-    """The decode prelude (q/k RMS norm + RoPE, v scaling) and the KV append
-    fused into the decode (simpler_hip_pa_decode_prelude) on a bf16 GQA config
-    with 128-dim heads, beside the same work as two steps:
-    simpler_hip_qk_norm_rope_append over the new tokens, then
+    """The decode prelude (q/k RMS norm + RoPE, v scaling), the KV append and
+    the decode in one call (simpler_hip_pa_decode_prelude: the prelude's launch
+    at the slots the block table gives, then the decode's two) on a bf16 GQA
+    config with 128-dim heads, beside the same work as two calls:
+    simpler_hip_qk_norm_rope_append with a caller-built slot mapping, then
     simpler_hip_pa_decode on its query (and the decode alone)."""
     import torch
 
@@ -318,7 +319,7 @@ def bench_decode_prelude(args) -> int:
     stream = torch.cuda.current_stream(dev)
     sid = stream.cuda_stream
     variants = {
-        "fused": lambda: pa.launch(fargs, dev, sid, prelude=pre),
+        "one_call": lambda: pa.launch(fargs, dev, sid, prelude=pre),
         "separate": lambda: (kvc.launch_prelude(sargs, stream=sid), pa.launch(dargs, dev, sid)),
         "decode_only": lambda: pa.launch(dargs, dev, sid),
     }
@@ -341,19 +342,19 @@ def bench_decode_prelude(args) -> int:
     # decode bytes plus the projections read (fp32 q, k, v) and the new K/V rows written
     proj = b * ql * (hq + 2 * hkv) * d * 4
     nbytes = algorithmic_bytes(case_cpu, out_bytes=2) + proj + b * ql * hkv * 2 * d * 2
-    gbs = nbytes / (us["fused"] * 1e-6) / 1e9
+    gbs = nbytes / (us["one_call"] * 1e-6) / 1e9
     line = {
-        "metric": f"decode with fused prelude and KV append GB/s [{cfg.name}]", "value": round(gbs, 2),
+        "metric": f"decode with prelude and KV append in one call GB/s [{cfg.name}]", "value": round(gbs, 2),
         "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(us["fused"] / 1e3, 5), "us_per_step": round(us["fused"], 2), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "ms_per_step": round(us["one_call"] / 1e3, 5), "us_per_step": round(us["one_call"], 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.description}; q/k RMS norm + RoPE and the append of {ql} new "
-                               "token(s) per sequence fused into the decode", "parallelism": "single GPU"},
+                               "token(s) per sequence, then the decode", "parallelism": "single GPU"},
         "us_per_step_separate": round(us["separate"], 2), "us_per_step_decode_only": round(us["decode_only"], 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "pa_decode_kernel (prelude + append) + pa_merge_kernel",
-                     "kernel_us": round(us["fused"], 2), "algorithmic_bytes": nbytes},
+                     "kernel": "qk_norm_rope_append_kernel + pa_decode_kernel + pa_merge_kernel",
+                     "kernel_us": round(us["one_call"], 2), "algorithmic_bytes": nbytes},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
@@ -361,9 +362,11 @@ def bench_decode_prelude(args) -> int:
 
 
 def bench_decode_append(args) -> int:
-    """The KV append fused into the decode (simpler_hip_pa_decode_append) on a
-    decode config, beside the same work as two steps: simpler_hip_kv_append at
-    the derived slots, then simpler_hip_pa_decode (and the decode alone)."""
+    """The KV append and the decode in one call (simpler_hip_pa_decode_append:
+    fused into the decode's launches where a worker runs one row tile, else the
+    append's launch first) on a decode config, beside the same work as two
+    calls: simpler_hip_kv_append at caller-built slots, then
+    simpler_hip_pa_decode (and the decode alone)."""
     import torch
 
     from simpler_amd import kv_cache as kvc
@@ -393,7 +396,7 @@ def bench_decode_append(args) -> int:
     stream = torch.cuda.current_stream(dev)
     sid = stream.cuda_stream
     variants = {
-        "fused": lambda: pa.launch(pargs, dev, sid, key_new=k_new, value_new=v_new),
+        "one_call": lambda: pa.launch(pargs, dev, sid, key_new=k_new, value_new=v_new),
         "separate": lambda: (kvc.launch_append(aargs, stream=sid), pa.launch(pargs, dev, sid)),
         "decode_only": lambda: pa.launch(pargs, dev, sid),
     }
@@ -417,18 +420,19 @@ def bench_decode_append(args) -> int:
     # decode bytes plus the appended rows (read from key_new/value_new, written to the caches)
     new_rows = cfg.batch * cfg.q_len * cfg.kv_heads * (cfg.head_dim_k + cfg.head_dim_v) * 2
     nbytes = algorithmic_bytes(case_cpu, out_bytes=2) + 2 * new_rows
-    gbs = nbytes / (us["fused"] * 1e-6) / 1e9
+    gbs = nbytes / (us["one_call"] * 1e-6) / 1e9
     line = {
-        "metric": f"decode with fused KV append GB/s [{cfg.name}]", "value": round(gbs, 2), "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us["fused"] / 1e3, 5),
-        "us_per_step": round(us["fused"], 2), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "metric": f"decode with KV append in one call GB/s [{cfg.name}]", "value": round(gbs, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us["one_call"] / 1e3, 5),
+        "us_per_step": round(us["one_call"], 2), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.description}; {cfg.q_len} new token(s) per sequence appended",
                    "parallelism": "single GPU"},
         "us_per_step_separate": round(us["separate"], 2), "us_per_step_decode_only": round(us["decode_only"], 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "pa_decode_kernel (append) + pa_merge_kernel", "kernel_us": round(us["fused"], 2),
+                     "kernel": "pa_decode_kernel (append) + pa_merge_kernel (one row tile per worker; else "
+                               "kv_append_kernel first)", "kernel_us": round(us["one_call"], 2),
                      "algorithmic_bytes": nbytes},
         "cpu_baseline": None,
     }

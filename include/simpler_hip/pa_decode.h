@@ -178,6 +178,10 @@ int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stre
  * block table and seq_len (qwen3_14b_decode.py:106-115). Results and cache
  * contents are those of simpler_hip_kv_append with that slot mapping followed
  * by simpler_hip_pa_decode. q_len <= 16; bf16 and fp16 caches (not fp8).
+ * The append is fused into the decode's two launches where each worker runs
+ * one row tile; where the decode gives a worker several row tiles (GQA with
+ * more than 16 query rows per kv head), it runs as a launch of its own ahead
+ * of them, which measured faster there.
  * Same workspace as simpler_hip_pa_decode for these args. A length below
  * q_len is reported by simpler_hip_pa_decode_check as BAD_LENGTH (only the
  * new tokens at positions >= 0 are then written); new tokens in out-of-pool
@@ -187,30 +191,31 @@ int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *args, const void 
                                  void *workspace, size_t workspace_bytes, void *stream);
 
 /*
- * The decode prelude fused into the decode as well: the query and the new
- * tokens' K/V are computed inside the decode's launches from the fp32
- * projections, as simpler_hip_qk_norm_rope_append (include/simpler_hip/
- * kv_cache.h) computes them -- q/k = RoPE(RMSnorm(proj * inv_rms) * weight),
- * half-split RoPE, v = proj * inv_rms, all rounded to bf16 -- and the new K/V
- * are written into the caches and attended over as in
- * simpler_hip_pa_decode_append. Replaces the reference's prelude + append +
- * attention of one decode layer (simpler_setup/goldens/qwen3_14b_decode.py
- * :207-226, 261-269, then the paged attention; in the reference the prelude
- * and the cache write are phase 0 of the fused attention task,
- * paged_attention_cce/kernel/fai_body.hpp:199-230). Results and cache contents
- * equal, bit for bit, simpler_hip_qk_norm_rope_append per token (position
- * context_lens[b] - q_len + i, slot from the block table) followed by
- * simpler_hip_pa_decode on its query.
+ * The decode prelude, the KV append and the decode in one call: the query and
+ * the new tokens' K/V are computed from the fp32 projections as
+ * simpler_hip_qk_norm_rope_append (include/simpler_hip/kv_cache.h) computes
+ * them -- q/k = RoPE(RMSnorm(proj * inv_rms) * weight), half-split RoPE,
+ * v = proj * inv_rms, all rounded to bf16 -- the new K/V are written into the
+ * caches at each sequence's last q_len positions (the slots the block table
+ * gives, as for simpler_hip_pa_decode_append), and the decode attends over
+ * them. Replaces the reference's prelude + append + attention of one decode
+ * layer (simpler_setup/goldens/qwen3_14b_decode.py:207-226, 261-269, then the
+ * paged attention; in the reference the prelude and the cache write are
+ * phase 0 of the fused attention task, paged_attention_cce/kernel/
+ * fai_body.hpp:199-230). Three launches on `stream`: the prelude (its query
+ * rows into the workspace), then the decode's two. Results and cache
+ * contents equal, bit for bit, simpler_hip_qk_norm_rope_append per token
+ * (position context_lens[b] - q_len + i, slot from the block table) followed
+ * by simpler_hip_pa_decode on its query.
  *
  * args: as for simpler_hip_pa_decode_append, with bf16 caches (kv_format
  * BF16), head_dim_k = head_dim_v = 128, a GQA cache (not MLA), q_len <= 16;
- * args->query is not read (it may be NULL). Workspace: what
- * simpler_hip_pa_decode_workspace_size gives for these args suffices (two row
- * tiles per kv head run as sibling waves here, which needs no more partial
- * slots than the plain decode's two-tile wave).
+ * args->query is not read (it may be NULL). Workspace: at least
+ * simpler_hip_pa_decode_prelude_workspace_size(args) bytes (the decode's, then
+ * the bf16 query rows), otherwise as for simpler_hip_pa_decode.
  * A sequence whose length is below q_len or above max_position is reported by
  * simpler_hip_pa_decode_check as BAD_LENGTH; its tokens outside the RoPE table
- * get a zero query row and neither replace nor write cache rows.
+ * get a zero query row and do not write cache rows.
  */
 typedef struct SimplerHipDecodePreludeArgs {
     const float *q_proj;        /* [batch, q_len, num_heads, 128] fp32 */
@@ -227,6 +232,9 @@ typedef struct SimplerHipDecodePreludeArgs {
 
 int simpler_hip_pa_decode_prelude(const SimplerHipPaDecodeArgs *args, const SimplerHipDecodePreludeArgs *prelude,
                                   void *workspace, size_t workspace_bytes, void *stream);
+/* Bytes of workspace simpler_hip_pa_decode_prelude needs for these args (0 if
+ * unsupported or invalid). */
+size_t simpler_hip_pa_decode_prelude_workspace_size(const SimplerHipPaDecodeArgs *args);
 
 /* Measurement helpers: name of the main kernel the args select, and the
  * number of worker wavefronts a launch uses. */

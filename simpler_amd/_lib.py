@@ -125,6 +125,7 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_pa_decode_noalloc": (_I, [_ARGS_P, _VP]),
     "simpler_hip_pa_decode_append": (_I, [_ARGS_P, _VP, _VP, _VP, _SZ, _VP]),
     "simpler_hip_pa_decode_prelude": (_I, [_ARGS_P, ctypes.POINTER(DecodePreludeArgs), _VP, _SZ, _VP]),
+    "simpler_hip_pa_decode_prelude_workspace_size": (_SZ, [_ARGS_P]),
     "simpler_hip_pa_decode_kernel_name": (ctypes.c_char_p, [_ARGS_P]),
     "simpler_hip_pa_decode_plan": (_I, [_ARGS_P, ctypes.POINTER(_I32)]),
     # include/simpler_hip/kv_cache.h

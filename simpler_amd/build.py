@@ -25,7 +25,6 @@ SOURCES = [
     CSRC / "pa_kernels_gqa_f16.hip",
     CSRC / "pa_kernels_gqa_bf16_append.hip",
     CSRC / "pa_kernels_gqa_f16_append.hip",
-    CSRC / "pa_kernels_gqa_bf16_prelude.hip",
     CSRC / "pa_kernels_fp8.hip",
     CSRC / "pa_kernels_mla.hip",
     CSRC / "pa_kernels_merge.hip",

@@ -9,6 +9,12 @@
 // reference these run as phase 0 of the fused attention task
 // (kernels/vendor/paged_attention_cce/kernel/fai_body.hpp:199-230).
 //
+// Both also run in a paged form for the decode entries of pa_decode.h
+// (simpler_hip_pa_decode_append / _prelude): token t of the launch is position
+// context_lens[b] - q_len + j of sequence b = t / q_len (j = t % q_len), its
+// slot the block-table row's, as the reference derives it
+// (qwen3_14b_decode.py:106-115).
+//
 // Both kernels are HBM- or launch-bound byte movers:
 //   kv_append_kernel           one workgroup per token: 16-byte vector copies of
 //                              its K (and V) rows.
@@ -27,6 +33,7 @@
 #include <stdint.h>
 
 #include "simpler_hip/kv_cache.h"
+#include "pa_decode_internal.h"
 
 namespace simpler_hip_kv {
 namespace {
@@ -36,6 +43,15 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kMaxHeadDim = 1024;
 
+// The paged form's token -> (position, slot) inputs; block_table null: the
+// caller's slot mapping (and seq_lens) instead.
+struct Paged {
+    const int32_t *block_table, *context_lens;
+    unsigned *error_flag;  // the decode workspace's error word
+    unsigned bad_length;   // its bit for a position outside the RoPE table
+    int32_t q_len, max_blocks;
+};
+
 struct AppendParams {
     const uint16_t *key, *value;
     const int32_t *slot;
@@ -44,6 +60,7 @@ struct AppendParams {
     int64_t key_ts, key_hs, val_ts, val_hs;
     int64_t k_bs, k_ts, k_hs, v_bs, v_ts, v_hs;
     int32_t num_tokens, hkv, dk, dv, block_size, num_blocks;
+    Paged pg;
 };
 
 __device__ __forceinline__ bool slot_ok(int slot, int32_t num_blocks, int32_t block_size, int32_t *err) {
@@ -55,9 +72,25 @@ __device__ __forceinline__ bool slot_ok(int slot, int32_t num_blocks, int32_t bl
     return true;
 }
 
+// Paged form: position and slot of launch token t, or slot -1 where the
+// token is not written: a position below 0 or past the block-table row (a
+// length the decode reports), or an out-of-pool block (reported when the
+// decode reads it).
+__device__ __forceinline__ int paged_slot(const Paged &G, const int t, const int32_t block_size,
+                                          const int32_t num_blocks, int *pos) {
+    const int b = t / G.q_len;
+    const int p = G.context_lens[b] - G.q_len + (t - b * G.q_len);
+    *pos = p;
+    if (p < 0 || p >= G.max_blocks * block_size) return -1;
+    const int phys = G.block_table[(int64_t)b * G.max_blocks + p / block_size];
+    if ((unsigned)phys >= (unsigned)num_blocks) return -1;
+    return phys * block_size + p % block_size;
+}
+
 __global__ void __launch_bounds__(kThreads) kv_append_kernel(const AppendParams P) {
     const int t = blockIdx.x;
-    const int slot = P.slot[t];
+    int pos;
+    const int slot = P.pg.block_table ? paged_slot(P.pg, t, P.block_size, P.num_blocks, &pos) : P.slot[t];
     if (!slot_ok(slot, P.num_blocks, P.block_size, P.err)) return;
     const int blk = slot / P.block_size, off = slot - blk * P.block_size;
     const int kch = P.dk / 8;
@@ -83,6 +116,7 @@ struct PreludeParams {
     int64_t k_bs, k_ts, k_hs, v_bs, v_ts, v_hs;
     int32_t batch, hq, hkv, d, block_size, num_blocks, max_pos;
     float eps;
+    Paged pg;
 };
 
 // fp32 -> bf16, round to nearest even (NaN stays NaN)
@@ -104,10 +138,18 @@ __global__ void __launch_bounds__(64) qk_norm_rope_append_kernel(const PreludePa
     const int u = blockIdx.x;
     const int lane = threadIdx.x;
     const int half = P.d / 2;
-    const int pos = P.seq_lens[b] - 1;
+    int pos = 0, slot;
+    if (P.pg.block_table) {
+        slot = paged_slot(P.pg, b, P.block_size, P.num_blocks, &pos);
+    } else {
+        pos = P.seq_lens[b] - 1;
+        slot = P.slot[b];
+    }
     const bool pos_ok = pos >= 0 && pos < P.max_pos;
-    if (!pos_ok && u == 0 && threadIdx.x == 0 && P.err) atomicAdd(P.err, 1);
-    const int slot = P.slot[b];
+    if (!pos_ok && u == 0 && threadIdx.x == 0) {
+        if (P.err) atomicAdd(P.err, 1);
+        if (P.pg.error_flag && pos >= 0) atomicOr(P.pg.error_flag, P.pg.bad_length);  // past the RoPE table
+    }
     // count a bad slot once per token (on its first k unit)
     const bool write_kv = pos_ok && slot_ok(slot, P.num_blocks, P.block_size, u == P.hq ? P.err : nullptr);
     const int blk = write_kv ? slot / P.block_size : 0, off = write_kv ? slot - blk * P.block_size : 0;
@@ -172,8 +214,93 @@ __global__ void __launch_bounds__(64) qk_norm_rope_append_kernel(const PreludePa
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+Paged paged_of(const SimplerHipPaDecodeArgs *a, unsigned *error_flag, unsigned bad_length) {
+    Paged G{};
+    G.block_table = a->block_table;
+    G.context_lens = a->context_lens;
+    G.error_flag = error_flag;
+    G.bad_length = bad_length;
+    G.q_len = a->q_len;
+    G.max_blocks = a->max_blocks_per_seq;
+    return G;
+}
+
 }  // namespace
 }  // namespace simpler_hip_kv
+
+namespace simpler_hip {
+
+using namespace simpler_hip_kv;
+
+int launch_paged_append(const SimplerHipPaDecodeArgs *a, const void *key_new, const void *value_new,
+                        unsigned *error_flag, void *stream) {
+    const int tokens = a->batch * a->q_len;
+    if (tokens == 0) return SIMPLER_HIP_OK;
+    AppendParams P{};
+    P.key = (const uint16_t *)key_new;
+    P.value = (const uint16_t *)value_new;
+    P.kc = (uint16_t *)a->key_cache;
+    P.vc = (uint16_t *)a->value_cache;
+    P.key_ts = (int64_t)a->num_kv_heads * a->head_dim_k;
+    P.key_hs = a->head_dim_k;
+    P.val_ts = (int64_t)a->num_kv_heads * a->head_dim_v;
+    P.val_hs = a->head_dim_v;
+    P.k_bs = a->k_block_stride;
+    P.k_ts = a->k_token_stride;
+    P.k_hs = a->k_head_stride;
+    P.v_bs = a->v_block_stride;
+    P.v_ts = a->v_token_stride;
+    P.v_hs = a->v_head_stride;
+    P.num_tokens = tokens;
+    P.hkv = a->num_kv_heads;
+    P.dk = a->head_dim_k;
+    P.dv = a->head_dim_v;
+    P.block_size = a->block_size;
+    P.num_blocks = a->num_blocks;
+    P.pg = paged_of(a, error_flag, 0u);
+    hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)tokens), dim3(kThreads), 0, (hipStream_t)stream, P);
+    return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
+}
+
+int launch_paged_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre, void *q_out,
+                         unsigned *error_flag, unsigned bad_length, void *stream) {
+    const int tokens = a->batch * a->q_len;
+    if (tokens == 0) return SIMPLER_HIP_OK;
+    if (tokens > 65535) return SIMPLER_HIP_ERR_UNSUPPORTED;  // one grid row per token
+    PreludeParams P{};
+    P.q_proj = pre->q_proj;
+    P.k_proj = pre->k_proj;
+    P.v_proj = pre->v_proj;
+    P.inv_rms = pre->inv_rms;
+    P.q_w = pre->q_norm_weight;
+    P.k_w = pre->k_norm_weight;
+    P.cos = pre->rope_cos;
+    P.sin = pre->rope_sin;
+    P.q_out = (uint16_t *)q_out;
+    P.kc = (uint16_t *)a->key_cache;
+    P.vc = (uint16_t *)a->value_cache;
+    P.k_bs = a->k_block_stride;
+    P.k_ts = a->k_token_stride;
+    P.k_hs = a->k_head_stride;
+    P.v_bs = a->v_block_stride;
+    P.v_ts = a->v_token_stride;
+    P.v_hs = a->v_head_stride;
+    P.batch = tokens;
+    P.hq = a->num_heads;
+    P.hkv = a->num_kv_heads;
+    P.d = a->head_dim_k;
+    P.block_size = a->block_size;
+    P.num_blocks = a->num_blocks;
+    P.max_pos = pre->max_position;
+    P.eps = pre->eps;
+    P.pg = paged_of(a, error_flag, bad_length);
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)(a->num_heads + 2 * a->num_kv_heads),
+                                                        (unsigned)tokens),
+                       dim3(64), 0, (hipStream_t)stream, P);
+    return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
+}
+
+}  // namespace simpler_hip
 
 using namespace simpler_hip_kv;
 

@@ -97,15 +97,14 @@ bool v_is_k_prefix(const SimplerHipPaDecodeArgs *a) {
 
 // The main kernel(s) and the merge kernel a decode with these args runs;
 // main is null when the combination is not supported. With `append`, ka holds
-// the fused-append variants of k (same launch shapes; the plan is made from k);
-// with `prelude` too, the variants that also run the fused decode prelude.
+// the fused-append variants of k (same launch shapes; the plan is made from k).
 struct Kernels {
     KernelPair k;
     KernelPair ka;
     MergeFn merge;
 };
 
-Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false, bool prelude = false) {
+Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
     Kernels s{};
     const int bs = a->block_size, dk = a->head_dim_k, dv = a->head_dim_v, out = a->out_dtype;
     const bool f16 = a->kv_format == SIMPLER_HIP_KV_FP16;
@@ -118,8 +117,7 @@ Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false, bool p
         }
     } else if (dk == dv) {
         s.k = f16 ? pick_gqa_f16(bs, dk, out) : pick_gqa_bf16(bs, dk, out);
-        if (prelude) s.ka = f16 ? KernelPair{} : pick_gqa_bf16_prelude(bs, dk, out);
-        else if (append) s.ka = f16 ? pick_gqa_f16_append(bs, dk, out) : pick_gqa_bf16_append(bs, dk, out);
+        if (append) s.ka = f16 ? pick_gqa_f16_append(bs, dk, out) : pick_gqa_bf16_append(bs, dk, out);
     }
     s.merge = pick_merge(dv, out);
     if (!s.merge.fn || (append && !s.ka.main)) s.k.main = nullptr;
@@ -176,10 +174,7 @@ int wave_slots(KernelFn fn, int threads, int want_per_cu, size_t lds = 0) {
     return slots;
 }
 
-// k: the main kernels of pick_kernel. allow_pair = false keeps two row tiles
-// as sibling waves (the fused prelude: its two-tile wave needs more registers
-// than the wave has).
-Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, const bool allow_pair = true) {
+Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: the main kernels of pick_kernel
     Plan p{};
     const int group = a->num_heads / a->num_kv_heads;
     p.rows = group * a->q_len;
@@ -204,7 +199,7 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k, const bool 
         // Row tiles of one kv head run as sibling waves of one worker workgroup
         // (up to four), so K/V of a block is fetched once for all of them;
         // two row tiles with K through LDS run in one wave instead.
-        const bool pair = allow_pair && k.main_pair && p.row_tiles == 2;
+        const bool pair = k.main_pair && p.row_tiles == 2;
         p.tiles_per_worker = pair ? 2 : (p.row_tiles < kMaxWavesPerWorker ? p.row_tiles : kMaxWavesPerWorker);
         p.threads = pair ? 64 : 64 * p.tiles_per_worker;
         p.main = pair ? k.main_pair : p.tiles_per_worker > 1 ? k.main_multi : k.main;
@@ -328,18 +323,16 @@ extern "C" int simpler_hip_pa_decode(const SimplerHipPaDecodeArgs *a, void *work
 
 namespace simpler_hip {
 namespace {
-// k_new / v_new: the fused append's new tokens; pre: the fused prelude, whose
-// projections give the query and the new tokens (both null: plain decode).
+// k_new / v_new: the fused append's new tokens (null: plain decode).
 int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t workspace_bytes, void *stream,
-                     int phases, unsigned *err_mirror, const void *k_new = nullptr, const void *v_new = nullptr,
-                     const SimplerHipDecodePreludeArgs *pre = nullptr) {
+                     int phases, unsigned *err_mirror, const void *k_new = nullptr, const void *v_new = nullptr) {
     if (phases & ~(SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE)) return SIMPLER_HIP_ERR_INVALID;
     int rc = validate(a);
     if (rc != SIMPLER_HIP_OK) return rc;
-    const bool append = k_new != nullptr || pre != nullptr;
-    const Kernels s = pick_kernel(a, append, pre != nullptr);
+    const bool append = k_new != nullptr;
+    const Kernels s = pick_kernel(a, append);
     if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
-    Plan plan = make_plan(a, s.k, pre == nullptr);
+    Plan plan = make_plan(a, s.k);
     if (append)
         plan.main = plan.main == s.k.main_multi ? s.ka.main_multi : plan.main == s.k.main_pair ? s.ka.main_pair : s.ka.main;
     if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255)) return SIMPLER_HIP_ERR_WORKSPACE;
@@ -385,18 +378,6 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     P.err_mirror = (phases & SIMPLER_HIP_PHASE_MERGE) ? err_mirror : nullptr;
     P.k_new = (const uint16_t *)k_new;
     P.v_new = (const uint16_t *)v_new;
-    if (pre) {
-        P.pre_q = pre->q_proj;
-        P.pre_k = pre->k_proj;
-        P.pre_v = pre->v_proj;
-        P.pre_inv_rms = pre->inv_rms;
-        P.pre_qw = pre->q_norm_weight;
-        P.pre_kw = pre->k_norm_weight;
-        P.pre_cos = pre->rope_cos;
-        P.pre_sin = pre->rope_sin;
-        P.pre_max_pos = pre->max_position;
-        P.pre_eps = pre->eps;
-    }
 
     const int64_t tiles = (int64_t)a->batch * a->num_kv_heads * plan.row_tiles;
     if (phases & SIMPLER_HIP_PHASE_MAIN) {
@@ -434,30 +415,92 @@ extern "C" int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *a, con
     const bool mla = is_mla_shape(a) && v_is_k_prefix(a);
     if (!key_new || ((uintptr_t)key_new & 15)) return SIMPLER_HIP_ERR_INVALID;
     if (mla ? value_new != nullptr : (!value_new || ((uintptr_t)value_new & 15))) return SIMPLER_HIP_ERR_INVALID;
+    if (!mla) {
+        // Two or more row tiles per worker (the two-tile wave, sibling waves):
+        // the append runs as its own launch ahead of the plain decode. There
+        // the fused form's unpipelined new-token blocks measured slower (the
+        // verify shape: 155.2 against 140.2 us per step); with one tile per
+        // worker the fused form is the faster one (cfg2: 113.3 against 114.5).
+        const Kernels s = pick_kernel(a);
+        if (s.k.main) {
+            const Plan plan = make_plan(a, s.k);
+            if (plan.tiles_per_worker > 1) {
+                if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255))
+                    return SIMPLER_HIP_ERR_WORKSPACE;
+                if (a->batch == 0) return SIMPLER_HIP_OK;
+                const int rc2 = launch_paged_append(a, key_new, value_new, (unsigned *)workspace, stream);
+                if (rc2 != SIMPLER_HIP_OK) return rc2;
+                return pa_decode_launch(a, workspace, workspace_bytes, stream,
+                                        SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr);
+            }
+        }
+    }
     return simpler_hip::pa_decode_launch(a, workspace, workspace_bytes, stream,
                                          SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr, key_new,
                                          value_new);
 }
 
-extern "C" int simpler_hip_pa_decode_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre,
-                                             void *workspace, size_t workspace_bytes, void *stream) {
-    if (!a || !pre) return SIMPLER_HIP_ERR_INVALID;
-    // the query comes from q_proj: validate the rest with q_proj standing in for it
-    SimplerHipPaDecodeArgs args = *a;
-    args.query = pre->q_proj;
-    const int rc = validate(&args);
-    if (rc != SIMPLER_HIP_OK) return rc;
-    if (args.kv_format != SIMPLER_HIP_KV_BF16 || args.head_dim_k != 128 || args.head_dim_v != 128 ||
-        args.q_len > kMaxAppendTokens || (is_mla_shape(&args) && v_is_k_prefix(&args)))
+namespace {
+
+// simpler_hip_pa_decode_prelude's workspace after the decode's: the bf16
+// query rows the prelude writes.
+size_t prelude_query_bytes(const SimplerHipPaDecodeArgs *a) {
+    return align_up((size_t)a->batch * a->q_len * a->num_heads * a->head_dim_k * 2, 256);
+}
+
+// The prelude entry's checks beyond validate(); a->query is not read.
+int check_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre) {
+    if (a->kv_format != SIMPLER_HIP_KV_BF16 || a->head_dim_k != 128 || a->head_dim_v != 128 ||
+        a->q_len > kMaxAppendTokens || (is_mla_shape(a) && v_is_k_prefix(a)))
         return SIMPLER_HIP_ERR_UNSUPPORTED;
+    if (!pre) return SIMPLER_HIP_OK;
     const void *ptrs[8] = {pre->q_proj,        pre->k_proj,        pre->v_proj,   pre->inv_rms,
                            pre->q_norm_weight, pre->k_norm_weight, pre->rope_cos, pre->rope_sin};
     for (const void *p : ptrs)
         if (!p || ((uintptr_t)p & 15)) return SIMPLER_HIP_ERR_INVALID;
     if (pre->max_position < 1 || !(pre->eps >= 0.f)) return SIMPLER_HIP_ERR_INVALID;
-    return simpler_hip::pa_decode_launch(&args, workspace, workspace_bytes, stream,
-                                         SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr, nullptr, nullptr,
-                                         pre);
+    return SIMPLER_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" size_t simpler_hip_pa_decode_prelude_workspace_size(const SimplerHipPaDecodeArgs *a) {
+    if (!a) return 0;
+    SimplerHipPaDecodeArgs args = *a;
+    if (!args.query) args.query = (const void *)(uintptr_t)256;  // not read: any aligned stand-in validates
+    if (validate(&args) != SIMPLER_HIP_OK || check_prelude(&args, nullptr) != SIMPLER_HIP_OK) return 0;
+    const Kernels s = pick_kernel(&args);
+    if (!s.k.main) return 0;
+    return make_plan(&args, s.k).total + prelude_query_bytes(&args);
+}
+
+extern "C" int simpler_hip_pa_decode_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre,
+                                             void *workspace, size_t workspace_bytes, void *stream) {
+    if (!a || !pre) return SIMPLER_HIP_ERR_INVALID;
+    // the query is computed: validate the rest with q_proj standing in for it
+    SimplerHipPaDecodeArgs args = *a;
+    args.query = pre->q_proj;
+    int rc = validate(&args);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    rc = check_prelude(&args, pre);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    const Kernels s = pick_kernel(&args);
+    if (!s.k.main) return SIMPLER_HIP_ERR_UNSUPPORTED;
+    const size_t total = make_plan(&args, s.k).total;
+    if (!workspace || workspace_bytes < total + prelude_query_bytes(&args) || ((uintptr_t)workspace & 255))
+        return SIMPLER_HIP_ERR_WORKSPACE;
+    if (args.batch == 0) return SIMPLER_HIP_OK;
+    // The prelude as a launch of its own (query rows into the workspace after
+    // the decode's part, new K/V rows into the caches), then the plain
+    // decode on that query. Computing the prelude inside the decode's workers
+    // measured slower on every shape tried (cfg2 117.4 against 115.6 us per
+    // step, the verify shape 161.0 against 142.6, cfg1 17.5 against 14.3).
+    void *const q = (char *)workspace + total;
+    rc = launch_paged_prelude(&args, pre, q, (unsigned *)workspace, kErrBadLength, stream);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    args.query = q;
+    return simpler_hip::pa_decode_launch(&args, workspace, total, stream,
+                                         SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr);
 }
 
 // ---------------------------------------------------------------------------

@@ -125,20 +125,9 @@ struct KernelParams {
     // null for MLA (V is a prefix of K). Null when not appending.
     const uint16_t *k_new;
     const uint16_t *v_new;
-    // fused decode prelude (bf16, 128-dim heads, with the fused append): the
-    // query and the new tokens' K/V come from fp32 projections
-    // [batch, q_len, heads, 128] as q/k = RoPE(RMSnorm(proj * inv_rms) * w),
-    // v = proj * inv_rms; pre_q null otherwise
-    const float *pre_q, *pre_k, *pre_v;
-    const float *pre_inv_rms;       // [batch, q_len]
-    const float *pre_qw, *pre_kw;   // [128] norm weights
-    const float *pre_cos, *pre_sin; // [max_position, 128]
-    int32_t pre_max_pos;
-    float pre_eps;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4_t *>(p); }
-
 
 // V rows are read as whole 128-byte lines exactly once: non-temporal loads
 // keep them from displacing useful lines (measured ~11% more read bandwidth on
@@ -171,86 +160,6 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
     // fp32 -> bf16 round-to-nearest-even (gfx950: v_cvt_pk_bf16_f32)
     const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
     return __builtin_bit_cast(unsigned, h);
-}
-
-// One 128-dim q or k head row of the fused prelude, in the QK operand layout:
-// lane (pc, qd) gets dims 32kk + 8qd .. +7 (kk = 0..3) of its row, the four
-// lanes qd of a row holding it all (every lane of the wave calls this; `src`
-// is read only where `valid`). x = src * inv_rms, r = 1 / sqrt(mean(x^2) +
-// eps), y = x * r * w, half-split RoPE at the row's position (dim d pairs
-// with d + 64: k-steps kk and kk + 2 of the same lane), rounded to bf16; zero
-// where the position is outside the table. The arithmetic is the standalone
-// prelude kernel's (qk_norm_rope_append_kernel in kv_cache.hip): no fused
-// multiply-adds, correctly rounded division and square root, and the sum of
-// squares added in its order (leaf i = x_i^2 + x_{i+64}^2, then an xor tree
-// over i with steps 32, 16, 8, 4, 2, 1), so both produce the same bits.
-__device__ __forceinline__ void prelude_qk_row(const float *src, const float ir, const float *w, const float *cosr,
-                                               const float *sinr, const float eps, const bool pos_ok,
-                                               const bool valid, u32x4_t (&out)[4]) {
-#pragma clang fp contract(off)
-    const int qd = (threadIdx.x & 63) >> 4;
-    float x[4][8];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        f32x4_t a = (f32x4_t){0.f, 0.f, 0.f, 0.f}, c = a;
-        if (valid) {
-            a = *reinterpret_cast<const f32x4_t *>(src + 32 * kk + 8 * qd);
-            c = *reinterpret_cast<const f32x4_t *>(src + 32 * kk + 8 * qd + 4);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[kk][j] = a[j] * ir;
-            x[kk][4 + j] = c[j] * ir;
-        }
-    }
-    // leaves i = 32kk + 8qd + j (kk = 0, 1), then the tree's steps 32 (kk), 16
-    // (qd bit 1: lane ^ 32), 8 (qd bit 0: lane ^ 16), 4, 2, 1 (j)
-    float t[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float l0 = x[0][j] * x[0][j] + x[2][j] * x[2][j];
-        const float l1 = x[1][j] * x[1][j] + x[3][j] * x[3][j];
-        t[j] = l0 + l1;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = t[j] + __shfl_xor(t[j], 32, 64);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = t[j] + __shfl_xor(t[j], 16, 64);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) t[j] = t[j] + t[j + 4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) t[j] = t[j] + t[j + 2];
-    const float ss = t[0] + t[1];
-    const float r = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, 128.f) + eps));
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        unsigned lo_w[4], hi_w[4];
-#pragma unroll
-        for (int q4 = 0; q4 < 2; ++q4) {  // dims i = 32kk + 8qd + 4q4 .. +3 (16-byte loads of the tables)
-            const int i0 = 32 * kk + 8 * qd + 4 * q4;
-            const f32x4_t wl = *reinterpret_cast<const f32x4_t *>(w + i0);
-            const f32x4_t wh = *reinterpret_cast<const f32x4_t *>(w + i0 + 64);
-            const f32x4_t cl = *reinterpret_cast<const f32x4_t *>(cosr + i0);
-            const f32x4_t ch = *reinterpret_cast<const f32x4_t *>(cosr + i0 + 64);
-            const f32x4_t sl = *reinterpret_cast<const f32x4_t *>(sinr + i0);
-            const f32x4_t sh = *reinterpret_cast<const f32x4_t *>(sinr + i0 + 64);
-            float ol[4], oh[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 4 * q4 + e;
-                const float zl = (x[kk][j] * r) * wl[e];
-                const float zh = (x[kk + 2][j] * r) * wh[e];
-                ol[e] = pos_ok ? zl * cl[e] - zh * sl[e] : 0.f;
-                oh[e] = pos_ok ? zh * ch[e] + zl * sh[e] : 0.f;
-            }
-            lo_w[2 * q4] = pack_bf16x2(ol[0], ol[1]);
-            lo_w[2 * q4 + 1] = pack_bf16x2(ol[2], ol[3]);
-            hi_w[2 * q4] = pack_bf16x2(oh[0], oh[1]);
-            hi_w[2 * q4 + 1] = pack_bf16x2(oh[2], oh[3]);
-        }
-        out[kk] = (u32x4_t){lo_w[0], lo_w[1], lo_w[2], lo_w[3]};
-        out[kk + 2] = (u32x4_t){hi_w[0], hi_w[1], hi_w[2], hi_w[3]};
-    }
 }
 
 // The 16-bit element type of the query and the caches: its MFMA forms and
@@ -378,13 +287,11 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
     if (blockIdx.x != 0 || threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     const int64_t cap = (int64_t)P.max_blocks * P.block_size;
-    const bool appending = P.k_new || P.pre_k;
-    const int lo = (P.causal || appending) ? P.q_len : 0;  // an appended context holds its new tokens
+    const int lo = (P.causal || P.k_new) ? P.q_len : 0;  // an appended context holds its new tokens
     bool bad = false;
     for (int b = lane; b < P.batch; b += 64) {
         const int len = P.context_lens[b];
         bad |= len < lo || (int64_t)len > cap;
-        bad |= P.pre_k && len > P.pre_max_pos;  // the prelude's positions len-q_len .. len-1 need RoPE rows
     }
     if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
 }
@@ -608,9 +515,8 @@ __device__ __forceinline__ int tile_of(const int p, const int blk) {
 // ---------------------------------------------------------------------------
 
 // RTW row tiles rt, rt+1, .. of one wave (each K and V operand feeds every
-// tile's MFMAs); min_rowlen is the first tile's (the shortest). PRE: the
-// fused prelude (with APPEND), whose new rows come from the fp32 projections.
-template <int BS, int DK, int DV, typename ET, bool APPEND, int RTW = 1, bool PRE = false>
+// tile's MFMAs); min_rowlen is the first tile's (the shortest).
+template <int BS, int DK, int DV, typename ET, bool APPEND, int RTW = 1>
 __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const int b, const int kvh, const int rt,
                                                    const int ctx, const int blk_begin, const int lo, const int hi,
                                                    const u32x4_t (&qv)[RTW][(DK + 31) / 32], const int (&rowlen)[RTW],
@@ -649,44 +555,7 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
     const int new0 = ctx - P.q_len;
     int pk = -1, pe[4] = {-1, -1, -1, -1};
     u32x4_t knew[APPEND ? KS : 1], vnew[APPEND ? 4 : 1][DVS];
-    static_assert(!PRE || (APPEND && DK == 128 && DV == 128), "fused prelude: with the append, 128-dim heads");
-    // fused prelude: the new rows from the fp32 projections (every lane takes
-    // part in the K row's norm); positions outside the RoPE table are neither
-    // substituted nor written. (Computing them once the first K loads are
-    // out measured no faster and needs more registers.)
-    if constexpr (PRE) {
-        {
-            const int64_t row0 = (int64_t)b * P.q_len - new0;  // projection row of position p: row0 + p
-            pk = new_token_at(new0, ctx, pc);
-            const bool kvalid = pk >= 0, kpos_ok = kvalid && pk < P.pre_max_pos;
-            const int64_t kc = (int64_t)(kpos_ok ? pk : 0) * 128;
-            u32x4_t k4[4];
-            prelude_qk_row(P.pre_k + ((row0 + (kvalid ? pk : new0)) * P.kv_heads + kvh) * 128,
-                           kvalid ? P.pre_inv_rms[row0 + pk] : 0.f, P.pre_kw, P.pre_cos + kc, P.pre_sin + kc,
-                           P.pre_eps, kpos_ok, kvalid, k4);
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) knew[kk] = k4[kk < 4 ? kk : 0];
-            if (!kpos_ok) pk = -1;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                pe[e] = new_token_at(new0, ctx, 4 * qd + e);
-                if (pe[e] >= P.pre_max_pos) pe[e] = -1;
-#pragma unroll
-                for (int ds = 0; ds < DVS; ++ds) {
-                    vnew[e][ds] = (u32x4_t){0u, 0u, 0u, 0u};
-                    if (pe[e] >= 0) {
-                        const float ir = P.pre_inv_rms[row0 + pe[e]];
-                        const float *vs = P.pre_v + ((row0 + pe[e]) * P.kv_heads + kvh) * 128 + 128 * ds + 8 * pc;
-                        const f32x4_t a = *reinterpret_cast<const f32x4_t *>(vs);
-                        const f32x4_t c = *reinterpret_cast<const f32x4_t *>(vs + 4);
-                        vnew[e][ds] = (u32x4_t){pack_bf16x2(a[0] * ir, a[1] * ir), pack_bf16x2(a[2] * ir, a[3] * ir),
-                                                pack_bf16x2(c[0] * ir, c[1] * ir), pack_bf16x2(c[2] * ir, c[3] * ir)};
-                    }
-                }
-            }
-        }
-    }
-    if constexpr (APPEND && !PRE) {
+    if constexpr (APPEND) {
         const int64_t row0 = (int64_t)b * P.q_len - new0;  // k_new row of position p: row0 + p
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) knew[kk] = (u32x4_t){0u, 0u, 0u, 0u};
@@ -948,7 +817,7 @@ __device__ __forceinline__ void run_segment_big(const KernelParams &P, const int
 // ET: the element type of the query and bf16/fp16 caches (fp8 caches widen
 // to bf16, so KV8 takes ET = bf16).
 template <int BS, int DK, int DV, typename OutT, bool V_SHARED, bool KV8, bool KLDS = false, typename ET = __bf16,
-          bool APPEND = false, int RTW = 1, bool PRE = false>
+          bool APPEND = false, int RTW = 1>
 __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, const int kvh, const int rt,
                                             const int ctx, const int nblk, const int blk_begin, const int blk_end,
                                             float *const part_o, float *const part_ml,
@@ -962,7 +831,6 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     static_assert(!KV8 || std::is_same<ET, __bf16>::value, "fp8 caches widen to bf16");
     static_assert(!(KV8 && APPEND), "fused append: 16-bit caches");
     static_assert(RTW == 1 || KLDS, "two row tiles per wave: K through LDS");
-    static_assert(!PRE || (APPEND && KLDS && RTW == 1), "fused prelude: with the append, K through LDS, one tile");
     const int lane = threadIdx.x & 63;
     const int qd = lane >> 4;
     const int pc = lane & 15;
@@ -976,7 +844,6 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         rowlen[r] = 0;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) qv[r][kk] = (u32x4_t){0u, 0u, 0u, 0u};
-        if constexpr (PRE) continue;  // fused prelude: computed by prep_q once the first loads are out
         if (pc < min(16, P.rows - (rt + r) * 16)) {
             const int row = (rt + r) * 16 + pc;
             const int i = row / P.group, hh = row - i * P.group;
@@ -989,30 +856,6 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             rowlen[r] = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
         }
     }
-    // Fused prelude: the query rows from q_proj (every lane takes part in a
-    // row's norm). Called after the segment's first K/V loads are issued, so
-    // its loads' latency overlaps theirs.
-    auto prep_q = [&] {
-        if constexpr (PRE) {
-#pragma unroll
-            for (int r = 0; r < RTW; ++r) {
-                const bool valid = pc < min(16, P.rows - (rt + r) * 16);
-                const int row = (rt + r) * 16 + pc;
-                const int i = valid ? row / P.group : 0, hh = valid ? row - i * P.group : 0;
-                const int pos = ctx - P.q_len + i;
-                const bool pos_ok = pos >= 0 && pos < P.pre_max_pos;
-                const int64_t tok = (int64_t)b * P.q_len + i;
-                const float ir = valid ? P.pre_inv_rms[tok] : 0.f;
-                const int64_t cs = (int64_t)(pos_ok ? pos : 0) * 128;
-                u32x4_t q4[4];
-                prelude_qk_row(P.pre_q + (tok * P.num_heads + kvh * P.group + hh) * 128, ir, P.pre_qw,
-                               P.pre_cos + cs, P.pre_sin + cs, P.pre_eps, pos_ok, valid, q4);
-#pragma unroll
-                for (int kk = 0; kk < KS; ++kk) qv[r][kk] = q4[kk < 4 ? kk : 0];
-                rowlen[r] = valid ? (P.causal ? ctx - (P.q_len - 1 - i) : ctx) : 0;
-            }
-        }
-    };
     // shortest visible length over the valid rows of the wave's tiles
     // (wave-uniform; the first tile's first row): blocks that end at or before
     // it need no masking.
@@ -1333,9 +1176,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     constexpr bool kRefillV = KV8;
     bool bad = false;
     int phys = checked(bt_row[blk_begin], bad);
-    auto step = [&](const int blk, auto has_next, auto v_issued) {
+    auto step = [&](const int blk, auto has_next) {
         constexpr bool NEXT = decltype(has_next)::value;
-        constexpr bool V_ISSUED = decltype(v_issued)::value;  // V(blk) already issued by the caller
         const bool blk_bad = bad;
         const int phys_b = phys;
         const int raw_next = NEXT ? bt_row[blk + 1] : 0;  // in flight during this block's loads
@@ -1343,7 +1185,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // Sibling waves (row tiles of one kv head) read the same K/V: issuing a
         // block's loads together lets the caches serve the second request.
         if (V_SHARED && sync_siblings) __builtin_amdgcn_s_barrier();
-        if constexpr (!kRefillV && !V_ISSUED) load_v(vreg, vraw, phys_b, blk);
+        if constexpr (!kRefillV) load_v(vreg, vraw, phys_b, blk);
         auto stage_k_and_prefetch = [&] {
             if constexpr (KLDS) {
                 // K(i) into LDS (waits for it; V(i) stays in flight), then K(i+1) into the freed registers
@@ -1376,22 +1218,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
     auto pipeline = [&](const int end) {
         load_k(kreg, phys, blk_begin);
         if constexpr (kRefillV) load_v(vreg, vraw, phys, blk_begin);
-        if constexpr (PRE) {
-            // the first block's V goes out with its K, then the prelude's
-            // query (its loads complete behind them), then the first step
-            load_v(vreg, vraw, phys, blk_begin);
-            prep_q();
-            if (end - blk_begin > 1) {
-                step(blk_begin, std::true_type{}, std::true_type{});
-                for (int blk = blk_begin + 1; blk + 1 < end; ++blk) step(blk, std::true_type{}, std::false_type{});
-                step(end - 1, std::false_type{}, std::false_type{});
-            } else {
-                step(blk_begin, std::false_type{}, std::true_type{});
-            }
-        } else {
-            for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{}, std::false_type{});
-            step(end - 1, std::false_type{}, std::false_type{});
-        }
+        for (int blk = blk_begin; blk + 1 < end; ++blk) step(blk, std::true_type{});
+        step(end - 1, std::false_type{});
     };
     if constexpr (APPEND) {
         // Fused append: the blocks from the first one holding a new token on
@@ -1401,9 +1229,8 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
         // compiler's wait counts in the loop.)
         const int pipe_end = max(blk_begin, min(blk_end, ctx - P.q_len < 0 ? 0 : (ctx - P.q_len) / BS));
         if (pipe_end > blk_begin) pipeline(pipe_end);
-        else if constexpr (PRE) prep_q();  // no pipelined block: the query is needed by the tail alone
         if (pipe_end < blk_end)
-            unpipelined_blocks<BS, DK, DV, ET, true, RTW, PRE>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
+            unpipelined_blocks<BS, DK, DV, ET, true, RTW>(P, b, kvh, rt, ctx, blk_begin, pipe_end, blk_end, qv, rowlen,
                                                           min_rowlen, acc, lacc, m_run, f_run);
     } else {
         pipeline(blk_end);
@@ -1427,7 +1254,7 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
 // RTW = 2 (with MAXW = 1): one wave runs both row tiles of a row group,
 // every K and V operand feeding the two tiles' MFMAs.
 template <int BS, int DK, int DV, typename OutT, int MAXW, bool KV8 = false, typename ET = __bf16,
-          bool APPEND = false, int RTW = 1, bool PRE = false>
+          bool APPEND = false, int RTW = 1>
 __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams P) {
     static_assert(BS % 16 == 0 && BS >= 16 && BS <= 128, "block_size must be 16..128, multiple of 16");
     static_assert(DK % 8 == 0 && DV % 8 == 0, "head dims must be multiples of 8");
@@ -1478,7 +1305,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
             if constexpr (BS * DK > 16384 || BS * DV > 16384)  // a block's K or V exceeds the registers
                 run_segment_big<BS, DK, DV, OutT, ET, APPEND>(P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml);
             else
-                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND, RTW, PRE>(
+                run_segment<BS, DK, DV, OutT, (MAXW > 1), KV8, KLDS, ET, APPEND, RTW>(
                     P, b, kvh, rt, ctx, nb, blk, blk + seg, po, pml, MAXW > 1 && full_group, klds);
         }
         pos += seg;
@@ -2235,9 +2062,6 @@ KernelPair pick_gqa_f16(int bs, int d, int out_dtype);
 // The same with the fused KV append (KernelParams::k_new / v_new).
 KernelPair pick_gqa_bf16_append(int bs, int d, int out_dtype);
 KernelPair pick_gqa_f16_append(int bs, int d, int out_dtype);
-// The fused append with the fused decode prelude (KernelParams::pre_*): bf16
-// caches, Dk == Dv == 128.
-KernelPair pick_gqa_bf16_prelude(int bs, int d, int out_dtype);
 // GQA decode with fp8 E4M3FN caches (bf16 query), Dk == Dv == 128.
 KernelPair pick_gqa_fp8(int bs, int d, int out_dtype);
 // MLA (Dk 576, Dv 512, V a prefix of K), bf16, without or with the fused KV append.

@@ -1,10 +1,8 @@
 // Kernel tables of the GQA decode for one element type: every supported
 // (block size, head dim) pair of pa_decode_kernel, one wave per worker and up
-// to kMaxWavesPerWorker sibling waves, without or with the fused KV append
-// (and, bf16 with 128-dim heads, with the fused decode prelude).
-// Included by pa_kernels_gqa_{bf16,f16}{,_append}.hip and
-// pa_kernels_gqa_bf16_prelude.hip, so each element type and variant is
-// instantiated in its own translation unit.
+// to kMaxWavesPerWorker sibling waves, without or with the fused KV append.
+// Included by pa_kernels_gqa_{bf16,f16}{,_append}.hip, so each element type
+// and variant is instantiated in its own translation unit.
 #pragma once
 
 #include "pa_kernels.h"
@@ -15,6 +13,10 @@ namespace {
 
 template <int BS, int D, typename OutT, typename ET, bool APPEND>
 KernelPair gqa_pair() {
+    // The fused append runs with one row tile per worker only: the host sends
+    // shapes with more tiles per worker through a separate append launch.
+    if constexpr (APPEND)
+        return KernelPair{pa_decode_kernel<BS, D, D, OutT, 1, false, ET, true>, nullptr, false, D == 128};
     KernelPair k{pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND>,
                  pa_decode_kernel<BS, D, D, OutT, kMaxWavesPerWorker, false, ET, APPEND>, false, D == 128};
     if constexpr (D == 128) k.main_pair = pa_decode_kernel<BS, D, D, OutT, 1, false, ET, APPEND, 2>;
@@ -42,28 +44,6 @@ KernelPair gqa_by_block(int bs, int d) {
         case 32: return gqa_by_dim<32, OutT, ET, APPEND>(d);
         case 64: return gqa_by_dim<64, OutT, ET, APPEND>(d);
         case 128: return gqa_by_dim<128, OutT, ET, APPEND>(d);
-        default: return KernelPair{};
-    }
-}
-
-// The fused prelude's kernels: 128-dim heads only (the prelude's norm and
-// RoPE tables are 128 wide), every block size; no two-tile wave (two row
-// tiles run as sibling waves).
-template <int BS, typename OutT>
-KernelPair prelude_pair() {
-    return KernelPair{pa_decode_kernel<BS, 128, 128, OutT, 1, false, __bf16, true, 1, true>,
-                      pa_decode_kernel<BS, 128, 128, OutT, kMaxWavesPerWorker, false, __bf16, true, 1, true>, false,
-                      true};
-}
-
-template <typename OutT>
-KernelPair prelude_by_block(int bs, int d) {
-    if (d != 128) return KernelPair{};
-    switch (bs) {
-        case 16: return prelude_pair<16, OutT>();
-        case 32: return prelude_pair<32, OutT>();
-        case 64: return prelude_pair<64, OutT>();
-        case 128: return prelude_pair<128, OutT>();
         default: return KernelPair{};
     }
 }

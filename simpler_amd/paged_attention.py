@@ -198,13 +198,15 @@ def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = N
     a merge must follow a main launch with the same args. With ``key_new``
     (checked by ``append_tensors``) the decode runs with the fused KV append
     (``simpler_hip_pa_decode_append``, both phases); with ``prelude`` (from
-    ``prelude_args``) with the fused prelude and append
+    ``prelude_args``) after the prelude and append
     (``simpler_hip_pa_decode_prelude``, both phases).
     """
     lib = _lib.lib()
     if stream is None:
         stream = torch.cuda.current_stream(device).cuda_stream
-    need = lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(args))
+    size_of = (lib.simpler_hip_pa_decode_prelude_workspace_size if prelude is not None
+               else lib.simpler_hip_pa_decode_workspace_size)
+    need = size_of(ctypes.byref(args))
     if need == 0:
         raise PagedAttentionError(-1)
     ws = _WORKSPACE.get(device, need, stream)
@@ -351,8 +353,8 @@ def paged_attention_decode_prelude(
     out_dtype: torch.dtype = torch.float32,
     num_workers: int = 0,
 ) -> torch.Tensor:
-    """Decode prelude, KV append and decode in the decode's launches
-    (``simpler_hip_pa_decode_prelude``).
+    """Decode prelude, KV append and decode in one call
+    (``simpler_hip_pa_decode_prelude``: the prelude's launch, then the decode's two).
 
     From the fp32 projections ``q_proj`` ``[B, (q_len,) Hq, 128]`` and ``k_proj``
     / ``v_proj`` ``[B, (q_len,) Hkv, 128]``: q and k are RoPE(RMSnorm(proj *
@@ -406,7 +408,7 @@ def prelude_args(q_proj: torch.Tensor, k_proj: torch.Tensor, v_proj: torch.Tenso
         if t.shape[1] != d or not t.is_contiguous() or t.shape != rope_cos.shape:
             raise ValueError(f"{name} must be a contiguous float32 [max_position, {d}] tensor")
     # the decode args take their query shape from q_proj (the query itself is
-    # computed in the kernel; this bf16 view over q_proj's storage is not read)
+    # computed by the prelude; this bf16 view over q_proj's storage is not read)
     query_shape = torch.empty(0, dtype=torch.bfloat16, device=q_proj.device).set_(
         q_proj.untyped_storage(), q_proj.storage_offset() * 2, tuple(q_proj.shape),
         tuple(torch.empty(q_proj.shape, device="meta").stride()))

@@ -287,6 +287,21 @@ def test_fused_prelude_validates_on_the_host():
     assert call(_mla_args(), pre()) == -2
 
 
+def test_prelude_workspace_holds_the_query_after_the_decode_part():
+    lib = _lib.lib()
+    size = lambda f, a: getattr(lib, f)(ctypes.byref(a))  # noqa: E731
+    for kw in (dict(), dict(q_len=8, causal=1, batch=16), dict(query=0)):
+        a = _args(**kw)
+        plain = size("simpler_hip_pa_decode_workspace_size", _args(**{**kw, "query": 0x1000}))
+        q_rows = a.batch * a.q_len * a.num_heads * 128 * 2  # bf16 query rows
+        assert size("simpler_hip_pa_decode_prelude_workspace_size", a) == plain + -(-q_rows // 256) * 256
+    # what the prelude does not run on
+    for kw in (dict(head_dim_k=64, head_dim_v=64, k_head_stride=64, v_head_stride=64), dict(kv_format=2),
+               dict(q_len=17, num_heads=8, causal=1)):
+        assert size("simpler_hip_pa_decode_prelude_workspace_size", _args(**kw)) == 0
+    assert size("simpler_hip_pa_decode_prelude_workspace_size", _mla_args()) == 0
+
+
 def test_worker_plan():
     # without a device the launcher assumes an MI355X (256 CUs). 128-dim bf16 heads
     # read K in whole rows through LDS: one worker per SIMD

@@ -1,4 +1,4 @@
-"""The decode prelude fused into the decode (``simpler_hip_pa_decode_prelude``) on the GPU.
+"""The decode prelude, append and decode in one call (``simpler_hip_pa_decode_prelude``) on the GPU.
 
 Checked bit for bit against the chain it replaces, on the same inputs: the
 standalone prelude ``simpler_hip_qk_norm_rope_append`` (one call over every new
