@@ -131,13 +131,41 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // One wave per (token, head unit): units are the q heads, then the k heads,
-// then the v heads, so every row's loads are in flight at once.
+// then the v heads, so every row's loads are in flight at once. DFIX: the
+// head dim when fixed at compile time (128: one element of each half per
+// lane), 0 for any even head dim up to kMaxHeadDim. The loads that do not
+// depend on the token's position (the row, inv_rms, the norm weight) are
+// issued before it is known, so the position's load and the RoPE rows' loads
+// are the only ones in sequence.
+template <int DFIX>
 __global__ void __launch_bounds__(64) qk_norm_rope_append_kernel(const PreludeParams P) {
 #pragma clang fp contract(off)
+    constexpr int kPer = DFIX ? (DFIX + 127) / 128 : kMaxHeadDim / 2 / 64;  // elements of each half per lane
     const int b = blockIdx.y;
     const int u = blockIdx.x;
     const int lane = threadIdx.x;
-    const int half = P.d / 2;
+    const int half = DFIX ? DFIX / 2 : P.d / 2;
+    const bool is_q = u < P.hq, is_k = !is_q && u < P.hq + P.hkv;
+    const int h = is_q ? u : (is_k ? u - P.hq : u - P.hq - P.hkv);
+    const float *src = is_q ? P.q_proj + ((int64_t)b * P.hq + h) * P.d
+                            : (is_k ? P.k_proj : P.v_proj) + ((int64_t)b * P.hkv + h) * P.d;
+    const float *w = is_q ? P.q_w : P.k_w;
+    float xl[kPer], xh[kPer], wl[kPer], wh[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = lane + 64 * j;
+        xl[j] = xh[j] = wl[j] = wh[j] = 0.f;
+        if (DFIX == 128 || i < half) {
+            xl[j] = src[i];
+            xh[j] = src[i + half];
+            if (is_q || is_k) {
+                wl[j] = w[i];
+                wh[j] = w[i + half];
+            }
+        }
+    }
+    const float ir = P.inv_rms[b];
+
     int pos = 0, slot;
     if (P.pg.block_table) {
         slot = paged_slot(P.pg, b, P.block_size, P.num_blocks, &pos);
@@ -153,63 +181,62 @@ __global__ void __launch_bounds__(64) qk_norm_rope_append_kernel(const PreludePa
     // count a bad slot once per token (on its first k unit)
     const bool write_kv = pos_ok && slot_ok(slot, P.num_blocks, P.block_size, u == P.hq ? P.err : nullptr);
     const int blk = write_kv ? slot / P.block_size : 0, off = write_kv ? slot - blk * P.block_size : 0;
-    const float ir = P.inv_rms[b];
     const float *cosr = P.cos + (int64_t)(pos_ok ? pos : 0) * P.d;
     const float *sinr = P.sin + (int64_t)(pos_ok ? pos : 0) * P.d;
-    constexpr int kPer = kMaxHeadDim / 2 / 64;  // elements of each half per lane
 
-    {
-        const bool is_q = u < P.hq, is_k = !is_q && u < P.hq + P.hkv;
-        const int h = is_q ? u : (is_k ? u - P.hq : u - P.hq - P.hkv);
-        const float *src = is_q ? P.q_proj + ((int64_t)b * P.hq + h) * P.d
-                                : (is_k ? P.k_proj : P.v_proj) + ((int64_t)b * P.hkv + h) * P.d;
-        float lo[kPer], hi[kPer];
-        float ss = 0.f;
+    float lo[kPer], hi[kPer];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = lane + 64 * j;
+        lo[j] = hi[j] = 0.f;
+        if (DFIX == 128 || i < half) {
+            lo[j] = xl[j] * ir;
+            hi[j] = xh[j] * ir;
+            ss += lo[j] * lo[j];
+            ss += hi[j] * hi[j];
+        }
+    }
+    uint16_t *dst;
+    if (is_q) {
+        dst = P.q_out + ((int64_t)b * P.hq + h) * P.d;
+    } else {
+        if (!write_kv) return;
+        dst = is_k ? P.kc + blk * P.k_bs + off * P.k_ts + h * P.k_hs
+                   : P.vc + blk * P.v_bs + off * P.v_ts + h * P.v_hs;
+    }
+    if (is_q || is_k) {
+        ss = wave_sum(ss);
+        const float r = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)P.d) + P.eps));
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             const int i = lane + 64 * j;
-            lo[j] = hi[j] = 0.f;
-            if (i < half) {
-                lo[j] = src[i] * ir;
-                hi[j] = src[i + half] * ir;
-                ss += lo[j] * lo[j];
-                ss += hi[j] * hi[j];
-            }
+            if (DFIX != 128 && i >= half) continue;
+            const float zl = (lo[j] * r) * wl[j];
+            const float zh = (hi[j] * r) * wh[j];
+            float ol = zl * cosr[i] - zh * sinr[i];
+            float oh = zh * cosr[i + half] + zl * sinr[i + half];
+            if (!pos_ok) ol = oh = 0.f;
+            dst[i] = to_bf16(ol);
+            dst[i + half] = to_bf16(oh);
         }
-        uint16_t *dst;
-        if (is_q) {
-            dst = P.q_out + ((int64_t)b * P.hq + h) * P.d;
-        } else {
-            if (!write_kv) return;
-            dst = is_k ? P.kc + blk * P.k_bs + off * P.k_ts + h * P.k_hs
-                       : P.vc + blk * P.v_bs + off * P.v_ts + h * P.v_hs;
-        }
-        if (is_q || is_k) {
-            ss = wave_sum(ss);
-            const float r = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)P.d) + P.eps));
-            const float *w = is_q ? P.q_w : P.k_w;
+    } else {
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int i = lane + 64 * j;
-                if (i >= half) continue;
-                const float zl = (lo[j] * r) * w[i];
-                const float zh = (hi[j] * r) * w[i + half];
-                float ol = zl * cosr[i] - zh * sinr[i];
-                float oh = zh * cosr[i + half] + zl * sinr[i + half];
-                if (!pos_ok) ol = oh = 0.f;
-                dst[i] = to_bf16(ol);
-                dst[i + half] = to_bf16(oh);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int i = lane + 64 * j;
-                if (i >= half) continue;
-                dst[i] = to_bf16(lo[j]);
-                dst[i + half] = to_bf16(hi[j]);
-            }
+        for (int j = 0; j < kPer; ++j) {
+            const int i = lane + 64 * j;
+            if (DFIX != 128 && i >= half) continue;
+            dst[i] = to_bf16(lo[j]);
+            dst[i + half] = to_bf16(hi[j]);
         }
     }
+}
+
+// The prelude kernel for head dim d.
+void launch_prelude_kernel(const PreludeParams &P, unsigned units, unsigned tokens, hipStream_t stream) {
+    if (P.d == 128)
+        hipLaunchKernelGGL(qk_norm_rope_append_kernel<128>, dim3(units, tokens), dim3(64), 0, stream, P);
+    else
+        hipLaunchKernelGGL(qk_norm_rope_append_kernel<0>, dim3(units, tokens), dim3(64), 0, stream, P);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -294,9 +321,7 @@ int launch_paged_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecode
     P.max_pos = pre->max_position;
     P.eps = pre->eps;
     P.pg = paged_of(a, error_flag, bad_length);
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)(a->num_heads + 2 * a->num_kv_heads),
-                                                        (unsigned)tokens),
-                       dim3(64), 0, (hipStream_t)stream, P);
+    launch_prelude_kernel(P, (unsigned)(a->num_heads + 2 * a->num_kv_heads), (unsigned)tokens, (hipStream_t)stream);
     return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
 }
 
@@ -395,8 +420,7 @@ extern "C" int simpler_hip_qk_norm_rope_append(const SimplerHipQkNormRopeAppendA
     P.num_blocks = a->num_blocks;
     P.max_pos = a->max_position;
     P.eps = a->eps;
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)(a->num_heads + 2 * a->num_kv_heads),
-                                                        (unsigned)a->batch),
-                       dim3(64), 0, (hipStream_t)stream, P);
+    launch_prelude_kernel(P, (unsigned)(a->num_heads + 2 * a->num_kv_heads), (unsigned)a->batch,
+                          (hipStream_t)stream);
     return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
 }
