@@ -212,7 +212,7 @@ def launch(args: _lib.PaDecodeArgs, device: torch.device, stream: int | None = N
     ws = _WORKSPACE.get(device, need, stream)
     if prelude is not None:
         if phases != PHASE_MAIN | PHASE_MERGE:
-            raise ValueError("the fused prelude runs both phases")
+            raise ValueError("the prelude entry runs both phases")
         rc = lib.simpler_hip_pa_decode_prelude(ctypes.byref(args), ctypes.byref(prelude), ws.data_ptr(), ws.numel(),
                                                stream)
         if rc != 0:

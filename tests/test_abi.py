@@ -257,7 +257,7 @@ def test_fused_append_validates_on_the_host():
     assert call(_mla_args(), k, None, ws_bytes=16) == -4
 
 
-def test_fused_prelude_validates_on_the_host():
+def test_prelude_entry_validates_on_the_host():
     lib = _lib.lib()
 
     def pre(**kw):

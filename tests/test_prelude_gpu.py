@@ -68,7 +68,7 @@ def _chain(x, hq, q_len, bs, scale, workers):
                                      scale=scale, causal=q_len > 1, num_workers=workers)
 
 
-def _fused(x, q_len, scale, workers):
+def _one_call(x, q_len, scale, workers):
     q_proj = x["q_proj"] if q_len > 1 else x["q_proj"][:, 0]
     k_proj = x["k_proj"] if q_len > 1 else x["k_proj"][:, 0]
     v_proj = x["v_proj"] if q_len > 1 else x["v_proj"][:, 0]
@@ -89,15 +89,15 @@ CASES = {
 
 
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_fused_prelude_equals_prelude_then_decode(name, device):
+def test_prelude_in_one_call_equals_prelude_then_decode(name, device):
     batch, hq, hkv, bs, lens, q_len, workers = CASES[name]
-    print(f"[case] fused prelude {name}", flush=True)
+    print(f"[case] prelude in one call {name}", flush=True)
     x = _inputs(batch, hq, hkv, bs, lens, q_len, seed=960 + len(name))
     a = {n: t.to(device) for n, t in x.items()}
     b = {n: (t.clone() if n in ("key_cache", "value_cache") else t) for n, t in a.items()}
     scale = 1.0 / math.sqrt(D)
     want = _chain(a, hq, q_len, bs, scale, workers)
-    got = _fused(b, q_len, scale, workers)
+    got = _one_call(b, q_len, scale, workers)
     torch.cuda.synchronize(device)
     pa.check_errors(device)
     assert torch.equal(got, want), f"{name}: output differs from prelude then decode"
@@ -106,9 +106,9 @@ def test_fused_prelude_equals_prelude_then_decode(name, device):
     assert torch.isfinite(got).all()
 
 
-def test_fused_prelude_positions_past_the_rope_table(device):
+def test_prelude_in_one_call_positions_past_the_rope_table(device):
     # sequence 1's new tokens sit at positions 36..39 of a 32-row RoPE table
-    print("[case] fused prelude past the RoPE table", flush=True)
+    print("[case] prelude in one call past the RoPE table", flush=True)
     q_len = 4
     x = _inputs(2, 16, 4, 16, [5, 40], q_len, seed=990, rope_len=32)
     a = {n: t.to(device) for n, t in x.items()}
@@ -117,7 +117,7 @@ def test_fused_prelude_positions_past_the_rope_table(device):
     want = _chain(a, 16, q_len, 16, scale, 0)
     torch.cuda.synchronize(device)
     pa.check_errors(device)  # the plain decode sees valid lengths
-    got = _fused(b, q_len, scale, 0)
+    got = _one_call(b, q_len, scale, 0)
     torch.cuda.synchronize(device)
     with pytest.raises(pa.PagedAttentionError) as ei:
         pa.check_errors(device)
