@@ -48,7 +48,7 @@ constexpr int kMaxHeadDim = 1024;
 struct Paged {
     const int32_t *block_table, *context_lens;
     unsigned *error_flag;  // the decode workspace's error word
-    unsigned bad_length;   // its bit for a position outside the RoPE table
+    unsigned bad_length;   // its bit for a length below q_len (or a position outside the RoPE table)
     int32_t q_len, max_blocks;
 };
 
@@ -73,9 +73,9 @@ __device__ __forceinline__ bool slot_ok(int slot, int32_t num_blocks, int32_t bl
 }
 
 // Paged form: position and slot of launch token t, or slot -1 where the
-// token is not written: a position below 0 or past the block-table row (a
-// length the decode reports), or an out-of-pool block (reported when the
-// decode reads it).
+// token is not written: a position below 0 (a length below q_len, reported
+// by the caller of this), one past the block-table row (a length the decode
+// reports), or an out-of-pool block (reported when the decode reads it).
 __device__ __forceinline__ int paged_slot(const Paged &G, const int t, const int32_t block_size,
                                           const int32_t num_blocks, int *pos) {
     const int b = t / G.q_len;
@@ -89,8 +89,9 @@ __device__ __forceinline__ int paged_slot(const Paged &G, const int t, const int
 
 __global__ void __launch_bounds__(kThreads) kv_append_kernel(const AppendParams P) {
     const int t = blockIdx.x;
-    int pos;
+    int pos = 0;
     const int slot = P.pg.block_table ? paged_slot(P.pg, t, P.block_size, P.num_blocks, &pos) : P.slot[t];
+    if (pos < 0 && threadIdx.x == 0) atomicOr(P.pg.error_flag, P.pg.bad_length);  // paged form only
     if (!slot_ok(slot, P.num_blocks, P.block_size, P.err)) return;
     const int blk = slot / P.block_size, off = slot - blk * P.block_size;
     const int kch = P.dk / 8;
@@ -176,7 +177,7 @@ __global__ void __launch_bounds__(64) qk_norm_rope_append_kernel(const PreludePa
     const bool pos_ok = pos >= 0 && pos < P.max_pos;
     if (!pos_ok && u == 0 && threadIdx.x == 0) {
         if (P.err) atomicAdd(P.err, 1);
-        if (P.pg.error_flag && pos >= 0) atomicOr(P.pg.error_flag, P.pg.bad_length);  // past the RoPE table
+        if (P.pg.error_flag) atomicOr(P.pg.error_flag, P.pg.bad_length);  // below q_len, or past the RoPE table
     }
     // count a bad slot once per token (on its first k unit)
     const bool write_kv = pos_ok && slot_ok(slot, P.num_blocks, P.block_size, u == P.hq ? P.err : nullptr);
@@ -260,7 +261,7 @@ namespace simpler_hip {
 using namespace simpler_hip_kv;
 
 int launch_paged_append(const SimplerHipPaDecodeArgs *a, const void *key_new, const void *value_new,
-                        unsigned *error_flag, void *stream) {
+                        unsigned *error_flag, unsigned bad_length, void *stream) {
     const int tokens = a->batch * a->q_len;
     if (tokens == 0) return SIMPLER_HIP_OK;
     AppendParams P{};
@@ -284,7 +285,7 @@ int launch_paged_append(const SimplerHipPaDecodeArgs *a, const void *key_new, co
     P.dv = a->head_dim_v;
     P.block_size = a->block_size;
     P.num_blocks = a->num_blocks;
-    P.pg = paged_of(a, error_flag, 0u);
+    P.pg = paged_of(a, error_flag, bad_length);
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)tokens), dim3(kThreads), 0, (hipStream_t)stream, P);
     return hipGetLastError() == hipSuccess ? SIMPLER_HIP_OK : SIMPLER_HIP_ERR_LAUNCH;
 }

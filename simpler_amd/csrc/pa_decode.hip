@@ -428,7 +428,8 @@ extern "C" int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *a, con
                 if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255))
                     return SIMPLER_HIP_ERR_WORKSPACE;
                 if (a->batch == 0) return SIMPLER_HIP_OK;
-                const int rc2 = launch_paged_append(a, key_new, value_new, (unsigned *)workspace, stream);
+                const int rc2 =
+                    launch_paged_append(a, key_new, value_new, (unsigned *)workspace, kErrBadLength, stream);
                 if (rc2 != SIMPLER_HIP_OK) return rc2;
                 return pa_decode_launch(a, workspace, workspace_bytes, stream,
                                         SIMPLER_HIP_PHASE_MAIN | SIMPLER_HIP_PHASE_MERGE, nullptr);

@@ -22,17 +22,18 @@ int pa_decode_with_mirror(const SimplerHipPaDecodeArgs *a, void *workspace, size
 // The KV append (kv_cache.hip) for a decode's new tokens: the q_len new
 // tokens of sequence b, rows [b, j] of key_new / value_new ([batch, q_len,
 // num_kv_heads, head_dim] contiguous), go to positions context_lens[b] - q_len
-// + j at the slots the block table gives. Positions outside the table row and
-// out-of-pool blocks are not written (the decode reports both). `a` is
-// validated by the caller.
+// + j at the slots the block table gives. A position below 0 (a length below
+// q_len) sets `bad_length` in *error_flag; positions past the table row and
+// out-of-pool blocks are not written either (the decode reports both). `a`
+// is validated by the caller.
 int launch_paged_append(const SimplerHipPaDecodeArgs *a, const void *key_new, const void *value_new,
-                        unsigned *error_flag, void *stream);
+                        unsigned *error_flag, unsigned bad_length, void *stream);
 
 // The decode prelude (kv_cache.hip) over the same tokens: the bf16 query rows
 // into q_out ([batch, q_len, num_heads, head_dim]) and the new K/V rows into
 // the caches, as simpler_hip_qk_norm_rope_append computes them; a position
-// past the RoPE table sets `bad_length` in *error_flag (its query row is zero
-// and its cache rows are not written).
+// below 0 or past the RoPE table sets `bad_length` in *error_flag (its query
+// row is zero and its cache rows are not written).
 int launch_paged_prelude(const SimplerHipPaDecodeArgs *a, const SimplerHipDecodePreludeArgs *pre, void *q_out,
                          unsigned *error_flag, unsigned bad_length, void *stream);
 

@@ -183,6 +183,28 @@ def test_fused_append_length_shorter_than_the_new_tokens_is_reported(device):
     pa.check_errors(device)
 
 
+def test_append_of_two_row_tiles_length_shorter_than_the_new_tokens_is_reported(device):
+    # 32 query rows per kv head (two row tiles per worker): the append runs as
+    # its own launch ahead of the decode, non-causal, so only it sees the length
+    case = make_custom_case(batch=2, num_heads=32, kv_heads=8, head_dim=128, block_size=128, q_len=8,
+                            context_lens=[300, 50], seed=975)
+    k_new, v_new = new_tokens(case, 976)
+    d = case.to(device)
+    lens = d.context_lens.clone()
+    lens[1] = 5  # below q_len: tokens 3..7 of sequence 1 land at positions 0..4
+    before = d.key_cache.clone()
+    pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, lens, k_new.to(device),
+                                     v_new.to(device), scale=case.scale)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    blk = int(case.block_table[1, 0])
+    changed = sorted(set(tuple(x) for x in (d.key_cache != before).any(dim=(2, 3)).nonzero().tolist()))
+    assert [t for t in changed if t[0] == blk] == [(blk, p) for p in range(5)]
+    pa.check_errors(device)
+
+
 @pytest.mark.parametrize("name", ["gqa_d128", "verify_q8", "mla_q1"])
 def test_fused_append_replays_from_a_hip_graph(name, device):
     # The fused append allocates nothing once its workspace is sized, so a

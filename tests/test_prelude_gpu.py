@@ -47,8 +47,8 @@ def _inputs(batch, hq, hkv, bs, lens, q_len, seed, rope_len=None):
         value_cache=rn(pool, bs, hkv, D, std=0.5).to(torch.bfloat16))
 
 
-def _chain(x, hq, q_len, bs, scale, workers):
-    """Standalone prelude over every new token, then the plain decode."""
+def _standalone_prelude(x, hq, q_len, bs):
+    """The standalone prelude over every new token (positions and slots built here); returns the query."""
     batch = x["q_proj"].shape[0]
     hkv = x["k_proj"].shape[2]
     lens = x["context_lens"].cpu().long()
@@ -63,7 +63,12 @@ def _chain(x, hq, q_len, bs, scale, workers):
         x["inv_rms"].reshape(tok), x["q_norm_weight"], x["k_norm_weight"], x["rope_cos"], x["rope_sin"],
         (pos + 1).reshape(tok).to(torch.int32).to(dev), slot.reshape(tok).to(torch.int32).to(dev), x["key_cache"],
         x["value_cache"], num_heads=hq, error_count=torch.zeros(1, dtype=torch.int32, device=dev))
-    query = q_out.reshape(batch, q_len, hq, D) if q_len > 1 else q_out
+    return q_out.reshape(batch, q_len, hq, D) if q_len > 1 else q_out
+
+
+def _chain(x, hq, q_len, bs, scale, workers):
+    """Standalone prelude over every new token, then the plain decode."""
+    query = _standalone_prelude(x, hq, q_len, bs)
     return pa.paged_attention_decode(query, x["key_cache"], x["value_cache"], x["block_table"], x["context_lens"],
                                      scale=scale, causal=q_len > 1, num_workers=workers)
 
@@ -125,3 +130,27 @@ def test_prelude_in_one_call_positions_past_the_rope_table(device):
     assert torch.equal(got, want)
     assert torch.equal(b["key_cache"], a["key_cache"]) and torch.equal(b["value_cache"], a["value_cache"])
     np.testing.assert_array_equal(got[1].float().cpu().numpy(), want[1].float().cpu().numpy())
+
+
+def test_prelude_in_one_call_length_shorter_than_the_new_tokens_is_reported(device):
+    # non-causal q_len 8 (two row tiles per kv head): sequence 1 holds 5 tokens
+    print("[case] prelude in one call with a length below q_len", flush=True)
+    q_len = 8
+    x = _inputs(2, 32, 8, 128, [300, 5], q_len, seed=995)
+    a = {n: t.to(device) for n, t in x.items()}
+    b = {n: (t.clone() if n in ("key_cache", "value_cache") else t) for n, t in a.items()}
+    scale = 1.0 / math.sqrt(D)
+    got = pa.paged_attention_decode_prelude(
+        b["q_proj"], b["k_proj"], b["v_proj"], b["inv_rms"], b["q_norm_weight"], b["k_norm_weight"], b["rope_cos"],
+        b["rope_sin"], b["key_cache"], b["value_cache"], b["block_table"], b["context_lens"], scale=scale,
+        eps=kvc.EPS, causal=False)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    # the rows at positions 0..4 were written as the standalone prelude writes them
+    _standalone_prelude(a, 32, q_len, 128)
+    torch.cuda.synchronize(device)
+    assert torch.equal(b["key_cache"], a["key_cache"]) and torch.equal(b["value_cache"], a["value_cache"])
+    assert torch.isfinite(got[0]).all()
+
