@@ -104,6 +104,9 @@ CASES = {
                        context_lens=[16, 40]),
     "fp16_d128": dict(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, context_lens=[5, 129, 900],
                       dtype=torch.float16),
+    # fp16, two row tiles per kv head: the append's own launch ahead of the decode
+    "fp16_verify_q8": dict(batch=2, num_heads=32, kv_heads=8, head_dim=128, block_size=64, q_len=8, causal=True,
+                           context_lens=[70, 1000], dtype=torch.float16),
     "mla_q1": dict(batch=3, num_heads=128, kv_heads=1, head_dim=576, head_dim_v=512, block_size=64, mla=True,
                    context_lens=[1, 64, 700]),
     "mla_q4": dict(batch=2, num_heads=16, kv_heads=1, head_dim=576, head_dim_v=512, block_size=32, mla=True,
