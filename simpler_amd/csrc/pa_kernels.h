@@ -203,6 +203,24 @@ struct Elem<_Float16> {
     }
 };
 
+// P x V (and P x ones) over two 16-token tiles in one 16x16x32 MFMA: lane
+// (pc, qd) holds k-steps 8qd .. 8qd+7 of its A and B operands; the first four
+// are tile 0's tokens 4qd .. 4qd+3 (its 16x16x16 operands a0, b0), the last
+// four tile 1's (a1, b1), the same order in A and B, so the product sums
+// over all 32 tokens: one instruction where the 16x16x16 form takes two.
+// kTilePairs: where it is used. The single-tile waves (fp8 56.9 against 57.4
+// us per main launch in same-box pairs; cfg2, cfg3 and cfg1 unchanged); the
+// two-tile wave measured slower with it (the verify shape 138.3 against
+// 134.0) and keeps one 16x16x16 MFMA per tile.
+template <int NT, int RTW>
+constexpr bool kTilePairs = NT % 2 == 0 && RTW == 1;
+
+template <typename ET>
+__device__ __forceinline__ f32x4_t mma_tile_pair(const u32x2_t a0, const u32x2_t a1, const u32x2_t b0,
+                                                 const u32x2_t b1, const f32x4_t c) {
+    return Elem<ET>::mma32((u32x4_t){a0[0], a0[1], a1[0], a1[1]}, (u32x4_t){b0[0], b0[1], b1[0], b1[1]}, c);
+}
+
 // Four E4M3FN bytes -> four bf16 (two words); exact (every E4M3FN value is a
 // bf16 value). gfx950 v_cvt_scalef32_pk_bf16_fp8 with scale 1.
 __device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
@@ -677,8 +695,15 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
                     for (int jj = 0; jj < 8; ++jj) acc[r][ds][jj] *= cv;
                 lacc[r] *= cv;
             }
+            // (tile pairs as run_segment forms them: the same bits either way)
+            if constexpr (kTilePairs<NT, RTW>) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
+                for (int t = 0; t < NT; t += 2)
+                    lacc[r] = mma_tile_pair<ET>(pa[r][t], pa[r][t + 1], ones4, ones4, lacc[r]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
+            }
         }
 
         // ---- PV, GT tiles of V at a time; V rows past the context (or of an
@@ -704,20 +729,33 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
                         vr[t][ds][e] = zero ? (u32x4_t){0u, 0u, 0u, 0u} : x;
                     }
                 }
+            auto v_words = [&](const int t, const int ds, const int jj) -> u32x2_t {
+                const int w = jj >> 1;
+                constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                return (u32x2_t){__builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel),
+                                 __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel)};
+            };
+            static_assert(!kTilePairs<NT, RTW> || GT % 2 == 0, "load groups of whole tile pairs");
+            constexpr int TP = kTilePairs<NT, RTW> ? 2 : 1;  // token tiles per PV MFMA, as in run_segment
 #pragma unroll
-            for (int t = 0; t < GT; ++t)
+            for (int t = 0; t < GT; t += TP)
 #pragma unroll
                 for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
-                        const int w = jj >> 1;
-                        constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
-                        const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
-                        const unsigned d0 = __builtin_amdgcn_perm(vr[t][ds][1][w], vr[t][ds][0][w], sel);
-                        const unsigned d1 = __builtin_amdgcn_perm(vr[t][ds][3][w], vr[t][ds][2][w], sel);
+                        const u32x2_t b0 = v_words(t, ds, jj);
+                        if constexpr (TP == 2) {
+                            const u32x2_t b1 = v_words(t + 1, ds, jj);
 #pragma unroll
-                        for (int r = 0; r < RTW; ++r)
-                            acc[r][ds][jj] = Elem<ET>::mma16(pa[r][g + t], (u32x2_t){d0, d1}, acc[r][ds][jj]);
+                            for (int r = 0; r < RTW; ++r)
+                                acc[r][ds][jj] =
+                                    mma_tile_pair<ET>(pa[r][g + t], pa[r][g + t + 1], b0, b1, acc[r][ds][jj]);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < RTW; ++r)
+                                acc[r][ds][jj] = Elem<ET>::mma16(pa[r][g + t], b0, acc[r][ds][jj]);
+                        }
                     }
         }
         // the new tokens of this block into the caches (row tile 0's wave)
@@ -1090,8 +1128,14 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
             }
             // row sums of the rounded p (every column of P x ones is the
             // sum), also for a block whose V adds nothing
+            if constexpr (kTilePairs<NT, RTW>) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
+                for (int t = 0; t < NT; t += 2)
+                    lacc[r] = mma_tile_pair<ET>(pa[r][t], pa[r][t + 1], ones4, ones4, lacc[r]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) lacc[r] = Elem<ET>::mma16(pa[r][t], ones4, lacc[r]);
+            }
         }
 
         // ---- PV: A += P * V ----
@@ -1116,47 +1160,101 @@ __device__ __forceinline__ void run_segment(const KernelParams &P, const int b, 
                                 vr[t][ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                         }
         }
+        if constexpr (kTilePairs<NT, RTW>) {  // two token tiles per PV MFMA
+            // V^T operand words of token tile t: the bf16 of dim 2w + (jj & 1) of
+            // tokens (0, 1) and (2, 3) of lane (pc, qd)'s four rows 4qd + e, low
+            // halves (bytes 0-1 of each) or high halves (bytes 2-3), one v_perm_b32
+            // each (bytes 0-3 from the second operand, 4-7 from the first)
+            auto v_words = [&](const u32x4_t (&vt4)[4], const int jj) -> u32x2_t {
+                const int w = jj >> 1;
+                constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                return (u32x2_t){__builtin_amdgcn_perm(vt4[1][w], vt4[0][w], sel),
+                                 __builtin_amdgcn_perm(vt4[3][w], vt4[2][w], sel)};
+            };
+            // tile t's V rows (8 bf16 dims of tokens 16t + 4qd + e), rows past
+            // vvalid zeroed
+            auto v_tile = [&](const int t, u32x4_t (&vt4)[DVS][4]) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if (!(KV8 && v_zero)) {  // wave-uniform: a zero-scale block adds nothing
-            u32x4_t vt4[DVS][4];       // 8 bf16 dims of tokens 16t + 4qd + e
+                for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
-            for (int ds = 0; ds < DVS; ++ds)
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (KV8)
+                            vt4[ds][e] = fp8x8_to_bf16x8(vrw[t][ds][e][0], vrw[t][ds][e][1]);
+                        else
+                            vt4[ds][e] = vr[t][ds][e];
+                    }
+                if (!kZeroAhead && vvalid < BS) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (KV8)
-                        vt4[ds][e] = fp8x8_to_bf16x8(vrw[t][ds][e][0], vrw[t][ds][e][1]);
-                    else
-                        vt4[ds][e] = vr[t][ds][e];
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * t + 4 * qd + e >= vvalid)
+#pragma unroll
+                            for (int ds = 0; ds < DVS; ++ds) vt4[ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                 }
-            if (!kZeroAhead && vvalid < BS) {
+            };
+            constexpr int TP = 2;  // token tiles per PV MFMA (mma_tile_pair)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (16 * t + 4 * qd + e >= vvalid)
+            for (int t = 0; t < NT; t += TP) {
+              if (!(KV8 && v_zero)) {  // wave-uniform: a zero-scale block adds nothing
+                u32x4_t vt4[TP][DVS][4];
 #pragma unroll
-                        for (int ds = 0; ds < DVS; ++ds) vt4[ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
+                for (int u = 0; u < TP; ++u) v_tile(t + u, vt4[u]);
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const u32x2_t b0 = v_words(vt4[0][ds], jj), b1 = v_words(vt4[1][ds], jj);
+#pragma unroll
+                        for (int r = 0; r < RTW; ++r)
+                            acc[r][ds][jj] = mma_tile_pair<ET>(pa[r][t], pa[r][t + 1], b0, b1, acc[r][ds][jj]);
+                    }
+              }
+#pragma unroll
+                for (int u = 0; u < TP; ++u) after_pv_tile(t + u);
             }
+        } else {
 #pragma unroll
-            for (int ds = 0; ds < DVS; ++ds)
+            for (int t = 0; t < NT; ++t) {
+              if (!(KV8 && v_zero)) {  // wave-uniform: a zero-scale block adds nothing
+                u32x4_t vt4[DVS][4];       // 8 bf16 dims of tokens 16t + 4qd + e
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int w = jj >> 1;
-                    const unsigned a0 = vt4[ds][0][w], a1 = vt4[ds][1][w];
-                    const unsigned a2 = vt4[ds][2][w], a3 = vt4[ds][3][w];
-                    // the bf16 of dim 2w + (jj & 1) of tokens (0, 1) and (2, 3):
-                    // low halves (bytes 0-1 of each) or high halves (bytes 2-3),
-                    // one v_perm_b32 each (bytes 0-3 from the second operand,
-                    // 4-7 from the first)
-                    constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
-                    const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
-                    const unsigned d0 = __builtin_amdgcn_perm(a1, a0, sel);
-                    const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
+                for (int ds = 0; ds < DVS; ++ds)
 #pragma unroll
-                    for (int r = 0; r < RTW; ++r)
-                        acc[r][ds][jj] = Elem<ET>::mma16(pa[r][t], (u32x2_t){d0, d1}, acc[r][ds][jj]);
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (KV8)
+                            vt4[ds][e] = fp8x8_to_bf16x8(vrw[t][ds][e][0], vrw[t][ds][e][1]);
+                        else
+                            vt4[ds][e] = vr[t][ds][e];
+                    }
+                if (!kZeroAhead && vvalid < BS) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * t + 4 * qd + e >= vvalid)
+#pragma unroll
+                            for (int ds = 0; ds < DVS; ++ds) vt4[ds][e] = (u32x4_t){0u, 0u, 0u, 0u};
                 }
-          }
-            after_pv_tile(t);
+#pragma unroll
+                for (int ds = 0; ds < DVS; ++ds)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int w = jj >> 1;
+                        const unsigned a0 = vt4[ds][0][w], a1 = vt4[ds][1][w];
+                        const unsigned a2 = vt4[ds][2][w], a3 = vt4[ds][3][w];
+                        // the bf16 of dim 2w + (jj & 1) of tokens (0, 1) and (2, 3):
+                        // low halves (bytes 0-1 of each) or high halves (bytes 2-3),
+                        // one v_perm_b32 each (bytes 0-3 from the second operand,
+                        // 4-7 from the first)
+                        constexpr unsigned kLoHalves = 0x05040100u, kHiHalves = 0x07060302u;
+                        const unsigned sel = (jj & 1) ? kHiHalves : kLoHalves;
+                        const unsigned d0 = __builtin_amdgcn_perm(a1, a0, sel);
+                        const unsigned d1 = __builtin_amdgcn_perm(a3, a2, sel);
+#pragma unroll
+                        for (int r = 0; r < RTW; ++r)
+                            acc[r][ds][jj] = Elem<ET>::mma16(pa[r][t], (u32x2_t){d0, d1}, acc[r][ds][jj]);
+                    }
+              }
+                after_pv_tile(t);
+            }
         }
     };
 

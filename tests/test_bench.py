@@ -47,7 +47,8 @@ def test_default_line_carries_the_contract(device, capsys, monkeypatch):
     roof = line["roofline"]
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert 0 < roof["frac"] < 1 and abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
-    # the step's throughput (both kernels) is below the main kernel's alone
-    assert 0 < line["value"] <= roof["achieved"]
+    # the step's throughput (both kernels) is below the main kernel's alone; a
+    # 5-step run times each within a few percent (event overhead, clocks)
+    assert 0 < line["value"] <= 1.05 * roof["achieved"]
     cpu = line["cpu_baseline"]
     assert cpu["kind"] in ("port", "reference") and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
