@@ -154,3 +154,51 @@ def test_prelude_in_one_call_length_shorter_than_the_new_tokens_is_reported(devi
     assert torch.equal(b["key_cache"], a["key_cache"]) and torch.equal(b["value_cache"], a["value_cache"])
     assert torch.isfinite(got[0]).all()
 
+
+
+@pytest.mark.parametrize("name", ["q1_qwen3_heads", "q8_two_tiles"])
+def test_prelude_in_one_call_replays_from_a_hip_graph(name, device):
+    # The one call allocates nothing once its workspace is sized, so a caller
+    # can capture its three launches. Between replays, eager work changes the
+    # projections and restores the caches; every replay must equal the
+    # standalone prelude then decode on the same inputs.
+    batch, hq, hkv, bs, lens, q_len, workers = CASES[name]
+    print(f"[case] prelude in one call, hip graph replays {name}", flush=True)
+    xs = [_inputs(batch, hq, hkv, bs, lens, q_len, seed=1200 + s) for s in range(2)]
+    scale = 1.0 / math.sqrt(D)
+    wants = []
+    for x in xs:  # the projections of x, everything else (tables, weights, caches) of xs[0]
+        a = {n: (x[n] if n in ("q_proj", "k_proj", "v_proj", "inv_rms") else t).to(device) for n, t in xs[0].items()}
+        wants.append(_chain(a, hq, q_len, bs, scale, workers))
+    torch.cuda.synchronize(device)
+    b = {n: t.to(device) for n, t in xs[0].items()}
+    caches0 = (xs[0]["key_cache"].to(device), xs[0]["value_cache"].to(device))
+    out = torch.empty(wants[0].shape, dtype=torch.float32, device=device)
+
+    def step():
+        proj = [b[n] if q_len > 1 else b[n][:, 0] for n in ("q_proj", "k_proj", "v_proj")]
+        pa.paged_attention_decode_prelude(
+            *proj, b["inv_rms"], b["q_norm_weight"], b["k_norm_weight"], b["rope_cos"], b["rope_sin"],
+            b["key_cache"], b["value_cache"], b["block_table"], b["context_lens"], out, scale, eps=kvc.EPS,
+            causal=q_len > 1, num_workers=workers)
+
+    side = torch.cuda.Stream(device)
+    with torch.cuda.stream(side):
+        step()  # sizes and zeroes the capture stream's workspace outside the capture
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step()
+    torch.cuda.synchronize(device)
+    for i in range(4):
+        x = xs[i % 2]
+        for n in ("q_proj", "k_proj", "v_proj", "inv_rms"):
+            b[n].copy_(x[n].to(device))
+        b["key_cache"].copy_(caches0[0])
+        b["value_cache"].copy_(caches0[1])
+        out.fill_(float("nan"))
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(out, wants[i % 2]), f"{name}: replay {i} differs"
+    pa.check_errors(device)
