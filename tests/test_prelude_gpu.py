@@ -8,9 +8,10 @@ itself pinned against the oracle (tests/test_kv_cache_gpu.py), the decode
 likewise (tests/test_pa_gpu.py). The output and both caches must be equal.
 Shapes: one row tile (q_len 1, the Qwen3-8B head layout), causal q_len 4 with
 16-token blocks and a forced worker count, two row tiles in one wave (q_len 8),
-four tiles as sibling waves (q_len 16), and lengths past the RoPE table
+four tiles as sibling waves (q_len 16), lengths past the RoPE table
 (reported as BAD_LENGTH, those tokens' query rows zero and their cache rows
-untouched, as the standalone prelude leaves them).
+untouched, as the standalone prelude leaves them), lengths below q_len, and
+replays of the call captured in a HIP graph.
 """
 
 from __future__ import annotations
