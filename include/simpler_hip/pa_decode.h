@@ -154,7 +154,7 @@ int simpler_hip_pa_decode_check(void *workspace, size_t workspace_bytes, void *s
  * as in simpler_hip_pa_decode (skipped / clamped) but not reported: there is
  * no workspace to pass to simpler_hip_pa_decode_check.
  */
-#define SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES (80u << 20)
+#define SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES (136u << 20)
 int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stream);
 
 /*

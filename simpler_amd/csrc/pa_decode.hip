@@ -111,9 +111,9 @@ Kernels pick_kernel(const SimplerHipPaDecodeArgs *a, bool append = false) {
     if (a->kv_format == SIMPLER_HIP_KV_FP8_E4M3) {
         if (dk == dv && !append) s.k = pick_gqa_fp8(bs, dk, out);  // no fused append for fp8 caches
     } else if (is_mla_shape(a)) {
-        if (v_is_k_prefix(a) && a->kv_format == SIMPLER_HIP_KV_BF16) {
-            s.k = pick_mla(bs, out, false);
-            if (append) s.ka = pick_mla(bs, out, true);
+        // (the kernel's fill offsets use 24-bit multiplies: token rows below 8 MB)
+        if (v_is_k_prefix(a) && a->kv_format == SIMPLER_HIP_KV_BF16 && a->k_token_stride * 2 < (1 << 23)) {
+            s.k = pick_mla(bs, out);  // no fused form: the append runs as its own launch
         }
     } else if (dk == dv) {
         s.k = f16 ? pick_gqa_f16(bs, dk, out) : pick_gqa_bf16(bs, dk, out);
@@ -181,10 +181,10 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
     p.row_tiles = (p.rows + 15) / 16;
     p.lanes = 1;
     if (k.mla) {
-        // A work slice runs as `groups` sibling workgroups of 64 rows (4 row
-        // tiles) each; `workers` counts slices.
+        // A work slice runs as `groups` sibling workgroups of 128 rows (8 row
+        // tiles of 16) each; `workers` counts slices.
         p.groups = (p.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
-        p.tiles_per_worker = 4 * p.groups;
+        p.tiles_per_worker = kMlaRowsPerGroup / 16 * p.groups;
         p.row_groups = 1;
         p.threads = 256;
         p.main = k.main;
@@ -415,16 +415,18 @@ extern "C" int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *a, con
     const bool mla = is_mla_shape(a) && v_is_k_prefix(a);
     if (!key_new || ((uintptr_t)key_new & 15)) return SIMPLER_HIP_ERR_INVALID;
     if (mla ? value_new != nullptr : (!value_new || ((uintptr_t)value_new & 15))) return SIMPLER_HIP_ERR_INVALID;
-    if (!mla) {
-        // Two or more row tiles per worker (the two-tile wave, sibling waves):
-        // the append runs as its own launch ahead of the plain decode. There
-        // the fused form's unpipelined new-token blocks measured slower (the
-        // verify shape: 155.2 against 140.2 us per step); with one tile per
-        // worker the fused form is the faster one (cfg2: 113.3 against 114.5).
+    {
+        // Two or more row tiles per worker (the two-tile wave, sibling waves,
+        // MLA's 128-row workgroups): the append runs as its own launch ahead
+        // of the plain decode. There the fused form's unpipelined new-token
+        // blocks measured slower (the verify shape: 155.2 against 140.2 us per
+        // step), and MLA's register budget has no room for the new rows; with
+        // one tile per worker the fused form is the faster one (cfg2: 113.3
+        // against 114.5).
         const Kernels s = pick_kernel(a);
         if (s.k.main) {
             const Plan plan = make_plan(a, s.k);
-            if (plan.tiles_per_worker > 1) {
+            if (plan.tiles_per_worker > 1 || s.k.mla) {
                 if (!workspace || workspace_bytes < plan.total || ((uintptr_t)workspace & 255))
                     return SIMPLER_HIP_ERR_WORKSPACE;
                 if (a->batch == 0) return SIMPLER_HIP_OK;
@@ -514,8 +516,9 @@ namespace {
 
 // Every decode of the direct entry fits here at the default worker count on
 // MI355X (256 CUs): a GQA plan needs at most 2048 partial slots of 16 rows x
-// Dv fp32 (Dv 128: 16 MiB, Dv 256: 32 MiB), the MLA plan 2048 slots of 16 x 512
-// fp32 (64 MiB), plus (m, l) pairs, the error word and the zero page.
+// Dv fp32 (Dv 128: 16 MiB, Dv 256: 32 MiB), the MLA plan 4096 slots of 16 x 512
+// fp32 (256 slices x 8 row tiles x 2: 128 MiB), plus (m, l) pairs, the error
+// word and the zero page.
 constexpr size_t kScratchBytes = (size_t)SIMPLER_HIP_PA_NOALLOC_SCRATCH_BYTES;
 static_assert(kScratchBytes % 256 == 0, "scratch size");
 

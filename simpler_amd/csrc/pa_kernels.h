@@ -1558,29 +1558,35 @@ __global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const Ker
 // MLA decode: one latent KV head shared by every query head (Hkv = 1 in the
 // DeepSeek shape, Dk = 576, Dv = 512), V = the first Dv dims of K.
 //
-// A worker workgroup of four waves owns 64 query rows (a "row group", 16 rows
-// per wave). Each KV block is copied from HBM into LDS with direct
-// global->LDS loads (double buffered: the next block is in flight during the
-// math on this one) and consumed by the four waves. The row groups of one
-// work slice run as sibling workgroups whose ids differ by multiples of 8, so
-// they land on the same XCD and the second reader of a block hits its L2.
-// Q (Dk/32 operand quads) and O^T (Dv x 16 rows, fp32) stay in registers:
-//   QK  S^T[token][row] = K[token][:] . Q[row][:]   MFMA 16x16x32 bf16,
-//       A = K rows from LDS (16-B reads), B = Q registers.
-//   PV  O^T[dim][row] += V^T[dim][token] . P^T[token][row]   MFMA 16x16x32,
-//       A = V^T from LDS by transposing reads (ds_read_b64_tr_b16),
-//       B = P^T, which is the QK result layout itself: lane l holds row l%16
-//       and, per 32-token k-step, tokens {4q..4q+3, 16+4q..16+4q+3}
-//       (q = l/16); the V^T reads pick the same token order.
-// Every lane of O^T holds a single query row, so the per-block rescale is one
-// scalar per lane. Numerics are the same per-block recipe as the decode kernel.
+// A worker workgroup of four waves owns up to 128 query rows (a "row group",
+// 32 rows per wave), so with 128 query heads each KV block of a work slice
+// is fetched from HBM into LDS once, by one compute unit. Blocks are copied
+// with direct global->LDS loads (double buffered: the next block is in flight
+// during the math on this one), plus an L2 prefetch two blocks ahead. Each
+// wave runs its 32 rows end to end; Q (Dk/16 operand quads) and O^T (Dv x 32
+// rows, fp32) stay in its registers, and the waves share only the block
+// buffers.
+//   QK  S^T[token][row] = K[token][:] . Q[row][:]   MFMA 32x32x16 bf16,
+//       A = K rows from LDS (16-B reads), B = Q registers. C: lane l holds
+//       row l%32 and, in register 4a+e, token 8a+4h+e of the 32-token tile
+//       (h = l/32).
+//   PV  O^T[dim][row] += V^T[dim][token] . P^T[token][row]   MFMA 32x32x16,
+//       A = V^T from LDS by transposing reads (ds_read_b64_tr_b16, two per
+//       operand), B = P^T, which is the QK result layout itself: for the
+//       16-token k-step s of a 32-token tile, registers 8s..8s+7 of lane l
+//       hold tokens {16s+4h..16s+4h+3, 16s+8+4h..16s+8+4h+3}; the V^T reads
+//       pick the same token order.
+// Every lane of S^T and O^T holds a single query row, so the block max, the
+// rescale and the row sum are per lane plus one exchange between the two lane
+// halves. Numerics are the same per-block recipe as the decode kernel.
 //
 // LDS row layout: a token's Dk*2 bytes as 16-byte chunks, the row padded to a
 // chunk count = 10 (mod 16): 74 chunks (1184 B) for Dk = 576. Measured on
-// MI355X with the kernel's exact access patterns, that stride runs both the
-// K-operand reads (16 rows x 16 B per 16 lanes) and the transposing V^T reads
-// at full LDS speed (534-548 and 420-427 B/ns per CU), where 73, 76 and 77
-// chunks, with or without XOR swizzles of the chunk index, halve one of them.
+// MI355X with the kernel's access patterns (per 16 lanes: 16 token rows x 16 B
+// for K, 4 token rows x 32 B for the transposing V^T reads), that stride runs
+// both at full LDS speed (534-548 and 420-427 B/ns per CU), where 73, 76 and
+// 77 chunks, with or without XOR swizzles of the chunk index, halve one of
+// them.
 // ---------------------------------------------------------------------------
 
 template <int DK>
@@ -1594,22 +1600,17 @@ __device__ __forceinline__ i16x4_t lds_ld_tr(const char *base, uint32_t off) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4_t *)((LDS_AS char *)base + off));
 }
 
-constexpr int kMlaRowsPerGroup = 64;  // four waves x 16 rows
+constexpr int kMlaRowsPerWave = 32;    // MFMA N of the 32x32x16 tiles
+constexpr int kMlaRowsPerGroup = 128;  // four waves x 32 rows
 
-// LDS exchange area of the MLA workgroup: P^T operands of the four waves'
-// rows ([wave][k-step][lane] x 16 B), then 2 x 64 per-row floats.
-template <int BS>
-struct MlaExchange {
-    static constexpr int kPBytes = 4 * (BS / 32) * 64 * 16;
-    static constexpr int kBytes = kPBytes + 2 * 64 * 4;
-};
-
-__device__ __forceinline__ void lds_stf(char *base, uint32_t off, float v) {
-    *reinterpret_cast<LDS_AS float *>((LDS_AS char *)base + off) = v;
+__device__ __forceinline__ f32x16_t mma_32x32x16(const u32x4_t a, const u32x4_t b, const f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float lds_ldf(const char *base, uint32_t off) {
-    return *reinterpret_cast<const LDS_AS float *>((const LDS_AS char *)base + off);
+// The two bf16 values of a packed word, summed in fp32.
+__device__ __forceinline__ float bf16_pair_sum(const unsigned w) {
+    return __uint_as_float(w << 16) + __uint_as_float(w & 0xffff0000u);
 }
 
 // Workgroup barrier that orders LDS accesses only: the block fill and L2
@@ -1677,65 +1678,46 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t num_re
                      __builtin_amdgcn_readfirstlane((int)num_records), 0x00020000};
 }
 
-template <int BS, int DK, int DV, typename OutT, bool APPEND = false>
+template <int BS, int DK, int DV, typename OutT>
 __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
                                                 const int groups, const int b, const int kvh, const int nblk,
                                                 const int blk_begin, const int blk_end, const int slot,
-                                                char *const smem0, char *const smem1, char *const sink,
-                                                char *const pexch) {
+                                                char *const smem0, char *const smem1, char *const sink) {
     using L = MlaLayout<DK>;
     constexpr int RB = L::kRowBytes;
     constexpr int RC = L::kRowChunks;
     constexpr int KC = L::kChunks;
-    constexpr int NI = BS * RC / 64;  // 1 KB direct-to-LDS loads per block
-    constexpr int NII = (NI + 3) / 4; // of which each wave issues at most NII
-    constexpr int KS = DK / 32;       // QK k-steps
-    constexpr int NT = BS / 16;       // 16-token tiles
-    constexpr int PS = BS / 32;       // PV k-steps
-    constexpr int NC = DV / 16;       // O^T column tiles
-    static_assert(BS % 32 == 0 && (BS * RC) % 64 == 0, "block of whole 32-token k-steps");
-    static_assert(DK % 32 == 0 && DV % 32 == 0 && DV <= DK, "V is a prefix of K");
+    constexpr int NI = BS * RC / 64;   // 1 KB direct-to-LDS loads per block
+    constexpr int NII = (NI + 3) / 4;  // of which each wave issues at most NII
+    constexpr int KS = DK / 16;        // QK k-steps
+    constexpr int NT = BS / 32;        // 32-token tiles
+    constexpr int PS = BS / 16;        // PV k-steps
+    constexpr int NM = DV / 32;        // O^T tiles of 32 dims
+    static_assert(BS % 32 == 0 && (BS * RC) % 64 == 0, "block of whole 32-token tiles");
+    static_assert(DK % 16 == 0 && DV % 32 == 0 && DV <= DK, "V is a prefix of K");
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int q = lane >> 4, pc = lane & 15;
-    const int r0 = rgrp * kMlaRowsPerGroup + 16 * wave;  // first query row of this wave
-    const int rows_here = min(16, P.rows - r0);
-    const bool active = rows_here > 0;
-    int ctx = P.context_lens[b];
-    ctx = min(max(ctx, 0), P.max_blocks * BS);
+    const int h = lane >> 5, j = lane & 31;  // lane half, query row of the wave
+    const int r0 = rgrp * kMlaRowsPerGroup + kMlaRowsPerWave * wave;  // first query row of this wave
+    const int rows_here = min(kMlaRowsPerWave, P.rows - r0);
+    const bool active = rows_here > 0;  // wave-uniform
+    const int ctx = min(max(P.context_lens[b], 0), P.max_blocks * BS);
 
-    // ---- Q (B operand of QK): row pc, dims 32kk+8q..+7 ----
+    // ---- Q (B operand of QK): row j, dims 16kk+8h..+7 ----
     u32x4_t qv[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) qv[kk] = (u32x4_t){0u, 0u, 0u, 0u};
     int rowlen = 0;
-    if (pc < rows_here) {
-        const int r = r0 + pc;
+    if (j < rows_here) {
+        const int r = r0 + j;
         const int i = r / P.group, hh = r - i * P.group;
-        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK + 8 * q;
+        const uint16_t *qrow = P.q + ((int64_t)(b * P.q_len + i) * P.num_heads + kvh * P.group + hh) * DK + 8 * h;
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk) qv[kk] = ld16(qrow + 32 * kk);
+        for (int kk = 0; kk < KS; ++kk) qv[kk] = ld16(qrow + 16 * kk);
         rowlen = P.causal ? ctx - (P.q_len - 1 - i) : ctx;
     }
     const int min_rowlen = P.causal ? ctx - (P.q_len - 1 - r0 / P.group) : ctx;
-
-    // ---- fused append: the new tokens' K rows (positions new0 .. ctx-1),
-    // 16-byte chunk c = threadIdx.x + 256u of the q_len x KC chunks in this
-    // thread's registers, patched into the LDS copy of their block once it is
-    // filled, and written to the cache by row group 0 at the segment's end ----
-    constexpr int NU = APPEND ? (16 * KC + 255) / 256 : 1;  // q_len <= 16
-    const int new0 = ctx - P.q_len;
-    u32x4_t knew[NU];
-    if constexpr (APPEND) {
-#pragma unroll
-        for (int u = 0; u < NU; ++u) {
-            knew[u] = (u32x4_t){0u, 0u, 0u, 0u};
-            const int c = (int)threadIdx.x + 256 * u, j = c / KC;
-            if (blk_end * BS > new0 && j < P.q_len && new0 + j >= 0)
-                knew[u] = ld16(P.k_new + ((int64_t)(b * P.q_len + j) * P.kv_heads + kvh) * DK + 8 * (c - j * KC));
-        }
-    }
 
     // Block-table entries are read through the scalar cache (constant
     // address space): the load is counted by lgkmcnt, so waiting for it never
@@ -1755,123 +1737,162 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
     // out-of-pool block) makes every later token read zeros. ----
     const uint32_t tok_b = (uint32_t)(P.k_token_stride * 2);  // block bytes < 2^31 (host-checked)
     const char *k_head = reinterpret_cast<const char *>(P.k) + (int64_t)kvh * P.k_head_stride * 2;
-    uint32_t voff[NII];
-#pragma unroll
-    for (int ii = 0; ii < NII; ++ii) {
-        const int pch = 64 * (4 * ii + wave) + lane;
-        const int row = pch / RC, pos = pch - row * RC;
-        voff[ii] = (uint32_t)row * tok_b + (pos < KC ? (uint32_t)pos << 4 : 0u);
-    }
-    // ---- L2 prefetch two blocks ahead: this row group's share of the block's
-    // 128-byte lines (tokens r with r % groups == rgrp), each touched by one
-    // 4-byte load into a scratch LDS slot, so the block's later fill is an L2
-    // hit for both row groups. Tokens past the context are not fetched. ----
-    constexpr int LPR = (DK * 2 + 127) / 128;  // lines per token
-    constexpr int NPF = (BS * LPR + 255) / 256;
-    // Every lane issues all NPF loads (lanes without a line of their own touch
-    // the group's first line again), so each wave has exactly NPF prefetch
+    // Lane l of load ii fills LDS chunk p = 256 ii + 64 wave + l of the
+    // buffer: token p / RC, chunk p % RC. Since 256 = 3 RC + 34 for RC = 74,
+    // its byte offset in the block follows from the lane's first chunk
+    // (token t0, chunk c0) as t0*tok + 16 c0 + ii (3 tok + 16*34) + k (tok -
+    // 16 RC), k = (c0 + 34 ii) / RC, computed per load rather than held in
+    // NII registers. Pad chunks (p % RC >= KC) fetch the first bytes of the
+    // next token, or zeros past the descriptor's record count.
+    constexpr int kStepChunks = 256 % RC;  // chunks past the whole rows a load index advances
+    constexpr int kStepRows = 256 / RC;
+    const int p0 = 64 * wave + lane;
+    const int t0 = p0 / RC, c0 = p0 - (p0 / RC) * RC;
+    const uint32_t fill_base = (uint32_t)t0 * tok_b + 16u * (uint32_t)c0;
+    const uint32_t fill_step = (uint32_t)kStepRows * tok_b + 16u * kStepChunks;
+    const uint32_t fill_wrap = tok_b - 16u * RC;  // one more whole row, less the chunks
+    constexpr uint32_t kDivRC = (65536u + RC - 1) / RC;
+    static_assert([] {
+        for (uint32_t x = 0; x < RC + kStepChunks * NII; ++x)
+            if ((x * kDivRC) >> 16 != x / RC) return false;
+        return true;
+    }(), "multiply-shift division by RC");
+    // ---- L2 prefetch two blocks ahead: every 128-byte line of the block's
+    // valid tokens (as one byte range), each touched by one 4-byte load into a
+    // scratch LDS slot, so the block's later fill is an L2 hit. Row group g
+    // of a slice takes lines g, g + groups, ... Lines past the descriptor's
+    // record count (tokens past the context) are not fetched. ----
+    constexpr int LPB = (BS * DK * 2 + 127) / 128;  // lines of a block of dense rows
+    constexpr int NPF = (LPB + 255) / 256;
+    // Every lane issues all NPF loads, so each wave has exactly NPF prefetch
     // loads outstanding after its block fill: see the barrier below.
-    uint32_t pfoff[NPF];
-#pragma unroll
-    for (int pi = 0; pi < NPF; ++pi) {
-        const int idx = pi * 256 + (int)threadIdx.x;
-        const int rl = idx / LPR, ln = idx - rl * LPR;
-        const int row = rl * groups + rgrp;
-        pfoff[pi] = row < BS ? (uint32_t)row * tok_b + 128u * ln : (uint32_t)rgrp * tok_b;
-    }
-    auto prefetch = [&](int blk) {
-        bool bad = false;
-        const int phys = phys_of(blk, bad);
-        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
-        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
-        const uint32_t sink_addr = lds_addr_of(sink);
-#pragma unroll
-        for (int pi = 0; pi < NPF; ++pi) lds_fill4(rsrc, pfoff[pi], sink_addr);
+    const uint32_t pf_base = 128u * ((uint32_t)threadIdx.x * groups + rgrp);
+    const uint32_t pf_step = 128u * 256u * groups;
+    // A block's fill (or L2 prefetch) as a buffer descriptor and an LDS
+    // address, both wave-uniform; its loads are issued one at a time so that
+    // those of the next block can be spread over this block's math (issued
+    // in a burst, the four waves' loads queue behind each other at the
+    // compute unit's vector-memory unit and stall every wave's issue).
+    struct Fill {
+        i32x4_t rsrc;
+        uint32_t lds;
     };
-    auto issue = [&](int blk, char *dst) -> bool {
-        bool bad = false;
-        const int phys = phys_of(blk, bad);
-        const int vvalid = bad ? 0 : min(BS, ctx - blk * BS);
-        const i32x4_t rsrc = buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b);
-        const uint32_t dst_addr = lds_addr_of(dst) + 1024u * wave;
-#pragma unroll
-        for (int ii = 0; ii < NII; ++ii) {
-            const int i = 4 * ii + wave;
-            if (NI % 4 == 0 || i < NI) lds_fill16(rsrc, voff[ii], dst_addr + 4096u * ii);
+    // blk < 0: a descriptor with no records, whose loads fetch nothing (and
+    // write zeros to LDS): the loads stay unconditional, without branches in
+    // the math and with a fixed count for the vmcnt waits.
+    auto fill_of = [&](int blk, char *dst, bool &bad) -> Fill {
+        bad = false;
+        const int phys = blk >= 0 ? phys_of(blk, bad) : 0;
+        const int vvalid = (bad || blk < 0) ? 0 : min(BS, ctx - blk * BS);
+        return {buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b),
+                (uint32_t)__builtin_amdgcn_readfirstlane(dst ? lds_addr_of(dst) + 1024u * wave : lds_addr_of(sink))};
+    };
+    // Per-lane offsets: recomputed for every block from two registers. The
+    // empty asm hides that they do not change, so the compiler cannot hoist
+    // NII offsets out of the block loop into registers it does not have.
+    auto fill_regs = [&](uint32_t &base, uint32_t &cc, uint32_t &pf) {
+        base = fill_base;
+        cc = (uint32_t)c0;
+        pf = pf_base;
+        asm volatile("" : "+v"(base), "+v"(cc), "+v"(pf));
+    };
+    auto fill_one = [&](const Fill &f, int ii, uint32_t base, uint32_t cc) {
+        if (NI % 4 == 0 || 4 * ii + wave < NI) {
+            // (cc + kStepChunks ii) / RC by a 24-bit multiply and shift, exact
+            // over the operand's range (checked at compile time); k * wrap as
+            // a signed 24-bit multiply-add (the host keeps |wrap| < 2^23)
+            const uint32_t k = __umul24(cc + kStepChunks * ii, kDivRC) >> 16;
+            const uint32_t off = (uint32_t)(__mul24((int)k, (int)fill_wrap) + (int)(base + ii * fill_step));
+            lds_fill16(f.rsrc, off, f.lds + 4096u * ii);
         }
-        return bad;
+    };
+    auto prefetch_one = [&](const Fill &f, int pi, uint32_t pf) { lds_fill4(f.rsrc, pf + pi * pf_step, f.lds); };
+
+    // O^T accumulators (tile mt: dims 32mt .. 32mt+31 of row j) and the row
+    // sum, both in the frame of the latest used block max f.
+    f32x16_t acc[NM];
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[mt][e] = 0.f;
+    float l_run = 0.f;
+    float m_run = kNegClamp, f_run = kNegClamp;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const bf16x2_t ones2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+
+    // per-lane LDS byte offsets within a block buffer: K operand token j, dims
+    // 8h..; V^T operand (16-lane group g: dims 16(g&1)..+15, tokens 4h..4h+3,
+    // lane pc addressing token 4h + pc/4, dims 4(pc%4)..+3)
+    const uint32_t kofs = j * RB + 16 * h;
+    const int g = lane >> 4, pc = lane & 15;
+    const uint32_t vofs = (4 * h + (pc >> 2)) * RB + 32 * (g & 1) + 8 * (pc & 3);
+
+    // The value of the other lane half (lane l ^ 32), combined with this
+    // lane's: both halves get the same result (lower half's operand first).
+    auto halves_max = [](float x) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    };
+    auto halves_sum = [](float x) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
     };
 
-    // O^T accumulators and the row-sum tile (ones x P^T: every lane holds its
-    // row's sum), both in the frame of the latest used block max f.
-    // PV's output dims are split across the four waves: wave w accumulates
-    // O^T column tiles NCW*w .. NCW*w + NCW-1 (dims 16 c ..) for the four row
-    // tiles of the workgroup (acc[cl][r]), so each wave reads a quarter of V^T
-    // from LDS; the P^T operands of all four row tiles come through pexch.
-    constexpr int NCW = NC / 4;
-    f32x4_t acc[NCW][4];
-#pragma unroll
-    for (int c = 0; c < NCW; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[c][r] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    f32x4_t lacc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegClamp, f_run = kNegClamp;
-    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-    constexpr float kLog2e = 1.4426950408889634f;
-
-    // per-lane LDS byte offsets within a block buffer
-    const uint32_t kofs = pc * RB + 16 * q;
-    const uint32_t vbase = (4 * q + (pc >> 2)) * RB + 8 * (pc & 1);
-    const uint32_t vofs_even = vbase + 16 * ((pc & 3) >> 1);
-    const uint32_t vofs_odd = vofs_even + 32;
-
-    // Scheduling: LDS reads are issued two stages ahead of the MFMAs that
-    // consume them (an LDS read takes longer than one stage of MFMAs), and the
-    // group barriers pin the order of reads, VALU work and MFMAs in a stage.
+    // Scheduling: LDS reads are issued ahead of the MFMAs that consume them
+    // (an LDS read takes longer than one stage of MFMAs), and the group
+    // barriers pin the order of reads, VALU work and MFMAs in a stage.
     constexpr int kDsRead = 0x100, kValu = 0x002, kMfma = 0x008;
-    auto compute = [&](const char *kb, int blk, bool blk_bad) {
+    constexpr int KA = 1;  // QK stages (k-steps) the K reads run ahead
+    constexpr int VA = 2;  // PV stages (single MFMAs) the V^T reads run ahead
+    constexpr int NPV = NM * PS;  // PV stages
+    static_assert(NM % 2 == 0, "PV runs over pairs of O^T tiles");
+    // next: the fill of the next block (its loads spread over the QK
+    // stages), pf: the L2 prefetch of the block after (in the first PV
+    // stages, after every fill load, for the vmcnt accounting below).
+    auto compute = [&](const char *kb, int blk, bool blk_bad, const Fill &next, const Fill &pf) {
         const bool first = (blk == blk_begin);
-        // ---- QK: stage = one 32-dim k-step over the NT token tiles ----
-        f32x4_t s[NT];
+        uint32_t fbase, fcc, fpf;
+        fill_regs(fbase, fcc, fpf);
+        // ---- QK: stage = one 16-dim k-step over the NT token tiles ----
+        f32x16_t s[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) s[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-        u32x4_t kf[3][NT];
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
+        u32x4_t kf[KA + 1][NT];
         auto load_k = [&](int kk, u32x4_t (&dst)[NT]) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) dst[t] = lds_ld16(kb, kofs + 64 * kk + t * 16 * RB);
+            for (int t = 0; t < NT; ++t) dst[t] = lds_ld16(kb, kofs + t * 32 * RB + 32 * kk);
         };
-        load_k(0, kf[0]);
-        load_k(1, kf[1]);
+#pragma unroll
+        for (int kk = 0; kk < KA; ++kk) load_k(kk, kf[kk]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
-            if (kk + 2 < KS) load_k(kk + 2, kf[(kk + 2) % 3]);
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kk % 3][t]),
-                                                              __builtin_bit_cast(bf16x8_t, qv[kk]), s[t], 0, 0, 0);
-            if (kk + 2 < KS) __builtin_amdgcn_sched_group_barrier(kDsRead, NT, 0);
+            for (int ii = 0; ii < NII; ++ii)
+                if (ii * KS / NII == kk) fill_one(next, ii, fbase, fcc);
+            if (kk + KA < KS) load_k(kk + KA, kf[(kk + KA) % (KA + 1)]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) s[t] = mma_32x32x16(kf[kk % (KA + 1)][t], qv[kk], s[t]);
+            if (kk + KA < KS) __builtin_amdgcn_sched_group_barrier(kDsRead, NT, 0);
             __builtin_amdgcn_sched_group_barrier(kMfma, NT, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // ---- PV operand reads for the first two stages go out before the
-        // softmax math (they do not depend on it) ----
-        constexpr int NSC = NCW / 2;  // PV stages of two of this wave's O^T column tiles
-        i16x4_t vf[3][2][PS][2];
-        auto load_v = [&](int sc, i16x4_t (&dst)[2][PS][2]) {
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const uint32_t co = (cc ? vofs_odd : vofs_even) + 64 * (NSC * wave + sc);
-#pragma unroll
-                for (int u = 0; u < PS; ++u) {
-                    dst[cc][u][0] = lds_ld_tr(kb, co + u * 32 * RB);
-                    dst[cc][u][1] = lds_ld_tr(kb, co + u * 32 * RB + 16 * RB);
-                }
-            }
+        // ---- V^T operand reads of the first PV stages go out before the
+        // softmax math (they do not depend on it). Stage q = (pair q / (2 PS),
+        // k-step (q / 2) % PS, tile 2 (q / (2 PS)) + q % 2) ----
+        i16x4_t vf[VA + 1][2];
+        auto stage_tile = [](int q) { return 2 * (q / (2 * PS)) + (q & 1); };
+        auto stage_kstep = [](int q) { return (q >> 1) % PS; };
+        auto load_v = [&](int q, i16x4_t (&dst)[2]) {
+            const uint32_t o = vofs + 64 * stage_tile(q) + 16 * stage_kstep(q) * RB;
+            dst[0] = lds_ld_tr(kb, o);
+            dst[1] = lds_ld_tr(kb, o + 8 * RB);
         };
-        load_v(0, vf[0]);
-        load_v(1, vf[1]);
+#pragma unroll
+        for (int q = 0; q < VA; ++q) load_v(q, vf[q]);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- mask, block max of s*scale (golden :145-165). For scale > 0 the
@@ -1889,16 +1910,15 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (16 * t + 4 * q + e >= rvalid) s[t][e] = -INFINITY;
+                for (int e = 0; e < 16; ++e)
+                    if (32 * t + 8 * (e >> 2) + 4 * h + (e & 3) >= rvalid) s[t][e] = -INFINITY;
         }
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = halves_max(mx);
         const float mb = fmaxf(mx * sc, kNegClamp);
         // ---- online merge (aiv_online_update.cpp:183-207) in the block frame ----
         const float mnew = first ? mb : fmaxf(m_run, mb);
@@ -1908,190 +1928,155 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         const float mb2 = use ? mb * kLog2e : INFINITY;  // a skipped block gives p = 0
         const float sc2 = sc * kLog2e;
         u32x4_t pk[PS];
+        float lsum = 0.f;
 #pragma unroll
-        for (int u = 0; u < PS; ++u) {
-            unsigned wv[4];
+        for (int ks = 0; ks < PS; ++ks) {
+            const int t = ks >> 1, s8 = 8 * (ks & 1);
+            unsigned w[4];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                for (int e2 = 0; e2 < 2; ++e2) {
-                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2], sc2, -mb2));
-                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + hf][2 * e2 + 1], sc2, -mb2));
-                    wv[2 * hf + e2] = pack_bf16x2(p0, p1);
-                }
-            pk[u] = (u32x4_t){wv[0], wv[1], wv[2], wv[3]};
+            for (int i = 0; i < 4; ++i) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][s8 + 2 * i], sc2, -mb2));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][s8 + 2 * i + 1], sc2, -mb2));
+                w[i] = pack_bf16x2(p0, p1);
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[i]), ones2, lsum, false);
+            }
+            pk[ks] = (u32x4_t){w[0], w[1], w[2], w[3]};
         }
+        lsum = halves_sum(lsum);  // the row's other 32 tokens
         m_run = mnew;
         if (use) f_run = mb;
-        // l (sum of the rounded p) on the matrix unit: ones x P^T
-        lacc *= cf;
-#pragma unroll
-        for (int u = 0; u < PS; ++u)
-            lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8_t, pk[u]), lacc, 0, 0, 0);
-
-        // ---- hand this wave's P^T and per-row factor to the other waves ----
-#pragma unroll
-        for (int u = 0; u < PS; ++u) lds_st16(pexch, ((wave * PS + u) * 64 + lane) * 16, pk[u]);
-        if (q == 0) lds_stf(pexch, MlaExchange<BS>::kPBytes + (wave * 16 + pc) * 4, cf);
-        lds_barrier();
-        u32x4_t pb[4][PS];  // P^T of row tile r (wave r's rows), k-step u
-        float cfr[4];       // e^{f - m_blk} of row pc of row tile r
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-            for (int u = 0; u < PS; ++u) pb[r][u] = lds_ld16(pexch, ((r * PS + u) * 64 + lane) * 16);
-            cfr[r] = lds_ldf(pexch, MlaExchange<BS>::kPBytes + (r * 16 + pc) * 4);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            acc[0][r] *= cfr[r];
-            acc[1][r] *= cfr[r];
-        }
+        l_run = l_run * cf + lsum;
+        acc[0] *= cf;
+        acc[1] *= cf;
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- A' = e^{f - m_blk} A + P V: stage sc = this wave's column tiles
-        // 2sc, 2sc+1 for the four row tiles; the next stage's tiles are rescaled
-        // between this stage's MFMAs ----
+        // ---- A' = e^{f - m_blk} A + P V over pairs of O^T tiles: a pair's
+        // MFMAs alternate between its two tiles (an MFMA right after one into
+        // the same accumulator waits for it), and the next pair is rescaled
+        // during them ----
+        constexpr int RPS = 32 / (2 * PS);  // rescale multiplies per stage
 #pragma unroll
-        for (int sc = 0; sc < NSC; ++sc) {
-            if (sc + 2 < NSC) load_v(sc + 2, vf[(sc + 2) % 3]);
-            if (sc + 1 < NSC) {
+        for (int q = 0; q < NPV; ++q) {
+            const int mt = stage_tile(q), ks = stage_kstep(q);
+            const int pair = q / (2 * PS), qi = q % (2 * PS);
+            if (q < NPF) prefetch_one(pf, q, fpf);
+            if (q + VA < NPV) load_v(q + VA, vf[(q + VA) % (VA + 1)]);
+            if (2 * pair + 2 < NM) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc[2 * sc + 2][r] *= cfr[r];
-                    acc[2 * sc + 3][r] *= cfr[r];
+                for (int e = 0; e < RPS; ++e) {
+                    const int idx = qi * RPS + e;  // of the next pair's 32 values
+                    acc[2 * pair + 2 + idx / 16][idx % 16] *= cf;
                 }
             }
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                for (int u = 0; u < PS; ++u) {
-                    const bf16x8_t va = __builtin_bit_cast(
-                        bf16x8_t,
-                        __builtin_shufflevector(vf[sc % 3][cc][u][0], vf[sc % 3][cc][u][1], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[2 * sc + cc][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            va, __builtin_bit_cast(bf16x8_t, pb[r][u]), acc[2 * sc + cc][r], 0, 0, 0);
-                }
-            if (sc + 2 < NSC) __builtin_amdgcn_sched_group_barrier(kDsRead, 4 * PS, 0);
-#pragma unroll
-            for (int g2 = 0; g2 < 8 * PS; ++g2) {
-                __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-                if (sc + 1 < NSC) __builtin_amdgcn_sched_group_barrier(kValu, 32 / (8 * PS), 0);
-            }
+            const i16x4_t *vv = vf[q % (VA + 1)];
+            const u32x4_t va = __builtin_bit_cast(u32x4_t, __builtin_shufflevector(vv[0], vv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[mt] = mma_32x32x16(va, pk[ks], acc[mt]);
+            if (q + VA < NPV) __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+            if (2 * pair + 2 < NM) __builtin_amdgcn_sched_group_barrier(kValu, RPS, 0);
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // ---- block loop: wait + barrier, fill the other buffer with the next
-    // block, prefetch the one after into L2, math on this one ----
-    // Vector memory ops complete in order. At the top of iteration blk this
-    // wave has outstanding: the fill of blk, then (if issued) the NPF prefetch
-    // loads of blk+1. Waiting for "at most NPF outstanding" therefore
-    // completes the fill and leaves the prefetch in flight; with no prefetch
-    // issued the wait is for zero. lgkmcnt(0): this wave's LDS reads of the
-    // buffer about to be refilled are done.
+    // ---- block loop: wait + barrier, then the math on this block with the
+    // next block's fill and the L2 prefetch of the one after spread over it
+    // (both as loads of nothing where there is no such block) ----
+    // Vector memory ops complete in order. Before the loop, one wait for
+    // everything: the Q rows and the first block's fill. It is unconditional
+    // so that the compiler knows those loads are complete and inserts no
+    // waits for them inside the loop (a wait there would also wait for the
+    // next block's fill, which it does not count). At the top of iteration
+    // blk > blk_begin this wave has outstanding: the prefetch of blk, the
+    // fill of blk, then the NPF prefetch loads of blk+1. Waiting for "at most
+    // NPF outstanding" completes the fill and leaves the prefetch in flight.
+    // lgkmcnt(0): this wave's LDS reads of the buffer about to be refilled
+    // are done.
     // s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
     constexpr unsigned kWaitFillOnly = 0x0070u | ((unsigned)NPF & 15u) | (((unsigned)NPF >> 4) << 14);
     constexpr unsigned kWaitAll = 0x0070u;  // vmcnt(0) expcnt(7) lgkmcnt(0)
     static_assert(NPF < 64, "vmcnt range");
-    bool bad_cur = issue(blk_begin, smem0);
+    bool bad_cur = false, any_bad = false;
+    {
+        const Fill f0 = fill_of(blk_begin, smem0, bad_cur);
+        uint32_t fbase, fcc, fpf;
+        fill_regs(fbase, fcc, fpf);
+#pragma unroll
+        for (int ii = 0; ii < NII; ++ii) fill_one(f0, ii, fbase, fcc);
+        __builtin_amdgcn_s_waitcnt(kWaitAll);
+        bool unused = false;
+        const Fill f1 = fill_of(blk_begin + 1 < blk_end ? blk_begin + 1 : -1, nullptr, unused);
+#pragma unroll
+        for (int pi = 0; pi < NPF; ++pi) prefetch_one(f1, pi, fpf);
+    }
     for (int blk = blk_begin; blk < blk_end; ++blk) {
         const bool even = ((blk - blk_begin) & 1) == 0;
         __builtin_amdgcn_sched_barrier(0);
-        if (blk > blk_begin && blk + 1 < blk_end)  // prefetch of blk+1 was issued after the fill of blk
-            __builtin_amdgcn_s_waitcnt(kWaitFillOnly);
-        else
-            __builtin_amdgcn_s_waitcnt(kWaitAll);
+        if (blk > blk_begin) __builtin_amdgcn_s_waitcnt(kWaitFillOnly);
         __builtin_amdgcn_s_barrier();  // every wave's fill landed; the other buffer is free
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (APPEND) {
-            if (blk * BS + BS > new0) {  // the block holds new tokens (workgroup-uniform)
-                char *buf = even ? smem0 : smem1;
+        bool bad_next = false, unused = false;
+        // the buffer not read by this block takes the next one (or zeros)
+        const Fill next = fill_of(blk + 1 < blk_end ? blk + 1 : -1, even ? smem1 : smem0, bad_next);
+        const Fill pf = fill_of(blk + 2 < blk_end ? blk + 2 : -1, nullptr, unused);
+        any_bad |= bad_cur;
+        if (active) {
+            compute(even ? smem0 : smem1, blk, bad_cur, next, pf);
+        } else {  // no rows: the loads only
+            uint32_t fbase, fcc, fpf;
+            fill_regs(fbase, fcc, fpf);
 #pragma unroll
-                for (int u = 0; u < NU; ++u) {
-                    const int c = (int)threadIdx.x + 256 * u, j = c / KC;
-                    const int o = new0 + j - blk * BS;  // row of the token in this block
-                    if (j < P.q_len && new0 + j >= 0 && (unsigned)o < (unsigned)BS)
-                        lds_st16(buf, (uint32_t)(o * RB + 16 * (c - j * KC)), knew[u]);
-                }
-                lds_barrier();
-            }
+            for (int ii = 0; ii < NII; ++ii) fill_one(next, ii, fbase, fcc);
+#pragma unroll
+            for (int pi = 0; pi < NPF; ++pi) prefetch_one(pf, pi, fpf);
         }
-        bool bad_next = false;
-        if (blk + 1 < blk_end) bad_next = issue(blk + 1, even ? smem1 : smem0);
-        if (blk + 2 < blk_end) prefetch(blk + 2);
-        if (bad_cur && threadIdx.x == 0) atomicOr(P.error_flag, kErrBadBlock);
-        compute(even ? smem0 : smem1, blk, bad_cur);
         bad_cur = bad_next;
     }
-    __syncthreads();  // the buffers are refilled by the next segment; pexch is free
-    if constexpr (APPEND) {  // the new tokens of this segment's blocks into the cache
-        if (rgrp == 0 && blk_end * BS > new0) {
-#pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const int c = (int)threadIdx.x + 256 * u, j = c / KC;
-                const int p = new0 + j;
-                if (j >= P.q_len || p < 0 || p < blk_begin * BS || p >= blk_end * BS) continue;
-                bool bad = false;
-                const int phys = phys_of(p / BS, bad);
-                if (bad) continue;
-                char *row = const_cast<char *>(k_head) + (int64_t)phys * P.k_block_stride * 2 + (int64_t)(p % BS) * tok_b;
-                *reinterpret_cast<u32x4_t *>(row + 16 * (c - j * KC)) = knew[u];
-            }
-        }
-    }
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // the last zero fill is done before the next segment's
+    if (any_bad && threadIdx.x == 0) atomicOr(P.error_flag, kErrBadBlock);
+    __syncthreads();  // the buffers are refilled by the next segment
 
-    // ---- finish: O = e^{f-m} A, l = e^{f-m} L. The row factors live with the
-    // row's wave; every wave holds a quarter of every row's dims ----
+    // ---- finish: O = e^{f-m} A, l = e^{f-m} L; lane (h, j) holds dims
+    // 32mt + 8a + 4h + e (register 4a+e of tile mt) of row j ----
+    if (!active || j >= rows_here) return;
+    const int row = r0 + j;
+    if (blk_begin == 0 && blk_end == nblk) {  // the whole tile: final output
+        const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // the frame factor cancels
+        const int64_t off = out_row_offset(P, b, kvh, row, DV) + 4 * h;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                OutStore<OutT>::store4(
+                    P.out, off + 32 * mt + 8 * a,
+                    (f32x4_t){acc[mt][4 * a], acc[mt][4 * a + 1], acc[mt][4 * a + 2], acc[mt][4 * a + 3]} * inv);
+        return;
+    }
+    // ---- a piece of the tile: partial (O relative to m, plus m and l) per
+    // 16-row tile (the merge kernel's unit) ----
     const float osc = __expf(f_run - m_run);
-    const float l_tot = lacc[0] * osc;
-    if (q == 0) {
-        lds_stf(pexch, (wave * 16 + pc) * 4, osc);
-        lds_stf(pexch, 256 + (wave * 16 + pc) * 4, lacc[0]);
-    }
-    lds_barrier();
-    const bool whole = blk_begin == 0 && blk_end == nblk;
+    const int64_t piece = ((int64_t)slice * P.tiles_per_worker + (row >> 4)) * 2 + slot;
+    float *dst = P.part_o + (piece * 16 + (row & 15)) * DV + 4 * h;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rows_r = min(16, P.rows - (rgrp * kMlaRowsPerGroup + 16 * r));
-        if (pc >= rows_r) continue;
-        const int row = rgrp * kMlaRowsPerGroup + 16 * r + pc;
-        if (whole) {
-            const float lr = lds_ldf(pexch, 256 + (r * 16 + pc) * 4);
-            const float inv = lr > 0.f ? 1.f / lr : 0.f;  // the frame factor cancels
-            const int64_t off = out_row_offset(P, b, kvh, row, DV) + 4 * q;
+    for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
-            for (int cl = 0; cl < NCW; ++cl)
-                OutStore<OutT>::store4(P.out, off + 16 * (NCW * wave + cl), acc[cl][r] * inv);
-        } else {
-            const float oscr = lds_ldf(pexch, (r * 16 + pc) * 4);
-            const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + r) * 2 + slot;
-            float *dst = P.part_o + (piece * 16 + pc) * DV + 4 * q;
-#pragma unroll
-            for (int cl = 0; cl < NCW; ++cl)
-                *reinterpret_cast<f32x4_t *>(dst + 16 * (NCW * wave + cl)) = acc[cl][r] * oscr;
-        }
-    }
-    if (!whole && active && pc < rows_here && q == 0) {
-        const int64_t piece = ((int64_t)slice * P.tiles_per_worker + rgrp * 4 + wave) * 2 + slot;
-        P.part_ml[piece * 32 + pc] = m_run;
-        P.part_ml[piece * 32 + 16 + pc] = l_tot;
+        for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<f32x4_t *>(dst + 32 * mt + 8 * a) =
+                (f32x4_t){acc[mt][4 * a], acc[mt][4 * a + 1], acc[mt][4 * a + 2], acc[mt][4 * a + 3]} * osc;
+    if (h == 0) {
+        P.part_ml[piece * 32 + (row & 15)] = m_run;
+        P.part_ml[piece * 32 + 16 + (row & 15)] = l_run * osc;
     }
 }
 
-// Worker workgroup = four waves = one row group of one work slice. The work
-// list holds (batch, kv head, KV block) entries; every row group of a slice
-// walks the same entries.
-template <int BS, int DK, int DV, typename OutT, bool APPEND = false>
+// Worker workgroup = four waves = one row group (up to 128 query rows) of one
+// work slice. The work list holds (batch, kv head, KV block) entries; every
+// row group of a slice walks the same entries.
+template <int BS, int DK, int DV, typename OutT>
 __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     using L = MlaLayout<DK>;
     __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
-    // P^T of every wave's rows and per-row factors, handed between the waves
-    __shared__ __attribute__((aligned(16))) char pexch[MlaExchange<BS>::kBytes];
     flag_bad_lengths(P);
     const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
     int slice = 0, rgrp = 0;
@@ -2114,8 +2099,8 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     int slot = 0;
     while (pos < end && nb > 0) {
         const int seg = min(end - pos, nb - blk);
-        run_mla_segment<BS, DK, DV, OutT, APPEND>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0,
-                                                  smem1, sink, pexch);
+        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0,
+                                                  smem1, sink);
         pos += seg;
         slot = 1;
         if (pos >= end) break;
@@ -2162,8 +2147,8 @@ KernelPair pick_gqa_bf16_append(int bs, int d, int out_dtype);
 KernelPair pick_gqa_f16_append(int bs, int d, int out_dtype);
 // GQA decode with fp8 E4M3FN caches (bf16 query), Dk == Dv == 128.
 KernelPair pick_gqa_fp8(int bs, int d, int out_dtype);
-// MLA (Dk 576, Dv 512, V a prefix of K), bf16, without or with the fused KV append.
-KernelPair pick_mla(int bs, int out_dtype, bool append);
+// MLA (Dk 576, Dv 512, V a prefix of K), bf16.
+KernelPair pick_mla(int bs, int out_dtype);
 // The split merge for output width dv.
 MergeFn pick_merge(int dv, int out_dtype);
 

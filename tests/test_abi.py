@@ -228,8 +228,9 @@ def test_mla_dispatch_and_plan():
     assert name(_mla_args()) == "pa_mla_kernel"
     assert name(_mla_args(block_size=32)) == "pa_mla_kernel"
     assert name(_args()) == "pa_decode_kernel"
-    # 128 query rows = two 64-row groups: 128 slices x 2 workgroups on a 256-CU device
-    assert pa.plan(_mla_args()) == 128
+    # 128 query rows = one 128-row group: 256 slices of one workgroup on a 256-CU device
+    assert pa.plan(_mla_args()) == 256
+    assert pa.plan(_mla_args(num_heads=192)) == 128  # two row groups per slice
     assert pa.plan(_mla_args(num_heads=16)) == 256
     ws = lambda **kw: lib.simpler_hip_pa_decode_workspace_size(ctypes.byref(_mla_args(**kw)))
     # two partial slots per row tile (8 per slice), 16 rows x 512 fp32 each
