@@ -29,6 +29,7 @@ using namespace pa;
 constexpr int kZeroOffset = 128;  // workspace bytes [128, 256) are never written after init
 constexpr int kMaxAppendTokens = 16;  // fused append: new tokens per sequence (one per residue mod 16)
 constexpr size_t kMaxZeroPageBytes = 1 << 20;  // larger token strides read the padding tiles as they are
+constexpr int kMlaSegTokens = 256;  // MLA: work charged for each sequence a slice starts, in tokens
 
 struct Plan {
     int workers;
@@ -40,6 +41,7 @@ struct Plan {
     size_t lds;   // dynamic LDS per workgroup (sibling waves' K buffers)
     int groups;   // workgroups per worker (MLA row groups), else 1
     int lanes;    // work lists (KernelParams::lanes)
+    int seg_cost; // KernelParams::seg_cost
     int64_t grid;
     KernelFn main;
     size_t flag_bytes, zero_bytes, part_ml_bytes, part_o_bytes;
@@ -195,6 +197,13 @@ Plan make_plan(const SimplerHipPaDecodeArgs *a, const KernelPair &k) {  // k: th
             p.workers = wgs / p.groups > 0 ? wgs / p.groups : 1;
         }
         p.grid = (int64_t)p.workers * p.groups;
+        // A slice that starts another sequence pays for its set-up: 147 KB of
+        // query rows, a first block fetched without prefetch and a 256 KB
+        // partial or output store, about 23 us per extra sequence on cfg4
+        // (per-workgroup timestamps: 228 / 252 / 275 us for slices of one,
+        // two and three sequences with equal blocks), so each sequence is
+        // charged kMlaSegTokens tokens of work ahead of its blocks.
+        p.seg_cost = (kMlaSegTokens + a->block_size - 1) / a->block_size;
     } else {
         // Row tiles of one kv head run as sibling waves of one worker workgroup
         // (up to four), so K/V of a block is fetched once for all of them;
@@ -371,6 +380,7 @@ int pa_decode_launch(const SimplerHipPaDecodeArgs *a, void *workspace, size_t wo
     P.num_pool_blocks = a->num_blocks;
     P.workers = plan.workers;
     P.lanes = plan.lanes;
+    P.seg_cost = plan.seg_cost;
     P.scale = a->scale;
     P.causal = (a->causal && a->q_len > 1) ? 1 : 0;
     P.k_scale = a->k_scale;

@@ -120,6 +120,11 @@ struct KernelParams {
     float scale;
     int32_t causal;
     unsigned *err_mirror;  // host-visible copy of *error_flag written by the merge kernel, or null
+    // Work units charged at the start of each work-list tile ahead of its
+    // blocks (0: a slice's work is its block count). A slice that starts
+    // further tiles pays for each one's set-up (query rows, first fill,
+    // partial or output stores) in blocks it does not get.
+    int32_t seg_cost;
     // fused KV append: the q_len new tokens of each sequence (its positions
     // len-q_len .. len-1), [batch, q_len, kv_heads, Dk] and [.., Dv]; v_new is
     // null for MLA (V is a prefix of K). Null when not appending.
@@ -338,9 +343,9 @@ __device__ __forceinline__ int list_of_tile(const KernelParams &P, int g, int b)
     return ((g - b) % P.lanes + P.lanes) % P.lanes;
 }
 
-// Wave-level scan over the batch for one list. Work of batch b = blocks_of(b)
-// * lane_tiles. Returns the total work; if `want_b` >= 0, *prefix_of_want = work
-// before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
+// Wave-level scan over the batch for one list. Work of batch b = (blocks_of(b)
+// + seg_cost) * lane_tiles, or 0 for an empty context. Returns the total
+// work; if `want_b` >= 0, *prefix_of_want = work before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
 // *prefix_of_pos = the batch whose work range contains pos and the work before
 // it. `pos` may be given as a fraction of the total (pos_num / pos_den of it,
 // rounded up to whole chunks) so that one pass suffices. All results are
@@ -352,7 +357,8 @@ __device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_o
     int carry = 0;
     for (int base = 0; base < P.batch; base += 64) {
         const int b = base + lane;
-        const int cnt = b < P.batch ? blocks_of(P, b) * tpb : 0;
+        const int nbb = b < P.batch ? blocks_of(P, b) : 0;
+        const int cnt = nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
         int incl = cnt;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -390,7 +396,8 @@ __device__ inline int locate_slice(const KernelParams &P, int c, int *start, int
         return total;
     }
     const int tpb = lane_tiles(P);
-    const int cnt = lane < P.batch ? blocks_of(P, lane) * tpb : 0;
+    const int nbl = lane < P.batch ? blocks_of(P, lane) : 0;
+    const int cnt = nbl > 0 ? (nbl + P.seg_cost) * tpb : 0;
     int incl = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -1464,8 +1471,9 @@ __global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const Ker
     }
     const int per_list = max(P.workers / P.lanes, 1);
     const int chunk = (total + per_list - 1) / per_list;
-    const int t0 = prefix + j * nb;
-    const int w_first = t0 / chunk, w_last = (t0 + nb - 1) / chunk;  // slices of the list
+    const int t0 = prefix + j * (nb + P.seg_cost);  // the tile's first work unit
+    const int tb = t0 + P.seg_cost;                 // its first block's
+    const int w_first = tb / chunk, w_last = (tb + nb - 1) / chunk;  // slices of the list
     if (w_first == w_last) return;  // a tile inside one slice is finished by the main kernel
     // Log-sum-exp over the pieces: the row max and total l from the (m, l)
     // pairs first, then O = sum_w e^{m_w - M} O_w / L, whose piece loads do not
@@ -2092,25 +2100,28 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     if (start >= end) return;
     int nb = blocks_of(P, b);
     if (nb == 0) return;
-    const int rel = start - prefix;
-    int kvh = rel / nb;
-    int blk = rel - kvh * nb;
-    int pos = start;
+    // Work units: each (batch, kv head) tile takes seg_cost units, then one
+    // per block. The slice [start, end) runs the blocks whose units it holds.
+    const int span = nb + P.seg_cost;
+    int kvh = (start - prefix) / span;
+    int t0 = prefix + kvh * span;  // the tile's first unit
     int slot = 0;
-    while (pos < end && nb > 0) {
-        const int seg = min(end - pos, nb - blk);
-        run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk, blk + seg, slot, smem0,
-                                                  smem1, sink);
-        pos += seg;
-        slot = 1;
-        if (pos >= end) break;
-        blk = 0;
+    while (nb > 0) {
+        const int blk0 = max(0, start - t0 - P.seg_cost), blk1 = min(nb, end - t0 - P.seg_cost);
+        if (blk1 > blk0) {
+            run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk0, blk1, slot, smem0, smem1,
+                                              sink);
+            slot = 1;
+        }
+        t0 += nb + P.seg_cost;
+        if (t0 >= end) break;
         if (++kvh == tpb) {
             kvh = 0;
             do {
                 ++b;
                 nb = blocks_of(P, b);
             } while (nb == 0 && b + 1 < P.batch);
+            if (nb == 0) break;
         }
     }
 }
