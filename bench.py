@@ -8,7 +8,11 @@ value = algorithmic KV-read GB/s (K+V of valid tokens + Q + out + tables,
 divided by the kernel time), plus µs/step, the roofline of the kernel and the
 CPU baseline (the C restatement of the reference kernels, timed on the host).
 
-    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--no-other-configs]
+
+The default run also times every other config (cfg1, cfg3-5, cfg2_fp8 and the
+reference's unroll Case1) on the GPU, and reports their main-kernel µs, HBM
+fraction and step µs under "other_configs".
 
 Only one GPU is used; --gpus N with N > 1 exits with a message.
 """
@@ -49,6 +53,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--workers", type=int, default=0, help="worker wavefronts; 0 = one per wave slot")
     p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-other-configs", action="store_true",
+                   help="default config only: skip timing the other configs in the same run")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample duration")
     p.add_argument("--cpu-threads", type=int, default=0,
                    help="0 = every CPU this process may use, capped at OMP_NUM_THREADS when set (the box's share)")
@@ -58,6 +64,82 @@ def parse() -> argparse.Namespace:
                    help="before the timed region, run 3 device copies of this many MiB (a kernel of known "
                         "traffic that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE in the same run)")
     return p.parse_args()
+
+
+def time_decode(case, out, num_workers: int, dev, steps: int, warmup: int) -> dict:
+    """Time one decode config on device-resident inputs: `steps` back-to-back
+    calls between two events on the launch stream (the step: main + merge
+    kernels), then the main kernel alone, with events around each main launch
+    (its merge kernel still runs after it, outside the events)."""
+    import torch
+
+    from simpler_amd import paged_attention as pa
+
+    cfg = case.config
+    pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
+                         case.scale, causal=cfg.causal, num_workers=num_workers, k_scale=case.k_scale,
+                         v_scale=case.v_scale)
+    stream = torch.cuda.current_stream(dev)
+    print(f"[bench] {cfg.name}: warmup {warmup}", file=sys.stderr, flush=True)
+    for _ in range(warmup):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    pa.check_errors(dev)
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        pa.launch(pargs, dev, stream.cuda_stream)
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    step_ms = start.elapsed_time(end) / steps
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)  # one untimed split step first
+    pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
+    torch.cuda.synchronize(dev)
+    for e0, e1 in evs:
+        e0.record(stream)
+        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)
+        e1.record(stream)
+        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
+    torch.cuda.synchronize(dev)
+    pa.check_errors(dev)
+    main_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / steps
+    print(f"[bench] {cfg.name}: {step_ms * 1e3:.1f} us/step, main kernel {main_ms * 1e3:.1f} us, "
+          f"wall {wall:.3f} s", file=sys.stderr, flush=True)
+    return {"step_ms": step_ms, "main_ms": main_ms, "wall_s": wall, "workers": pa.plan(pargs),
+            "kernel": pa.kernel_name(pargs)}
+
+
+def other_configs(args, dev, skip: str) -> dict:
+    """Every other benchmark config, timed in this same run (fewer steps, no CPU
+    baseline): main-kernel µs and its fraction of HBM peak, and the step µs."""
+    import torch
+
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, make_case
+
+    res = {}
+    steps, warmup = max(1, min(args.steps, 50)), max(1, min(args.warmup, 5))
+    out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
+    for name in CONFIGS:
+        if name == skip:
+            continue
+        case_cpu = make_case(name)
+        case = case_cpu.to(dev)
+        out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
+        tm = time_decode(case, out, args.workers, dev, steps, warmup)
+        nbytes = algorithmic_bytes(case_cpu, out_bytes=2 if out_dtype == torch.bfloat16 else 4)
+        res[name] = {"kernel": tm["kernel"], "workers": tm["workers"], "main_us": round(tm["main_ms"] * 1e3, 2),
+                     "frac": round(nbytes / (tm["main_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "step_us": round(tm["step_ms"] * 1e3, 2),
+                     "step_frac": round(nbytes / (tm["step_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": nbytes, "steps": steps}
+        del case, out
+        torch.cuda.empty_cache()
+    return res
 
 
 def api_time(case, out, cfg, steps: int, warmup: int) -> dict | None:
@@ -502,6 +584,9 @@ def bench_taskgraph(args) -> int:
     nbytes = algorithmic_bytes(case_cpu, out_bytes=2 if args.out_dtype == "bf16" else 4)
     gbs = nbytes / (ms * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
+    others = None
+    if cfg.name == DEFAULT_CONFIG and not args.no_other_configs:
+        others = other_configs(args, dev, skip=cfg.name)
     line = {
         "metric": f"{METRIC} [{cfg.name}, task graph {args.tg_mode}]",
         "value": round(gbs, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -539,7 +624,6 @@ def main() -> int:
 
     import torch
 
-    from simpler_amd import paged_attention as pa
     from simpler_amd.workloads import CONFIGS, algorithmic_bytes, algorithmic_flops, kv_bytes, make_case
 
     if not torch.cuda.is_available():
@@ -552,12 +636,6 @@ def main() -> int:
     case = case_cpu.to(dev)
     out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
     out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
-    pargs = pa.make_args(case.query, case.key_cache, case.value_cache, case.block_table, case.context_lens, out,
-                         case.scale, causal=cfg.causal, num_workers=args.workers, k_scale=case.k_scale,
-                         v_scale=case.v_scale)
-    workers = pa.plan(pargs)
-    kernel_name = pa.kernel_name(pargs)
-    stream = torch.cuda.current_stream(dev)
 
     if args.calibrate_copy_mib > 0:
         src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
@@ -567,40 +645,9 @@ def main() -> int:
         torch.cuda.synchronize(dev)
         del src, dst
 
-    print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        pa.launch(pargs, dev, stream.cuda_stream)
-    torch.cuda.synchronize(dev)
-    pa.check_errors(dev)
-
-    # timed region: K back-to-back launches on the stream the kernel runs on
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        pa.launch(pargs, dev, stream.cuda_stream)
-    end.record(stream)
-    torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
-    kernel_ms = start.elapsed_time(end) / args.steps
-    print(f"[bench] timed {args.steps} steps: {kernel_ms * 1e3:.1f} us/step (events), wall {wall:.3f} s",
-          file=sys.stderr, flush=True)
-
-    # The dominant kernel alone, for the roofline: events around each main
-    # launch (the merge kernel still runs after it, outside the events).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)  # one untimed split step first
-    pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
-    torch.cuda.synchronize(dev)
-    for e0, e1 in evs:
-        e0.record(stream)
-        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)
-        e1.record(stream)
-        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
-    torch.cuda.synchronize(dev)
-    main_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / args.steps
-    print(f"[bench] main kernel alone: {main_ms * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    tm = time_decode(case, out, args.workers, dev, args.steps, args.warmup)
+    workers, kernel_name = tm["workers"], tm["kernel"]
+    kernel_ms, main_ms, wall = tm["step_ms"], tm["main_ms"], tm["wall_s"]
 
     out_bytes = 2 if out_dtype == torch.bfloat16 else 4
     nbytes = algorithmic_bytes(case_cpu, out_bytes=out_bytes)
@@ -622,6 +669,9 @@ def main() -> int:
         print(f"[bench] API timing skipped: {exc}", file=sys.stderr, flush=True)
         api = None
     cpu = None if args.no_cpu_baseline else cpu_baseline(case_cpu, args)
+    others = None
+    if cfg.name == DEFAULT_CONFIG and not args.no_other_configs:
+        others = other_configs(args, dev, skip=cfg.name)
     line = {
         "metric": METRIC if cfg.name == DEFAULT_CONFIG else f"{METRIC} [{cfg.name}]",
         "value": round(gbs, 2),
@@ -669,6 +719,7 @@ def main() -> int:
         },
         "api": api,
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -180,12 +180,17 @@ int simpler_hip_pa_decode_noalloc(const SimplerHipPaDecodeArgs *args, void *stre
  * by simpler_hip_pa_decode. q_len <= 16; bf16 and fp16 caches (not fp8).
  * The append is fused into the decode's two launches where each worker runs
  * one row tile; where the decode gives a worker several row tiles (GQA with
- * more than 16 query rows per kv head), it runs as a launch of its own ahead
- * of them, which measured faster there.
+ * more than 16 query rows per kv head) and for MLA, it runs as a launch of
+ * its own ahead of them, which measured faster there. Both forms leave the
+ * same cache contents.
  * Same workspace as simpler_hip_pa_decode for these args. A length below
- * q_len is reported by simpler_hip_pa_decode_check as BAD_LENGTH (only the
- * new tokens at positions >= 0 are then written); new tokens in out-of-pool
- * blocks are neither read nor written (BAD_BLOCK).
+ * q_len or above max_blocks_per_seq*block_size is reported by
+ * simpler_hip_pa_decode_check as BAD_LENGTH: the new tokens are still placed
+ * by the raw length, only those at positions in
+ * [0, max_blocks_per_seq*block_size) are written (the others are dropped and
+ * no other cache row changes), and the decode attends over the length clamped
+ * into that range. New tokens in out-of-pool blocks are neither read nor
+ * written (BAD_BLOCK).
  */
 int simpler_hip_pa_decode_append(const SimplerHipPaDecodeArgs *args, const void *key_new, const void *value_new,
                                  void *workspace, size_t workspace_bytes, void *stream);

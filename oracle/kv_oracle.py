@@ -49,11 +49,15 @@ def new_token_slots(block_table: np.ndarray, seq_lens: np.ndarray, block_size: i
     """Slots ``[B, n_new]`` of each sequence's last ``n_new`` positions
     ``seq_len - n_new .. seq_len - 1``, derived as the reference derives the
     current token's (goldens/qwen3_14b_decode.py:106-115; ``n_new = 1`` is
-    ``slot_of``); positions below 0 get slot -1 (skipped by ``kv_append``)."""
+    ``slot_of``); positions below 0, or past what the table row holds
+    (``block_table.shape[1] * block_size`` and up), get slot -1 (skipped by
+    ``kv_append``)."""
     pos = seq_lens.astype(np.int64)[:, None] - n_new + np.arange(n_new, dtype=np.int64)[None, :]
+    cap = block_table.shape[1] * block_size
     rows = np.arange(len(seq_lens))[:, None]
-    phys = block_table[rows, np.maximum(pos, 0) // block_size].astype(np.int64)
-    return np.where(pos >= 0, phys * block_size + pos % block_size, -1).astype(np.int32)
+    phys = block_table[rows, np.clip(pos, 0, max(cap - 1, 0)) // block_size].astype(np.int64)
+    ok = (pos >= 0) & (pos < cap)
+    return np.where(ok, phys * block_size + pos % block_size, -1).astype(np.int32)
 
 
 def kv_append(key_cache: np.ndarray, value_cache: np.ndarray | None, key: np.ndarray, value: np.ndarray | None,

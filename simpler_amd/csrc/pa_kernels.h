@@ -503,7 +503,8 @@ __device__ __forceinline__ void finish_segment(const KernelParams &P, const int 
 }
 
 // Fused KV append. The q_len (<= 16) new tokens of sequence b are its
-// positions ctx-q_len .. ctx-1. They are consecutive, so each residue of a
+// positions len-q_len .. len-1 (len = context_lens[b]; ctx = len once it is
+// in range). They are consecutive, so each residue of a
 // position mod 16 belongs to one new token at most, and a lane, whose K and V
 // operands always hold the same residues (register K: token pc of every
 // 16-token tile; V and row-staged K: tokens 4qd+e), needs the rows of at most
@@ -576,8 +577,10 @@ __device__ __forceinline__ void unpipelined_blocks(const KernelParams &P, const 
     };
 
     // fused append: register-K rows of the new token at residue pc, V rows of
-    // those at residues 4qd+e
-    const int new0 = ctx - P.q_len;
+    // those at residues 4qd+e. The new tokens sit at the raw length's last
+    // q_len positions; those at or past the clamped ctx are not in the table
+    // and are dropped (new_token_at), as the routed append drops them.
+    const int new0 = max(P.context_lens[b], 0) - P.q_len;
     int pk = -1, pe[4] = {-1, -1, -1, -1};
     u32x4_t knew[APPEND ? KS : 1], vnew[APPEND ? 4 : 1][DVS];
     if constexpr (APPEND) {

@@ -439,7 +439,7 @@ def plan(args: _lib.PaDecodeArgs) -> int:
     """Number of workers (work-list slices) a launch with ``args`` uses on the current device.
 
     A worker is one workgroup for the decode kernel and one slice run by
-    ceil(rows / 64) sibling workgroups for the MLA kernel.
+    ceil(rows / 128) sibling workgroups for the MLA kernel.
     """
     n = ctypes.c_int32()
     rc = _lib.lib().simpler_hip_pa_decode_plan(ctypes.byref(args), ctypes.byref(n))

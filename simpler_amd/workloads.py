@@ -9,7 +9,9 @@ configs specify: context lengths, then the block table, then Q, K, V, each
 value N(0, 1) in fp32 rounded to bf16.
 
 Config names map to the five benchmark configurations (index = position):
-``cfg1_small``, ``cfg2_qwen3_8b``, ``cfg3_long``, ``cfg4_mla``, ``cfg5_verify``.
+``cfg1_small``, ``cfg2_qwen3_8b``, ``cfg3_long``, ``cfg4_mla``, ``cfg5_verify``;
+``cfg2_fp8`` is cfg2's draws with fp8 caches and ``ref_unroll_case1`` the
+reference's own paged_attention_unroll Case1 shape.
 """
 
 from __future__ import annotations
@@ -67,6 +69,11 @@ CONFIGS: dict[str, DecodeConfig] = {
         DecodeConfig("cfg2_fp8", 1, 32, 32, 8, 128, 128, 128, 1024, 8192, kv_format="fp8",
                      description="Qwen3-8B GQA decode, fp8 E4M3FN KV with per-(block, kv head) scales: B=32, Hq=32, "
                                  "Hkv=8, D=128, BS=128, L~U[1024,8192]"),
+        # the reference's paged_attention_unroll Case1 (test_paged_attention_unroll.py:63-76); block ids drawn
+        # without sharing (every sequence reads its own blocks), table width max_model_len / BS = 256
+        DecodeConfig("ref_unroll_case1", 5, 256, 16, 1, 128, 128, 128, 8192, 8192, max_blocks=256,
+                     description="reference unroll Case1: B=256, Hq=16, Hkv=1, D=128, BS=128, L=8192, "
+                                 "max_model_len 32768"),
     ]
 }
 

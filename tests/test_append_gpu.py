@@ -14,8 +14,10 @@ on caches whose new-token rows hold NaN, and checks:
 
 Shapes cover each kernel path: K staged through LDS (D = 128, one row tile),
 K in registers (D = 64), blocks larger than the registers (BS = 128,
-D = 256), sibling row-tile waves (causal q_len 8), fp16, MLA (576/512, two
-64-row groups), several worker counts, new tokens across a block boundary.
+D = 256); with the append as a launch of its own ahead of the decode: two row
+tiles in one wave (D = 128, causal q_len 8), sibling row-tile waves (D = 64,
+two row tiles), MLA (576/512, one 128-row workgroup); fp16, several worker
+counts, new tokens across a block boundary, lengths past the table row.
 """
 
 from __future__ import annotations
@@ -96,12 +98,15 @@ CASES = {
     # blocks larger than the registers
     "gqa_bs128_d256": dict(batch=3, num_heads=16, kv_heads=2, head_dim=256, block_size=128,
                            context_lens=[1, 1000, 2049]),
-    # sibling row-tile waves; new tokens 122..129 straddle blocks 0 and 1
+    # two row tiles in one wave (the append as its own launch); new tokens 122..129 straddle blocks 0 and 1
     "verify_q8": dict(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, q_len=8, causal=True,
                       context_lens=[8, 130, 2000]),
     # 16 new tokens, one row tile per kv head, straddling 16-token blocks
     "verify_q16": dict(batch=2, num_heads=2, kv_heads=2, head_dim=64, block_size=16, q_len=16, causal=True,
                        context_lens=[16, 40]),
+    # sibling row-tile waves (D = 64: two row tiles of 4 heads x 8 tokens), the append as its own launch
+    "multi_d64_q8": dict(batch=3, num_heads=32, kv_heads=8, head_dim=64, block_size=16, q_len=8, causal=True,
+                         context_lens=[8, 20, 700]),
     "fp16_d128": dict(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128, context_lens=[5, 129, 900],
                       dtype=torch.float16),
     # fp16, two row tiles per kv head: the append's own launch ahead of the decode
@@ -208,6 +213,55 @@ def test_append_of_two_row_tiles_length_shorter_than_the_new_tokens_is_reported(
     pa.check_errors(device)
 
 
+OVERLONG = {
+    # one row tile per worker: the append fused into the decode's launches
+    "fused_one_tile": dict(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128, q_len=4, causal=True,
+                           context_lens=[300, 50]),
+    # two row tiles per worker: the append's own launch ahead of the decode
+    "routed_two_tiles": dict(batch=2, num_heads=32, kv_heads=8, head_dim=128, block_size=128, q_len=8,
+                             causal=True, context_lens=[300, 50]),
+    "mla": dict(batch=2, num_heads=16, kv_heads=1, head_dim=576, head_dim_v=512, block_size=32, mla=True, q_len=4,
+                causal=True, context_lens=[40, 10]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(OVERLONG))
+def test_append_length_past_the_table_row_writes_only_in_table_positions(name, device):
+    # The first sequence's length is one past what its table row holds (cap =
+    # max_blocks * block_size). Its new tokens keep the positions the raw length
+    # gives (len - q_len + j); those at cap and up are dropped, no other row
+    # changes, BAD_LENGTH is reported, and the decode attends over cap tokens.
+    print(f"[case] append length cap+1 {name}", flush=True)
+    seed = 990 + sorted(OVERLONG).index(name)
+    case = make_custom_case(seed=seed, **OVERLONG[name])
+    c = case.config
+    cap = c.max_blocks * c.block_size
+    k_new, v_new = new_tokens(case, seed + 1)
+    raw = case.context_lens.clone()
+    raw[0] = cap + 1
+    over = DecodeCase(c, case.seed, case.query, case.key_cache, case.value_cache, case.block_table, raw, case.scale)
+    want = oracle_appended(over, k_new, v_new)  # slots at cap and up are -1: skipped
+    assert (u16(want.key_cache) != u16(case.key_cache)).any(axis=(2, 3)).sum() == (c.q_len - 1) + c.q_len
+    d = over.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode_append(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens,
+                                     k_new.to(device), None if v_new is None else v_new.to(device), out,
+                                     case.scale, causal=c.causal)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    np.testing.assert_array_equal(u16(d.key_cache.cpu()), u16(want.key_cache))
+    if not c.mla:
+        np.testing.assert_array_equal(u16(d.value_cache.cpu()), u16(want.value_cache))
+    # the output: the plain decode of the appended caches at the clamped length
+    clamped = raw.clone()
+    clamped[0] = cap
+    plain, _, _ = run_decode(DecodeCase(c, case.seed, case.query, want.key_cache, want.value_cache,
+                                        case.block_table, clamped, case.scale), device)
+    np.testing.assert_array_equal(out.cpu().numpy(), plain)
+
+
 @pytest.mark.parametrize("name", ["gqa_d128", "verify_q8", "mla_q1"])
 def test_fused_append_replays_from_a_hip_graph(name, device):
     # The fused append allocates nothing once its workspace is sized, so a
@@ -255,4 +309,5 @@ def test_fused_append_replays_from_a_hip_graph(name, device):
         if not case.config.mla:
             np.testing.assert_array_equal(u16(d.value_cache.cpu()), u16(wants[k].value_cache))
         np.testing.assert_array_equal(out.cpu().numpy(), plains[k])
-    pa.check_errors(device)
+    with torch.cuda.stream(side):  # the replays ran on the capture stream, whose workspace holds their flags
+        pa.check_errors(device)

@@ -32,7 +32,8 @@ def test_default_line_carries_the_contract(device, capsys, monkeypatch):
     sys.path.insert(0, str(ROOT))
     import bench
 
-    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "5", "--warmup", "2", "--cpu-seconds", "1"])
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "5", "--warmup", "2", "--cpu-seconds", "1",
+                                      "--no-other-configs"])
     assert bench.main() == 0
     out = capsys.readouterr().out
     lines = [l for l in out.splitlines() if l.startswith("{")]
@@ -52,3 +53,21 @@ def test_default_line_carries_the_contract(device, capsys, monkeypatch):
     assert 0 < line["value"] <= 1.05 * roof["achieved"]
     cpu = line["cpu_baseline"]
     assert cpu["kind"] in ("port", "reference") and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
+
+
+@pytest.mark.gpu
+def test_other_configs_are_timed_in_the_same_run(device, monkeypatch):
+    # the default run's "other_configs" figures, on two small configs
+    print("[case] bench.other_configs on cfg1_small + cfg5_verify", flush=True)
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from simpler_amd import workloads
+
+    keep = {k: workloads.CONFIGS[k] for k in ("cfg1_small", "cfg2_qwen3_8b", "cfg5_verify")}
+    monkeypatch.setattr(workloads, "CONFIGS", keep)
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "3", "--warmup", "1"])
+    res = bench.other_configs(bench.parse(), device, skip="cfg2_qwen3_8b")
+    assert sorted(res) == ["cfg1_small", "cfg5_verify"]
+    for r in res.values():
+        assert r["main_us"] > 0 and r["step_us"] >= 0.9 * r["main_us"] and 0 < r["frac"] < 1
+        assert r["kernel"].startswith("pa_") and r["workers"] >= 1

@@ -45,6 +45,18 @@ def test_new_token_slots_extend_the_reference_slot():
     assert got[3, 0] == shuffled[3, 0] * 128 + 127 and got[3, 1] == shuffled[3, 1] * 128
 
 
+def test_new_token_slots_past_the_table_row_are_dropped():
+    # a row of 3 blocks of 16 holds positions 0..47: a length of 50 with 4 new
+    # tokens puts them at 46..49, of which 46 and 47 fit
+    table = np.array([[5, 2, 9], [1, 0, 4]], dtype=np.int32)
+    got = ko.new_token_slots(table, np.array([50, 48], dtype=np.int32), 16, 4)
+    np.testing.assert_array_equal(got[0], [9 * 16 + 14, 9 * 16 + 15, -1, -1])
+    np.testing.assert_array_equal(got[1], [4 * 16 + 12, 4 * 16 + 13, 4 * 16 + 14, 4 * 16 + 15])
+    # far past the row: nothing fits
+    np.testing.assert_array_equal(ko.new_token_slots(table, np.array([10_000, 1], dtype=np.int32), 16, 2)[0],
+                                  [-1, -1])
+
+
 def test_append_writes_exactly_the_slots():
     rng = np.random.default_rng(1)
     nblk, bs, hkv, d = 12, 16, 3, 8

@@ -213,7 +213,7 @@ def test_out_of_pool_block_is_reported_not_read(device):
     pa.check_errors(device)  # cleared
 
 
-@pytest.mark.parametrize("name", ["cfg1_small", "cfg2_qwen3_8b", "cfg5_verify"])
+@pytest.mark.parametrize("name", ["cfg1_small", "cfg2_qwen3_8b", "cfg5_verify", "ref_unroll_case1"])
 def test_benchmark_configs_full_size(name, device):
     print(f"[case] {name} full size", flush=True)
     case = make_case(name)
