@@ -116,6 +116,48 @@ void simpler_hip_tg_destroy(SimplerHipTaskGraph *g);
  * to a built-in kernel. Unbound ids are rejected at submit. */
 int simpler_hip_tg_bind(SimplerHipTaskGraph *g, int32_t func_id, int32_t kernel);
 
+/* ---- Kernels of the caller's own ----
+ * A registered kernel is a gfx950 `extern "C" __global__` function in a code
+ * object file (hipcc --genco), taking one by-value SimplerHipKernelArgs: the
+ * task's tensors in submission order as the kernel sees them (OUTPUT tensors
+ * materialised by the runtime), then its scalars. This is the reference's
+ * incore entry convention, `kernel_entry(int64_t *args)` with the task's
+ * ChipTensors first and its scalars after them
+ * (examples/a2a3/tensormap_and_ringbuffer/vector_example/kernels/aiv/kernel_add.cpp:49-55),
+ * as one HIP kernel argument instead of a pointer to a device-side array. */
+#define SIMPLER_HIP_TG_KERNEL_MAX_TENSORS SIMPLER_CORE_MAX_TENSOR_ARGS
+
+typedef struct SimplerHipKernelTensor {
+    uint64_t addr;   /* device address of the view's first element (buffer.addr + start_offset * element size) */
+    uint32_t ndims;
+    uint32_t dtype;  /* SimplerDataType */
+    uint32_t shapes[SIMPLER_MAX_TENSOR_DIMS];
+    uint32_t strides[SIMPLER_MAX_TENSOR_DIMS]; /* elements */
+} SimplerHipKernelTensor;
+
+typedef struct SimplerHipKernelArgs {
+    int32_t n_tensors;
+    int32_t n_scalars;
+    SimplerHipKernelTensor tensors[SIMPLER_HIP_TG_KERNEL_MAX_TENSORS];
+    uint64_t scalars[SIMPLER_CORE_MAX_SCALAR_ARGS];
+} SimplerHipKernelArgs;
+
+/* Bind func_id to kernel `kernel_name` of the code object at
+ * `code_object_path` (loaded once per path and graph, on the graph's device).
+ * Replaces the reference's per-callable child binaries resolved at
+ * registration (src/common/task_interface/callable.h:99-163) and dispatched
+ * by func id from rt_submit_task (orchestration/pto_orchestration_api.h:170-194).
+ * Launch shape of each task: `block_threads` threads per workgroup (1..1024);
+ * grid = ceil(numel(tensor `grid_tensor`) / elems_per_workgroup) workgroups
+ * (at least 1), or exactly elems_per_workgroup workgroups when grid_tensor < 0.
+ * Tasks may pass any tensors of device memory (at most
+ * SIMPLER_HIP_TG_KERNEL_MAX_TENSORS) and scalars; checking their shapes is the
+ * kernel's business. Returns SIMPLER_HIP_ERR_INVALID for a bad argument and
+ * SIMPLER_HIP_ERR_UNSUPPORTED when the file or kernel cannot be loaded. */
+int simpler_hip_tg_register_kernel(SimplerHipTaskGraph *g, int32_t func_id, const char *code_object_path,
+                                   const char *kernel_name, uint32_t block_threads, int32_t grid_tensor,
+                                   uint32_t elems_per_workgroup);
+
 int simpler_hip_tg_scope_begin(SimplerHipTaskGraph *g);
 int simpler_hip_tg_scope_end(SimplerHipTaskGraph *g);
 
@@ -156,6 +198,29 @@ int simpler_hip_tg_wait(SimplerHipTaskGraph *g);
  * Bindings and the instantiated graph (for update on the next launch) stay. */
 int simpler_hip_tg_reset(SimplerHipTaskGraph *g);
 
+/* ---- Whole-step replay (GRAPH mode) ----
+ * A step orchestrated from a reset graph is a function of what its
+ * orchestration reads: the tensors it is given, its scalars, and the values it
+ * reads with get_tensor_data. The caller names those in `key`.
+ *   record_replay  after the step's tasks are submitted and before its launch:
+ *                  keep the graph's state under `key` (one key per graph; a
+ *                  new record replaces the old one). The step must have started
+ *                  on a reset (or new) graph, possibly inside open scopes that
+ *                  held nothing yet, and nothing may have been launched since;
+ *                  `key` must determine every task submitted since the reset.
+ *   replay         on a reset graph (the same depth of open, empty scopes as
+ *                  at the recorded step's start): if `key` equals the recorded
+ *                  one, restore that state (tasks, dependencies, allocations,
+ *                  scopes) and return 1; simpler_hip_tg_launch then runs the
+ *                  cached executable graph without any task being submitted
+ *                  again. Otherwise return 0 and change nothing.
+ * No counterpart in the reference, whose orchestration runs on the device
+ * each step; here it runs on the host, and a decode loop re-submits the same
+ * DAG every step. EAGER and RECORD_ONLY graphs never replay (replay returns 0,
+ * record_replay does nothing). */
+int simpler_hip_tg_record_replay(SimplerHipTaskGraph *g, const void *key, uint64_t key_bytes);
+int simpler_hip_tg_replay(SimplerHipTaskGraph *g, const void *key, uint64_t key_bytes);
+
 /* Orchestrations of the reference's examples, run against graph `g` (which
  * gets its func ids bound). Tensors are in the callable's order; kernel
  * operands must be device memory, tables read only through get_tensor_data
@@ -166,15 +231,21 @@ int simpler_hip_tg_reset(SimplerHipTaskGraph *g);
  *                       context_lens [B] i32, out [B,Hq,D] f32 or bf16; scale as f32 bits.
  *                       Per (sequence, 128-head tile) and KV block: QK -> SF -> PV -> UP.
  *   vector example   <- examples/a2a3/tensormap_and_ringbuffer/vector_example/kernels/orchestration/
- *                       example_orchestration.cpp:55-112: a, b, f fp32 [n]; f = (a+b+1)*(a+b+2) + (a+b). */
+ *                       example_orchestration.cpp:55-112: a, b, f fp32 [n]; f = (a+b+1)*(a+b+2) + (a+b).
+ * In GRAPH mode on a reset graph, both record their step for replay, keyed on
+ * the tensors, the scale and (paged attention) every context_lens and
+ * block_table value they read: a repeated step with the same tables replays
+ * its cached graph without being orchestrated again. */
 int simpler_hip_tg_orchestrate_paged_attention(SimplerHipTaskGraph *g, const SimplerChipTensor *tensors,
                                                uint64_t scale_bits);
 int simpler_hip_tg_orchestrate_vector_example(SimplerHipTaskGraph *g, const SimplerChipTensor *tensors);
 
-/* Inspection: number of tasks; the producers task `task` waits on (sorted,
- * at most cap written; returns the full count); bytes of device memory the
- * graph holds for runtime-allocated tensors. */
+/* Inspection: number of tasks; the steps replayed so far; the producers task
+ * `task` waits on (sorted, at most cap written; returns the full count); bytes
+ * of device memory the graph holds for runtime-allocated tensors. */
 int64_t simpler_hip_tg_task_count(const SimplerHipTaskGraph *g);
+/* Steps restored by simpler_hip_tg_replay over the graph's lifetime. */
+uint64_t simpler_hip_tg_replay_count(const SimplerHipTaskGraph *g);
 int32_t simpler_hip_tg_fanin(const SimplerHipTaskGraph *g, int64_t task, int64_t *producers, int32_t cap);
 uint64_t simpler_hip_tg_arena_bytes(const SimplerHipTaskGraph *g);
 

@@ -181,6 +181,9 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_tg_create": (_VP, [_I32, _VP]),
     "simpler_hip_tg_destroy": (None, [_VP]),
     "simpler_hip_tg_bind": (_I, [_VP, _I32, _I32]),
+    "simpler_hip_tg_register_kernel": (_I, [_VP, _I32, ctypes.c_char_p, ctypes.c_char_p, _U32, _I32, _U32]),
+    "simpler_hip_tg_record_replay": (_I, [_VP, _VP, _U64]),
+    "simpler_hip_tg_replay": (_I, [_VP, _VP, _U64]),
     "simpler_hip_tg_scope_begin": (_I, [_VP]),
     "simpler_hip_tg_scope_end": (_I, [_VP]),
     "simpler_hip_tg_submit": (ctypes.c_int64, [_VP, _I32, _VP, ctypes.POINTER(_I32), _I32, ctypes.POINTER(_U64),
@@ -194,6 +197,7 @@ SIGNATURES: dict[str, tuple] = {
     "simpler_hip_tg_orchestrate_paged_attention": (_I, [_VP, _VP, _U64]),
     "simpler_hip_tg_orchestrate_vector_example": (_I, [_VP, _VP]),
     "simpler_hip_tg_task_count": (ctypes.c_int64, [_VP]),
+    "simpler_hip_tg_replay_count": (_U64, [_VP]),
     "simpler_hip_tg_fanin": (_I32, [_VP, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _I32]),
     "simpler_hip_tg_arena_bytes": (_U64, [_VP]),
 }

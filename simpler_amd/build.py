@@ -97,5 +97,20 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, jobs: int
     return LIB_PATH
 
 
+def build_code_object(src: Path | str, out: Path | str, verbose: bool = False,
+                      extra_flags: list[str] | None = None) -> Path:
+    """Compile one ``.hip`` file to a gfx950 code object (``hipcc --genco``) for
+    ``simpler_hip_tg_register_kernel``: kernels declared ``extern "C"
+    __global__`` taking one ``SimplerHipKernelArgs``."""
+    src, out = Path(src), Path(out)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
+    _run([hipcc(), "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{ROOT / 'include'}",
+          "-Wno-unused-command-line-argument", *(extra_flags or []), str(src), "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

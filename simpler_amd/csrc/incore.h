@@ -12,11 +12,13 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "simpler_hip/abi_types.h"
 
 namespace simpler_hip {
 
-constexpr size_t kMaxKernelParamBytes = 256;
+constexpr size_t kMaxKernelParamBytes = 256;  // built-in kernels' parameter blocks
 
 struct KernelLaunch {
     const void *func = nullptr;  // __global__ function
@@ -24,6 +26,8 @@ struct KernelLaunch {
     dim3 block{64, 1, 1};
     size_t param_bytes = 0;
     alignas(16) unsigned char params[kMaxKernelParamBytes] = {};
+    std::vector<unsigned char> big;  // a larger parameter block (registered kernels), used instead of params
+    const unsigned char *data() const { return big.empty() ? params : big.data(); }
 };
 
 // Validates the task's tensors and scalars for `kernel` (a

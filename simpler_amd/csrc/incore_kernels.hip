@@ -89,23 +89,39 @@ __global__ void __launch_bounds__(256) tg_matmul_kernel(const MatParams P) {
     const int mt = tile / ntn, nt = tile - mt * ntn;
     const int r = lane & 15, g = lane >> 4;
     const int row = mt * 16 + r, col = nt * 16 + r;
+    // The operands of KCH k-steps are loaded before their MFMAs, so a wave
+    // waits for one memory round trip per 32*KCH of K rather than one per
+    // load (K = 128, the tasks' size, is one round trip). K % 8 == 0 (checked
+    // at launch), so a lane's 8 k-values are all in range or all out; out of
+    // range, the loads read element 0 of the operand (always in bounds) and
+    // the value is replaced by zero, with no branch between the loads.
+    constexpr int KCH = 4;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < P.K; k0 += 32) {
-        const int kk = k0 + 8 * g;
-        u32x4_t av = {0u, 0u, 0u, 0u};
-        if (row < P.M && kk < P.K) av = *reinterpret_cast<const u32x4_t *>(P.a + row * P.a_ld + kk);
-        u32x4_t bv = {0u, 0u, 0u, 0u};
-        if (B_ROWS_ARE_COLS) {
-            if (col < P.N && kk < P.K) bv = *reinterpret_cast<const u32x4_t *>(P.b + col * P.b_ld + kk);
-        } else if (col < P.N) {
-            u16x8_t h = {0, 0, 0, 0, 0, 0, 0, 0};
+    const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+    for (int k_base = 0; k_base < P.K; k_base += 32 * KCH) {
+        u32x4_t av[KCH], bv[KCH];
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
-                if (kk + t < P.K) h[t] = P.b[(int64_t)(kk + t) * P.b_ld + col];
-            bv = __builtin_bit_cast(u32x4_t, h);
+        for (int c = 0; c < KCH; ++c) {
+            const int kk = k_base + 32 * c + 8 * g;
+            const bool oka = row < P.M && kk < P.K, okb = col < P.N && kk < P.K;
+            const u32x4_t a = *reinterpret_cast<const u32x4_t *>(P.a + (oka ? (int64_t)row * P.a_ld + kk : 0));
+            av[c] = oka ? a : zero4;
+            if (B_ROWS_ARE_COLS) {
+                const u32x4_t b = *reinterpret_cast<const u32x4_t *>(P.b + (okb ? (int64_t)col * P.b_ld + kk : 0));
+                bv[c] = okb ? b : zero4;
+            } else {
+                const int64_t b0 = okb ? (int64_t)kk * P.b_ld + col : 0;
+                u16x8_t h;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) h[t] = P.b[b0 + (int64_t)t * P.b_ld];
+                bv[c] = okb ? __builtin_bit_cast(u32x4_t, h) : zero4;
+            }
         }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                      __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < KCH; ++c)
+            if (k_base + 32 * c < P.K)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[c]),
+                                                              __builtin_bit_cast(bf16x8_t, bv[c]), acc, 0, 0, 0);
     }
     // C layout: lane holds C[4g + e][r] of the tile.
 #pragma unroll
@@ -134,8 +150,18 @@ __global__ void __launch_bounds__(256) tg_softmax_prepare_kernel(const SfParams 
     const float *s = P.s + row * P.s_ld;
     uint16_t *p = P.p + row * P.p_ld;
     const int valid = P.valid < P.N ? P.valid : P.N;
+    // the first SV scores of each lane stay in registers between the two passes
+    // (N <= 64 * SV: one read of the row)
+    constexpr int SV = 4;
+    float xs[SV];
     float mx = -INFINITY;
-    for (int c = lane; c < P.N; c += 64) {
+#pragma unroll
+    for (int i = 0; i < SV; ++i) {
+        const int c = lane + 64 * i;
+        xs[i] = c < valid ? s[c] * P.scale : -INFINITY;
+        mx = fmaxf(mx, xs[i]);
+    }
+    for (int c = lane + 64 * SV; c < P.N; c += 64) {
         const float x = c < valid ? s[c] * P.scale : -INFINITY;
         mx = fmaxf(mx, x);
     }
@@ -143,7 +169,16 @@ __global__ void __launch_bounds__(256) tg_softmax_prepare_kernel(const SfParams 
     const bool any = valid > 0;
     const float m = any ? mx : kMaskedRowMax;
     float sum = 0.f;
-    for (int c = lane; c < P.N; c += 64) {
+#pragma unroll
+    for (int i = 0; i < SV; ++i) {
+        const int c = lane + 64 * i;
+        if (c < P.N) {
+            const uint16_t pb = any ? f32_to_bf16_rne(expf(xs[i] - m)) : (uint16_t)0;
+            p[c] = pb;
+            sum += bf16_to_f32(pb);
+        }
+    }
+    for (int c = lane + 64 * SV; c < P.N; c += 64) {
         const float x = c < valid ? s[c] * P.scale : -INFINITY;
         const uint16_t pb = any ? f32_to_bf16_rne(expf(x - m)) : (uint16_t)0;
         p[c] = pb;

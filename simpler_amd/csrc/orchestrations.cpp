@@ -17,8 +17,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <vector>
 
 #include "simpler_hip/task_graph.h"
+#include "task_graph_internal.h"
 
 namespace {
 
@@ -102,6 +104,24 @@ Submitted submit(SimplerHipTaskGraph *g, int32_t func_id, const Args &a) {
     return r;
 }
 
+// Replay key of a step: bytes appended in the order the orchestration reads them.
+struct StepKey {
+    std::vector<uint8_t> bytes;
+    void add(const void *p, size_t n) {
+        const uint8_t *b = static_cast<const uint8_t *>(p);
+        bytes.insert(bytes.end(), b, b + n);
+    }
+    void add_u64(uint64_t v) { add(&v, sizeof(v)); }
+};
+
+// A step replays in GRAPH mode only (there the host's orchestration is the
+// step's critical path; elsewhere the key's table reads would be wasted), and
+// only when it starts on a reset graph, so that its key describes every task
+// the graph will hold.
+bool replayable(const SimplerHipTaskGraph *g) {
+    return simpler_hip::tg_mode_of(g) == SIMPLER_HIP_TG_GRAPH && simpler_hip::tg_is_fresh(g);
+}
+
 uint64_t f32_bits(float f) {
     uint32_t u;
     memcpy(&u, &f, 4);
@@ -146,6 +166,36 @@ int simpler_hip_tg_orchestrate_paged_attention(SimplerHipTaskGraph *g, const Sim
     }
     for (int32_t f = 0; f < 4; ++f) simpler_hip_tg_bind(g, f, f);  // FUNC_* ids equal the kernel codes
     simpler_hip_tg_bind(g, FUNC_ZERO_FILL, SIMPLER_HIP_K_ZERO_FILL);
+
+    // GRAPH mode: the step is a function of the six tensors, the scale and
+    // the table values read below (context_lens[b], then block_table[b][bn]
+    // for the blocks it covers). With the same key as the recorded step, the
+    // recorded DAG is restored instead of being orchestrated again.
+    StepKey key;
+    const bool replay = replayable(g);
+    if (replay) {
+        const SimplerChipTensor tables[2] = {cl, bt};
+        int rc = simpler_hip::tg_prefetch_host(g, tables, 2);  // both tables, one synchronisation
+        if (rc != SIMPLER_HIP_OK) return rc;
+        key.add(tensors, 6 * sizeof(SimplerChipTensor));
+        key.add_u64(scale_bits);
+        for (uint32_t b = 0; b < batch; ++b) {
+            uint64_t raw = 0;
+            const uint32_t cl_idx[1] = {b};
+            rc = simpler_hip_tg_get_tensor_data(g, &cl, 1, cl_idx, &raw);
+            if (rc != SIMPLER_HIP_OK) return rc;
+            key.add_u64(raw);
+            const int64_t len = (int32_t)(uint32_t)raw;
+            const uint64_t nb = len <= 0 ? 0 : std::min<uint64_t>(((uint64_t)len + block_size - 1) / block_size, block_num);
+            for (uint64_t bn = 0; bn < nb; ++bn) {
+                const uint32_t bt_idx[2] = {b, (uint32_t)bn};
+                rc = simpler_hip_tg_get_tensor_data(g, &bt, 2, bt_idx, &raw);
+                if (rc != SIMPLER_HIP_OK) return rc;
+                key.add_u64(raw);
+            }
+        }
+        if (simpler_hip_tg_replay(g, key.bytes.data(), key.bytes.size()) == 1) return SIMPLER_HIP_OK;
+    }
 
     const uint32_t q_tile = std::min<uint32_t>(num_heads, 128);  // :105
     const uint32_t q_loop = (num_heads + q_tile - 1) / q_tile;
@@ -260,6 +310,7 @@ int simpler_hip_tg_orchestrate_paged_attention(SimplerHipTaskGraph *g, const Sim
             simpler_hip_tg_scope_end(g);
         }
     }
+    if (replay) return simpler_hip_tg_record_replay(g, key.bytes.data(), key.bytes.size());
     return SIMPLER_HIP_OK;
 }
 
@@ -270,6 +321,13 @@ int simpler_hip_tg_orchestrate_vector_example(SimplerHipTaskGraph *g, const Simp
     simpler_hip_tg_bind(g, 0, SIMPLER_HIP_K_VEC_ADD);
     simpler_hip_tg_bind(g, 1, SIMPLER_HIP_K_VEC_ADD_SCALAR);
     simpler_hip_tg_bind(g, 2, SIMPLER_HIP_K_VEC_MUL);
+    // GRAPH mode: the step depends on its three tensors only
+    StepKey key;
+    const bool replay = replayable(g);
+    if (replay) {
+        key.add(tensors, 3 * sizeof(SimplerChipTensor));
+        if (simpler_hip_tg_replay(g, key.bytes.data(), key.bytes.size()) == 1) return SIMPLER_HIP_OK;
+    }
     const uint32_t size = ext_a.shapes[0];
     const SimplerChipTensor inter_ci = create_info(&size, 1, SIMPLER_DT_FLOAT32);
 
@@ -310,6 +368,7 @@ int simpler_hip_tg_orchestrate_vector_example(SimplerHipTaskGraph *g, const Simp
     const Submitted o4 = submit(g, 0, t4);
     if (o4.task < 0) return (int)o4.task;
     simpler_hip_tg_scope_end(g);
+    if (replay) return simpler_hip_tg_record_replay(g, key.bytes.data(), key.bytes.size());
     return SIMPLER_HIP_OK;
 }
 

@@ -23,11 +23,23 @@
 //
 // Execution: EAGER launches each task on the stream at submit. GRAPH turns the
 // tasks submitted between launches (a segment) into one hipGraph, a kernel
-// node per task with its in-segment fanin as dependencies. The executable
+// node per task. The nodes form one chain in submission order (a topological
+// order of the inferred DAG), the order EAGER runs them in: on cfg1 a graph
+// with the DAG's own edges cost 146 µs of host time per hipGraphLaunch and
+// 212 µs on the device, the chain 55 and 147 µs (ROCm runs a DAG's branches
+// on internal streams joined by waits). The inferred edges still decide when
+// a cached graph may be replayed. The executable
 // graph is cached per segment index: when the next run submits the same
 // kernels, launch shapes and edges (a decode loop over stable buffers), it is
 // replayed, with hipGraphExecKernelNodeSetParams on the nodes whose parameter
-// blocks changed, instead of being rebuilt.
+// blocks changed, instead of being rebuilt. A whole step can also be replayed
+// without being submitted again: record_replay keeps the graph's state after a
+// step's orchestration under a caller key, and replay restores it on a reset
+// graph, so only the launch of the cached executable graph is left.
+//
+// Kernels: the built-in incore kernels (incore_kernels.hip), plus kernels the
+// caller registers from code object files; those get the task's tensors and
+// scalars as one SimplerHipKernelArgs.
 
 #include <hip/hip_runtime.h>
 
@@ -39,17 +51,20 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
 #include "incore.h"
 #include "simpler_hip/task_graph.h"
+#include "task_graph_internal.h"
 
 namespace {
 
 using simpler_hip::KernelLaunch;
 
 constexpr int kMaxFuncIds = 64;
+constexpr int32_t kCustomBase = 1 << 20;  // kernel codes of registered kernels: kCustomBase + index
 constexpr size_t kAlign = 256;
 constexpr size_t kChunkBytes = (size_t)64 << 20;
 constexpr uint64_t kRecordBase = 0x7e0000000000ull;  // placeholder device addresses in RECORD_ONLY mode
@@ -66,8 +81,16 @@ void tg_log(const char *fmt, ...) {
 struct Task {
     int32_t func_id = -1;
     int32_t kernel = -1;  // -1: dependency-only
-    KernelLaunch launch;
+    KernelLaunch launch;  // launch.func: a __global__ stub, or the hipFunction_t of a registered kernel
     std::vector<int32_t> fanin;
+};
+
+// A kernel registered from a code object: its function and launch shape rule.
+struct CustomKernel {
+    hipFunction_t fn = nullptr;
+    uint32_t block = 64;
+    int32_t grid_tensor = -1;
+    uint32_t per_wg = 1;
 };
 
 // One node of a cached executable graph: what must match for a replay.
@@ -83,7 +106,7 @@ struct SegmentCache {
     hipGraphExec_t exec = nullptr;
     std::vector<hipGraphNode_t> nodes;
     std::vector<NodeSig> sigs;
-    std::vector<std::array<unsigned char, simpler_hip::kMaxKernelParamBytes>> params;
+    std::vector<std::vector<unsigned char>> params;  // each node's parameter block as last set
     void clear() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
@@ -124,9 +147,28 @@ struct Chunk {
     size_t used;
 };
 
+// A host copy of an external tensor's bytes [begin, end), in pinned memory
+// (one asynchronous copy and one stream synchronisation per refresh).
 struct HostCopy {
-    uint64_t begin, end;  // bytes from the buffer address
-    std::vector<uint8_t> data;
+    uint64_t begin = 0, end = 0;  // bytes from the buffer address
+    uint8_t *data = nullptr;      // hipHostMalloc'ed, `cap` bytes
+    size_t cap = 0;
+    bool valid = false;
+};
+
+// The state of a graph after one step's orchestration, kept for replay.
+struct StepSnapshot {
+    bool valid = false;
+    std::vector<uint8_t> key;
+    std::deque<Task> tasks;
+    std::unordered_map<uint64_t, std::vector<Region>> tmap;
+    std::unordered_map<uint64_t, int32_t> buf_of;
+    std::vector<Buffer> bufs;
+    std::vector<std::vector<int32_t>> scopes;
+    std::multimap<size_t, FreeBlock> free_blocks;
+    std::vector<size_t> chunk_used;
+    size_t chunk_cursor = 0;
+    uint64_t record_next = 0;
 };
 
 uint64_t extent_elems(const SimplerChipTensor &t) {
@@ -249,6 +291,10 @@ struct SimplerHipTaskGraph {
     int32_t segment = 0;
     size_t segment_first = 0;
     std::vector<SegmentCache> cache;
+    StepSnapshot replay;
+    uint64_t replays = 0;
+    std::vector<CustomKernel> custom;
+    std::vector<std::pair<std::string, hipModule_t>> modules;
 
     SimplerHipTaskGraph() {
         for (int i = 0; i < kMaxFuncIds; ++i) func_kernel[i] = -1;
@@ -317,7 +363,7 @@ void producers_of(const SimplerHipTaskGraph *g, const SimplerChipTensor &t, std:
 }
 
 hipKernelNodeParams node_params(const Task &t, void **args) {
-    args[0] = const_cast<unsigned char *>(t.launch.params);
+    args[0] = const_cast<unsigned char *>(t.launch.data());
     hipKernelNodeParams p{};
     p.func = const_cast<void *>(t.launch.func);
     p.gridDim = t.launch.grid;
@@ -365,10 +411,8 @@ int build_segment(SegmentCache &c, SimplerHipTaskGraph *g, size_t first, size_t 
         s.block = t.launch.block.x;
         deps.clear();
         for (int32_t f : t.fanin)
-            if ((size_t)f >= first) {
-                s.deps.push_back((int32_t)((size_t)f - first));
-                deps.push_back(c.nodes[(size_t)f - first]);
-            }
+            if ((size_t)f >= first) s.deps.push_back((int32_t)((size_t)f - first));
+        if (i > 0) deps.push_back(c.nodes[i - 1]);  // one chain in submission order
         hipError_t e;
         if (t.kernel < 0) {
             e = hipGraphAddEmptyNode(&c.nodes[i], c.graph, deps.data(), deps.size());
@@ -376,7 +420,7 @@ int build_segment(SegmentCache &c, SimplerHipTaskGraph *g, size_t first, size_t 
             void *args[1];
             const hipKernelNodeParams p = node_params(t, args);
             e = hipGraphAddKernelNode(&c.nodes[i], c.graph, deps.data(), deps.size(), &p);
-            memcpy(c.params[i].data(), t.launch.params, t.launch.param_bytes);
+            c.params[i].assign(t.launch.data(), t.launch.data() + t.launch.param_bytes);
         }
         if (e != hipSuccess) {
             tg_log("adding graph node failed: %s", hipGetErrorString(e));
@@ -402,7 +446,7 @@ int launch_segment(SimplerHipTaskGraph *g) {
     if (c.exec && same_shape(c, g, first, n)) {
         for (size_t i = 0; i < n; ++i) {
             const Task &t = g->tasks[first + i];
-            if (t.kernel < 0 || memcmp(c.params[i].data(), t.launch.params, t.launch.param_bytes) == 0) continue;
+            if (t.kernel < 0 || memcmp(c.params[i].data(), t.launch.data(), t.launch.param_bytes) == 0) continue;
             void *args[1];
             const hipKernelNodeParams p = node_params(t, args);
             if (hipGraphExecKernelNodeSetParams(c.exec, c.nodes[i], &p) != hipSuccess) {
@@ -410,7 +454,7 @@ int launch_segment(SimplerHipTaskGraph *g) {
                 c.clear();
                 break;
             }
-            memcpy(c.params[i].data(), t.launch.params, t.launch.param_bytes);
+            c.params[i].assign(t.launch.data(), t.launch.data() + t.launch.param_bytes);
         }
     }
     if (!c.exec || !same_shape(c, g, first, n)) {
@@ -426,6 +470,54 @@ int launch_segment(SimplerHipTaskGraph *g) {
     return SIMPLER_HIP_OK;
 }
 
+// A task writes the buffer at `addr`: its host copy is stale.
+void invalidate_host_copy(SimplerHipTaskGraph *g, uint64_t addr) {
+    auto it = g->host_cache.find(addr);
+    if (it != g->host_cache.end()) it->second.valid = false;
+}
+
+// Mark every host copy stale, keeping the pinned buffers for the next step's
+// reads of the same tensors; free them all (`release`, or when more than 32
+// buffers have accumulated).
+void drop_host_copies(SimplerHipTaskGraph *g, bool release) {
+    release = release || g->host_cache.size() > 32;
+    for (auto &kv : g->host_cache) {
+        kv.second.valid = false;
+        if (release && kv.second.data) (void)hipHostFree(kv.second.data);
+    }
+    if (release) g->host_cache.clear();
+}
+
+// Queue the copy of external tensor t's bytes into its pinned host copy,
+// unless that copy is current (*queued = false). Stream order makes the copy
+// follow the work queued so far; the caller's synchronisation then waits for
+// both and marks the copy valid.
+int queue_host_copy(SimplerHipTaskGraph *g, const SimplerChipTensor &t, HostCopy **out, bool *queued) {
+    uint64_t b, e;
+    byte_range(t, &b, &e);
+    HostCopy &hc = g->host_cache[t.buffer.addr];
+    *out = &hc;
+    *queued = false;
+    if (hc.valid && hc.begin <= b && e <= hc.end) return SIMPLER_HIP_OK;
+    hc.valid = false;
+    if (hc.cap < e - b) {
+        if (hc.data) (void)hipHostFree(hc.data);
+        hc.data = nullptr;
+        hc.cap = 0;
+        void *p = nullptr;
+        if (hipHostMalloc(&p, e - b, hipHostMallocDefault) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+        hc.data = static_cast<uint8_t *>(p);
+        hc.cap = e - b;
+    }
+    if (hipMemcpyAsync(hc.data, (const void *)(uintptr_t)(t.buffer.addr + b), e - b, hipMemcpyDeviceToHost,
+                       g->stream) != hipSuccess)
+        return SIMPLER_HIP_ERR_LAUNCH;
+    hc.begin = b;
+    hc.end = e;
+    *queued = true;
+    return SIMPLER_HIP_OK;
+}
+
 // Make every task submitted so far complete (used before reading data).
 int drain(SimplerHipTaskGraph *g) {
     int rc = launch_segment(g);
@@ -433,12 +525,72 @@ int drain(SimplerHipTaskGraph *g) {
     return sync_stream(g);
 }
 
+bool is_custom(int32_t kernel) { return kernel >= kCustomBase; }
+
+// Launch record of a registered kernel: the task's tensors as views, then its
+// scalars, in one SimplerHipKernelArgs; the grid from the shape rule.
+int make_custom_launch(const SimplerHipTaskGraph *g, int32_t kernel, const SimplerChipTensor *tensors, int32_t n,
+                       const uint64_t *scalars, int32_t ns, KernelLaunch *out, char *why, size_t why_len) {
+    const CustomKernel &k = g->custom[(size_t)(kernel - kCustomBase)];
+    if (n > SIMPLER_HIP_TG_KERNEL_MAX_TENSORS) {
+        snprintf(why, why_len, "%d tensors, at most %d for a registered kernel", n, SIMPLER_HIP_TG_KERNEL_MAX_TENSORS);
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    if (k.grid_tensor >= n) {
+        snprintf(why, why_len, "the kernel's grid follows tensor %d, but the task has %d", k.grid_tensor, n);
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    SimplerHipKernelArgs a;
+    memset(&a, 0, sizeof(a));
+    a.n_tensors = n;
+    a.n_scalars = ns;
+    for (int i = 0; i < n; ++i) {
+        const SimplerChipTensor &t = tensors[i];
+        SimplerHipKernelTensor &v = a.tensors[i];
+        v.addr = t.buffer.addr + t.start_offset * simpler_dtype_size(t.dtype);
+        v.ndims = t.ndims;
+        v.dtype = t.dtype;
+        for (uint32_t d = 0; d < t.ndims; ++d) {
+            v.shapes[d] = t.shapes[d];
+            v.strides[d] = t.strides[d];
+        }
+    }
+    for (int i = 0; i < ns; ++i) a.scalars[i] = scalars[i];
+    uint64_t grid = k.per_wg;
+    if (k.grid_tensor >= 0) grid = (numel(tensors[k.grid_tensor]) + k.per_wg - 1) / k.per_wg;
+    if (grid == 0) grid = 1;
+    if (grid > 0x7fffffffu) {
+        snprintf(why, why_len, "grid of %llu workgroups", (unsigned long long)grid);
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    out->func = reinterpret_cast<const void *>(k.fn);
+    out->grid = dim3((unsigned)grid, 1, 1);
+    out->block = dim3(k.block, 1, 1);
+    out->param_bytes = sizeof(a);
+    const unsigned char *ab = reinterpret_cast<const unsigned char *>(&a);
+    out->big.assign(ab, ab + sizeof(a));
+    return SIMPLER_HIP_OK;
+}
+
+int make_launch(const SimplerHipTaskGraph *g, int32_t kernel, const SimplerChipTensor *tensors, int32_t n,
+                const uint64_t *scalars, int32_t ns, KernelLaunch *out, char *why, size_t why_len) {
+    if (is_custom(kernel)) return make_custom_launch(g, kernel, tensors, n, scalars, ns, out, why, why_len);
+    return simpler_hip::make_incore_launch(kernel, tensors, n, scalars, ns, out, why, why_len);
+}
+
 // EAGER: launch now. GRAPH: the task waits in the segment until launch.
 int record_task(SimplerHipTaskGraph *g, Task &t) {
     if (g->mode != SIMPLER_HIP_TG_EAGER || t.kernel < 0) return SIMPLER_HIP_OK;
-    void *args[1] = {t.launch.params};
-    if (hipLaunchKernel(t.launch.func, t.launch.grid, t.launch.block, args, 0, g->stream) != hipSuccess) {
-        tg_log("launch of kernel %d failed: %s", t.kernel, hipGetErrorString(hipGetLastError()));
+    void *args[1] = {const_cast<unsigned char *>(t.launch.data())};
+    hipError_t e;
+    if (is_custom(t.kernel))
+        e = hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(const_cast<void *>(t.launch.func)), t.launch.grid.x,
+                                  1, 1, t.launch.block.x, 1, 1, 0, g->stream, args, nullptr);
+    else
+        e = hipLaunchKernel(t.launch.func, t.launch.grid, t.launch.block, args, 0, g->stream);
+    if (e != hipSuccess) {
+        tg_log("launch of kernel %d failed: %s", t.kernel, hipGetErrorString(e));
+        (void)hipGetLastError();
         return SIMPLER_HIP_ERR_LAUNCH;
     }
     return SIMPLER_HIP_OK;
@@ -466,6 +618,40 @@ SimplerChipTensor materialize(const SimplerChipTensor &ci, uint64_t addr, size_t
 
 }  // namespace
 
+int32_t simpler_hip::tg_mode_of(const SimplerHipTaskGraph *g) { return g->mode; }
+
+int simpler_hip::tg_prefetch_host(SimplerHipTaskGraph *g, const SimplerChipTensor *tensors, int n) {
+    if (!device_mode(g)) return SIMPLER_HIP_OK;
+    std::vector<HostCopy *> pending;
+    for (int i = 0; i < n; ++i) {
+        const SimplerChipTensor &t = tensors[i];
+        if (t.address_space != SIMPLER_ADDR_DEVICE || !valid_tensor(t)) continue;
+        std::vector<int32_t> prod;
+        producers_of(g, t, &prod);
+        if (!prod.empty()) continue;  // written by this graph's tasks: read after they finish
+        HostCopy *hc = nullptr;
+        bool queued = false;
+        const int rc = queue_host_copy(g, t, &hc, &queued);
+        if (rc != SIMPLER_HIP_OK) return rc;
+        if (queued) pending.push_back(hc);
+    }
+    if (pending.empty()) return SIMPLER_HIP_OK;
+    if (hipStreamSynchronize(g->stream) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+    for (HostCopy *hc : pending) hc->valid = true;
+    return SIMPLER_HIP_OK;
+}
+
+bool simpler_hip::tg_is_fresh(const SimplerHipTaskGraph *g) {
+    if (!g->tasks.empty() || g->segment != 0 || g->segment_first != 0 || !g->free_blocks.empty() ||
+        !g->bufs.empty() || g->chunk_cursor != 0)
+        return false;
+    for (const auto &sc : g->scopes)  // scopes may be open, but hold nothing yet
+        if (!sc.empty()) return false;
+    for (const Chunk &c : g->chunks)
+        if (c.used) return false;
+    return true;
+}
+
 extern "C" {
 
 SimplerHipTaskGraph *simpler_hip_tg_create(int32_t mode, void *stream) {
@@ -488,6 +674,8 @@ void simpler_hip_tg_destroy(SimplerHipTaskGraph *g) {
         sync_stream(g);
         for (SegmentCache &c : g->cache) c.clear();
         for (Chunk &c : g->chunks) (void)hipFree(c.base);
+        for (auto &m : g->modules) (void)hipModuleUnload(m.second);
+        drop_host_copies(g, true);
     }
     delete g;
 }
@@ -496,6 +684,47 @@ int simpler_hip_tg_bind(SimplerHipTaskGraph *g, int32_t func_id, int32_t kernel)
     if (!g || func_id < 0 || func_id >= kMaxFuncIds || simpler_hip::incore_tensor_count(kernel) < 0)
         return SIMPLER_HIP_ERR_INVALID;
     g->func_kernel[func_id] = kernel;
+    return SIMPLER_HIP_OK;
+}
+
+int simpler_hip_tg_register_kernel(SimplerHipTaskGraph *g, int32_t func_id, const char *code_object_path,
+                                   const char *kernel_name, uint32_t block_threads, int32_t grid_tensor,
+                                   uint32_t elems_per_workgroup) {
+    if (!g || func_id < 0 || func_id >= kMaxFuncIds || !code_object_path || !kernel_name || block_threads == 0 ||
+        block_threads > 1024 || elems_per_workgroup == 0 || grid_tensor >= SIMPLER_HIP_TG_KERNEL_MAX_TENSORS) {
+        tg_log("register_kernel: bad argument");
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    if (g->custom.size() >= (size_t)kMaxFuncIds * 4) return SIMPLER_HIP_ERR_INVALID;
+    CustomKernel k;
+    k.block = block_threads;
+    k.grid_tensor = grid_tensor < 0 ? -1 : grid_tensor;
+    k.per_wg = elems_per_workgroup;
+    if (device_mode(g)) {
+        hipModule_t mod = nullptr;
+        for (auto &m : g->modules)
+            if (m.first == code_object_path) mod = m.second;
+        if (!mod) {
+            int cur = -1;
+            if (hipGetDevice(&cur) != hipSuccess || (cur != g->device && hipSetDevice(g->device) != hipSuccess))
+                return SIMPLER_HIP_ERR_LAUNCH;
+            const hipError_t e = hipModuleLoad(&mod, code_object_path);
+            if (cur != g->device) (void)hipSetDevice(cur);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                tg_log("register_kernel: cannot load code object %s: %s", code_object_path, hipGetErrorString(e));
+                return SIMPLER_HIP_ERR_UNSUPPORTED;
+            }
+            g->modules.emplace_back(code_object_path, mod);
+        }
+        if (hipModuleGetFunction(&k.fn, mod, kernel_name) != hipSuccess) {
+            (void)hipGetLastError();
+            tg_log("register_kernel: no kernel %s in %s", kernel_name, code_object_path);
+            return SIMPLER_HIP_ERR_UNSUPPORTED;
+        }
+    }
+    g->custom.push_back(k);
+    g->func_kernel[func_id] = kCustomBase + (int32_t)(g->custom.size() - 1);
     return SIMPLER_HIP_OK;
 }
 
@@ -511,7 +740,7 @@ int simpler_hip_tg_scope_end(SimplerHipTaskGraph *g) {
         Buffer &b = g->bufs[bi];
         g->tmap.erase(b.addr);
         g->buf_of.erase(b.addr);
-        g->host_cache.erase(b.addr);
+        invalidate_host_copy(g, b.addr);
         FreeBlock fb{b.addr, (b.bytes + kAlign - 1) / kAlign * kAlign, std::move(b.users)};
         g->free_blocks.emplace(fb.bytes, std::move(fb));
         b.users.clear();
@@ -567,7 +796,7 @@ int64_t simpler_hip_tg_submit(SimplerHipTaskGraph *g, int32_t func_id, const Sim
                 probe[i] = materialize(args[i], kRecordBase, numel(args[i]) * simpler_dtype_size(args[i].dtype), id);
         KernelLaunch tmp;
         char why[256] = {};
-        const int rc = simpler_hip::make_incore_launch(kernel, probe.data(), n, scalars, ns, &tmp, why, sizeof(why));
+        const int rc = make_launch(g, kernel, probe.data(), n, scalars, ns, &tmp, why, sizeof(why));
         if (rc != SIMPLER_HIP_OK) {
             tg_log("submit: func_id %d: %s", func_id, why);
             return rc;
@@ -633,7 +862,7 @@ int64_t simpler_hip_tg_submit(SimplerHipTaskGraph *g, int32_t func_id, const Sim
         const int32_t ty = arg_types[i];
         if ((ty != SIMPLER_HIP_TA_INOUT && ty != SIMPLER_HIP_TA_OUTPUT_EXISTING) || args[i].manual_dep) continue;
         g->tmap[args[i].buffer.addr].push_back(region_of(args[i], id));
-        g->host_cache.erase(args[i].buffer.addr);
+        invalidate_host_copy(g, args[i].buffer.addr);
     }
 
     std::sort(fanin.begin(), fanin.end());
@@ -641,8 +870,7 @@ int64_t simpler_hip_tg_submit(SimplerHipTaskGraph *g, int32_t func_id, const Sim
 
     if (kernel >= 0) {
         char why[256] = {};
-        const int rc =
-            simpler_hip::make_incore_launch(kernel, args.data(), n, scalars, ns, &t.launch, why, sizeof(why));
+        const int rc = make_launch(g, kernel, args.data(), n, scalars, ns, &t.launch, why, sizeof(why));
         if (rc != SIMPLER_HIP_OK) {  // not reached: the dry run accepted the same shapes
             tg_log("submit: func_id %d: %s", func_id, why);
             return rc;
@@ -697,19 +925,15 @@ int simpler_hip_tg_get_tensor_data(SimplerHipTaskGraph *g, const SimplerChipTens
     // external input: one copy of the view's extent, reused until a task writes the buffer
     uint64_t b, e;
     byte_range(*t, &b, &e);
-    HostCopy &hc = g->host_cache[t->buffer.addr];
-    if (!(hc.begin <= b && e <= hc.end && !hc.data.empty())) {
-        if (sync_stream(g) != SIMPLER_HIP_OK) return SIMPLER_HIP_ERR_LAUNCH;
-        hc.begin = b;
-        hc.end = e;
-        hc.data.resize(e - b);
-        if (hipMemcpy(hc.data.data(), (const void *)(uintptr_t)(t->buffer.addr + b), e - b, hipMemcpyDeviceToHost) !=
-            hipSuccess) {
-            hc.data.clear();
-            return SIMPLER_HIP_ERR_LAUNCH;
-        }
+    HostCopy *hc = nullptr;
+    bool queued = false;
+    int rc = queue_host_copy(g, *t, &hc, &queued);
+    if (rc != SIMPLER_HIP_OK) return rc;
+    if (queued) {
+        if (hipStreamSynchronize(g->stream) != hipSuccess) return SIMPLER_HIP_ERR_LAUNCH;
+        hc->valid = true;
     }
-    memcpy(&v, hc.data.data() + (off * esz - hc.begin), esz);
+    memcpy(&v, hc->data + (off * esz - hc->begin), esz);
     *value = v;
     return SIMPLER_HIP_OK;
 }
@@ -751,7 +975,7 @@ int simpler_hip_tg_reset(SimplerHipTaskGraph *g) {
     g->bufs.clear();
     g->scopes.clear();
     g->free_blocks.clear();
-    g->host_cache.clear();
+    drop_host_copies(g, false);
     for (Chunk &c : g->chunks) c.used = 0;
     g->chunk_cursor = 0;
     g->record_next = kRecordBase;
@@ -760,7 +984,54 @@ int simpler_hip_tg_reset(SimplerHipTaskGraph *g) {
     return rc;
 }
 
+int simpler_hip_tg_record_replay(SimplerHipTaskGraph *g, const void *key, uint64_t key_bytes) {
+    if (!g || (key_bytes && !key)) return SIMPLER_HIP_ERR_INVALID;
+    if (g->mode != SIMPLER_HIP_TG_GRAPH) return SIMPLER_HIP_OK;
+    if (g->segment != 0 || g->segment_first != 0) {
+        tg_log("record_replay: the step has launched work");
+        return SIMPLER_HIP_ERR_INVALID;
+    }
+    StepSnapshot &r = g->replay;
+    r.valid = false;
+    const uint8_t *kb = static_cast<const uint8_t *>(key);
+    r.key.assign(kb, kb + key_bytes);
+    r.tasks = g->tasks;
+    r.tmap = g->tmap;
+    r.buf_of = g->buf_of;
+    r.bufs = g->bufs;
+    r.scopes = g->scopes;
+    r.free_blocks = g->free_blocks;
+    r.chunk_used.clear();
+    for (const Chunk &c : g->chunks) r.chunk_used.push_back(c.used);
+    r.chunk_cursor = g->chunk_cursor;
+    r.record_next = g->record_next;
+    r.valid = true;
+    return SIMPLER_HIP_OK;
+}
+
+int simpler_hip_tg_replay(SimplerHipTaskGraph *g, const void *key, uint64_t key_bytes) {
+    if (!g || (key_bytes && !key)) return SIMPLER_HIP_ERR_INVALID;
+    const StepSnapshot &r = g->replay;
+    if (g->mode != SIMPLER_HIP_TG_GRAPH || !r.valid || r.key.size() != key_bytes ||
+        (key_bytes && memcmp(r.key.data(), key, key_bytes) != 0) || r.chunk_used.size() > g->chunks.size() ||
+        r.scopes.size() != g->scopes.size() || !simpler_hip::tg_is_fresh(g))
+        return 0;
+    g->tasks = r.tasks;
+    g->tmap = r.tmap;
+    g->buf_of = r.buf_of;
+    g->bufs = r.bufs;
+    g->scopes = r.scopes;
+    g->free_blocks = r.free_blocks;
+    for (size_t i = 0; i < g->chunks.size(); ++i) g->chunks[i].used = i < r.chunk_used.size() ? r.chunk_used[i] : 0;
+    g->chunk_cursor = r.chunk_cursor;
+    g->record_next = r.record_next;
+    ++g->replays;
+    return 1;
+}
+
 int64_t simpler_hip_tg_task_count(const SimplerHipTaskGraph *g) { return g ? (int64_t)g->tasks.size() : -1; }
+
+uint64_t simpler_hip_tg_replay_count(const SimplerHipTaskGraph *g) { return g ? g->replays : 0; }
 
 int32_t simpler_hip_tg_fanin(const SimplerHipTaskGraph *g, int64_t task, int64_t *producers, int32_t cap) {
     if (!g || task < 0 || task >= (int64_t)g->tasks.size()) return SIMPLER_HIP_ERR_INVALID;

@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import os
 import struct
 from enum import IntEnum
 from typing import Iterable, Sequence
@@ -169,6 +170,32 @@ class TaskGraph:
     def bind(self, func_id: int, kernel: IncoreKernel) -> None:
         self._check(self._lib.simpler_hip_tg_bind(self._g, int(func_id), int(kernel)), "bind")
 
+    def register_kernel(self, func_id: int, code_object: str | os.PathLike, kernel_name: str, *,
+                        block_threads: int = 256, grid_tensor: int = 0, elems_per_workgroup: int = 256) -> None:
+        """Bind ``func_id`` to ``extern "C"`` kernel ``kernel_name`` of a gfx950 code
+        object (``hipcc --genco``; :func:`simpler_amd.build.build_code_object`). The
+        kernel takes one ``SimplerHipKernelArgs`` (``include/simpler_hip/task_graph.h``):
+        the task's tensors, then its scalars. Each task launches ``block_threads``
+        threads per workgroup and ``ceil(numel(tensor grid_tensor) /
+        elems_per_workgroup)`` workgroups (``elems_per_workgroup`` of them when
+        ``grid_tensor`` < 0)."""
+        rc = self._lib.simpler_hip_tg_register_kernel(self._g, int(func_id), os.fsencode(os.fspath(code_object)),
+                                                      kernel_name.encode(), int(block_threads), int(grid_tensor),
+                                                      int(elems_per_workgroup))
+        self._check(rc, f"register_kernel({kernel_name})")
+
+    def record_replay(self, key: bytes) -> None:
+        """GRAPH mode: keep the step submitted since the last reset under ``key``."""
+        buf = ctypes.create_string_buffer(bytes(key), max(len(key), 1))
+        self._check(self._lib.simpler_hip_tg_record_replay(self._g, buf, len(key)), "record_replay")
+
+    def replay(self, key: bytes) -> bool:
+        """GRAPH mode, on a reset graph: restore the step recorded under ``key``
+        (True), so that :meth:`launch` runs it without its tasks being submitted
+        again; False if ``key`` is not the recorded one."""
+        buf = ctypes.create_string_buffer(bytes(key), max(len(key), 1))
+        return self._check(self._lib.simpler_hip_tg_replay(self._g, buf, len(key)), "replay") == 1
+
     def scope_begin(self) -> None:
         self._check(self._lib.simpler_hip_tg_scope_begin(self._g), "scope_begin")
 
@@ -272,6 +299,11 @@ class TaskGraph:
     @property
     def task_count(self) -> int:
         return int(self._lib.simpler_hip_tg_task_count(self._g))
+
+    @property
+    def replay_count(self) -> int:
+        """Steps restored by :meth:`replay` (or a native orchestration's own replay)."""
+        return int(self._lib.simpler_hip_tg_replay_count(self._g))
 
     def fanin(self, task: int) -> list[int]:
         cap = 256

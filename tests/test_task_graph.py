@@ -241,3 +241,39 @@ def test_chip_tensor_view_matches_reference_semantics():
     assert t.view((6, 10), (0, 0)).is_contiguous == 1
     with pytest.raises(ValueError):
         t.view((4, 4), (3, 0))
+
+
+def test_register_kernel_argument_checks():
+    # A record-only graph loads no code object: the checks on the arguments and
+    # on each task's launch shape still apply.
+    with TaskGraph("record") as g:
+        for kw in (dict(block_threads=0), dict(block_threads=2048), dict(elems_per_workgroup=0),
+                   dict(grid_tensor=32)):
+            with pytest.raises(TaskGraphError) as e:
+                g.register_kernel(5, "/nonexistent.hsaco", "k", **kw)
+            assert e.value.rc == -1
+        with pytest.raises(TaskGraphError):
+            g.register_kernel(64, "/nonexistent.hsaco", "k")
+        g.register_kernel(5, "/nonexistent.hsaco", "k", block_threads=128, grid_tensor=2, elems_per_workgroup=64)
+        a, b = ext(0x10000, (4, 100)), ext(0x20000, (4, 100))
+        args = CoreTaskArgs()
+        args.add_input(a, b)
+        with pytest.raises(TaskGraphError) as e:  # the grid follows tensor 2, the task has two
+            g.submit_task(5, args)
+        assert e.value.rc == -1
+        assert g.task_count == 0
+        args.add_output(TensorCreateInfo((4, 100), F32))
+        t = g.submit_task(5, args)
+        assert t.task_id() == 0 and g.fanin(0) == []
+        # a registered id rebinds to a built-in and back
+        g.bind(5, IncoreKernel.VEC_ADD)
+        g.register_kernel(5, "/nonexistent.hsaco", "k")
+
+
+def test_replay_is_graph_mode_only():
+    with TaskGraph("record") as g:
+        g.orchestrate_vector_example([ext(0x10000, (64,)), ext(0x20000, (64,)), ext(0x30000, (64,))])
+        g.record_replay(b"key")  # nothing is kept outside GRAPH mode
+        g.reset()
+        assert g.replay(b"key") is False
+        assert g.replay_count == 0

@@ -22,6 +22,7 @@
 from __future__ import annotations
 
 import ctypes
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -290,3 +291,119 @@ def test_worker_runs_reference_chain_on_the_task_graph(device, execution):
         assert torch.all(f == 47.0)
     finally:
         w.close()
+
+
+# ---- kernels of the caller's own (simpler_hip_tg_register_kernel) -----------------------------------
+
+_CODE_OBJECT = Path(__file__).resolve().parent / "kernels" / "_build" / "tg_user_kernels.hsaco"
+
+
+@pytest.fixture(scope="module")
+def user_code_object():
+    if not _CODE_OBJECT.exists():  # built by __graft_entry__.build(); build it here only if missing
+        from simpler_amd import build as native_build
+        native_build.build_code_object(_CODE_OBJECT.parent.parent / "tg_user_kernels.hip", _CODE_OBJECT)
+    return _CODE_OBJECT
+
+
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_registered_kernels_run_a_dag(device, user_code_object, mode):
+    # y0 = alpha*x + b (registered), y1 = y0 * s[row] into rows 4..11 of an
+    # external tensor (registered, a view with an offset), y2 = y1 + x (built-in)
+    print(f"[case] tg registered kernels mode={mode}", flush=True)
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((8, 96)).astype(np.float32)).to(device)
+    b = torch.from_numpy(rng.standard_normal((8, 96)).astype(np.float32)).to(device)
+    s = torch.from_numpy(rng.standard_normal(8).astype(np.float32)).to(device)
+    big = torch.full((16, 96), float("nan"), dtype=torch.float32, device=device)
+    big_ct = ct(big)
+    rows = big_ct.view([8, 96], [4, 0])
+    xn, bn, sn = x.cpu().numpy(), b.cpu().numpy(), s.cpu().numpy()
+    with TaskGraph(mode) as g:
+        g.register_kernel(10, user_code_object, "tg_axpb", block_threads=256, grid_tensor=2, elems_per_workgroup=256)
+        g.register_kernel(11, user_code_object, "tg_row_scale", block_threads=128, grid_tensor=-1,
+                          elems_per_workgroup=3)
+        g.bind(12, IncoreKernel.VEC_ADD)
+        for rep, alpha in enumerate((1.5, -0.25, 1.5)):
+            g.reset()
+            a0 = CoreTaskArgs()
+            a0.add_input(ct(x), ct(b))
+            a0.add_output(TensorCreateInfo((8, 96), DataType.FLOAT32))
+            a0.add_scalar(float(alpha))
+            y0 = g.submit_task(10, a0).get_ref(0)
+            a1 = CoreTaskArgs()
+            a1.add_input(y0, ct(s))
+            a1.add_output(rows)  # OUTPUT_EXISTING: a view of the external tensor
+            t1 = g.submit_task(11, a1)
+            a2 = CoreTaskArgs()
+            a2.add_input(rows, ct(x))
+            a2.add_output(TensorCreateInfo((8, 96), DataType.FLOAT32))
+            t2 = g.submit_task(12, a2)
+            assert g.fanin(t1.task_id()) == [0] and g.fanin(t2.task_id()) == [1]
+            g.launch()
+            y2 = g.read(t2.get_ref(0))
+            g.wait()
+            want1 = (np.float32(alpha) * xn + bn) * sn[:, None]
+            np.testing.assert_allclose(big[4:12].cpu().numpy(), want1, rtol=1e-6, atol=1e-6, err_msg=f"rep {rep}")
+            np.testing.assert_allclose(y2.reshape(8, 96), want1 + xn, rtol=1e-6, atol=1e-6, err_msg=f"rep {rep}")
+            assert torch.isnan(big[:4]).all() and torch.isnan(big[12:]).all()  # nothing outside the view
+            big.fill_(float("nan"))  # eager work between the runs
+            torch.cuda.synchronize(device)
+
+
+def test_registered_kernel_that_cannot_load_is_refused(device, user_code_object, tmp_path):
+    with TaskGraph("eager") as g:
+        with pytest.raises(TaskGraphError) as e:
+            g.register_kernel(3, tmp_path / "missing.hsaco", "tg_axpb")
+        assert e.value.rc == -2
+        with pytest.raises(TaskGraphError) as e:
+            g.register_kernel(3, user_code_object, "no_such_kernel")
+        assert e.value.rc == -2
+
+
+# ---- whole-step replay (GRAPH mode) --------------------------------------------------------------------
+
+def test_orchestration_step_replays_until_its_tables_change(device):
+    print("[case] tg paged attention step replay", flush=True)
+    case = make_case("cfg1_small")
+    d = case.to(device)
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    tensors = _pa_tensors(case, d) + [ct(out)]
+    q0 = d.query.clone()
+    with TaskGraph("graph") as g:
+        def step(expect_replays):
+            g.reset()
+            out.fill_(float("nan"))
+            torch.cuda.synchronize(device)
+            g.orchestrate_paged_attention(tensors, case.scale)
+            assert g.replay_count == expect_replays
+            g.launch()
+            g.wait()
+            return out.cpu().numpy()
+
+        assert_close(step(0), oracle_numpy(case), what="first step")
+        assert_close(step(1), oracle_numpy(case), what="replayed step")
+        assert g.task_count == 2 * (1 + 4 * 4)
+        # new query values at the same address: the key holds; the graph reads them
+        d.query.copy_((q0.float() * -0.75).to(torch.bfloat16))
+        case.query = d.query.cpu()
+        assert_close(step(2), oracle_numpy(case), what="replay, new query values")
+        # a shorter context: the tables changed, so the step is orchestrated again
+        d.context_lens[1] = 300
+        case.context_lens = d.context_lens.cpu()
+        assert_close(step(2), oracle_numpy(case), what="new tables")
+        assert g.task_count == 2 + 4 * 4 + 4 * 3
+        assert_close(step(3), oracle_numpy(case), what="replay of the new tables")
+
+
+def test_eager_graphs_do_not_replay(device):
+    case = make_case("cfg1_small")
+    d = case.to(device)
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    with TaskGraph("eager") as g:
+        for _ in range(2):
+            g.reset()
+            g.orchestrate_paged_attention(_pa_tensors(case, d) + [ct(out)], case.scale)
+            g.wait()
+        assert g.replay_count == 0
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what="eager")
