@@ -55,6 +55,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-other-configs", action="store_true",
                    help="default config only: skip timing the other configs in the same run")
+    p.add_argument("--q-len", type=int, default=0, help="shape variant: query tokens per sequence (0 = the config's)")
+    p.add_argument("--num-heads", type=int, default=0, help="shape variant: query heads (0 = the config's)")
+    p.add_argument("--causal", type=int, default=-1, choices=[-1, 0, 1],
+                   help="shape variant: causal multi-token decode (-1 = the config's)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample duration")
     p.add_argument("--cpu-threads", type=int, default=0,
                    help="0 = every CPU this process may use, capped at OMP_NUM_THREADS when set (the box's share)")
@@ -64,6 +68,25 @@ def parse() -> argparse.Namespace:
                    help="before the timed region, run 3 device copies of this many MiB (a kernel of known "
                         "traffic that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE in the same run)")
     return p.parse_args()
+
+
+def variant_config(cfg, args):
+    """The config with the shape overrides of --q-len / --num-heads / --causal
+    (same seed and draw order, so the context lengths and block table stay
+    the config's); its name records them."""
+    import dataclasses
+
+    changes, tags = {}, []
+    if args.q_len > 0 and args.q_len != cfg.q_len:
+        changes["q_len"], tags = args.q_len, tags + [f"q_len={args.q_len}"]
+    if args.num_heads > 0 and args.num_heads != cfg.num_heads:
+        changes["num_heads"], tags = args.num_heads, tags + [f"heads={args.num_heads}"]
+    if args.causal >= 0 and bool(args.causal) != cfg.causal:
+        changes["causal"], tags = bool(args.causal), tags + [f"causal={args.causal}"]
+    if not changes:
+        return cfg
+    name = f"{cfg.name}[{','.join(tags)}]"
+    return dataclasses.replace(cfg, name=name, description=f"{cfg.description}; variant {','.join(tags)}", **changes)
 
 
 def time_decode(case, out, num_workers: int, dev, steps: int, warmup: int) -> dict:
@@ -630,7 +653,7 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda", 0)
-    cfg = CONFIGS[args.config]
+    cfg = variant_config(CONFIGS[args.config], args)
     print(f"[bench] generating {cfg.name}: {cfg.description}", file=sys.stderr, flush=True)
     case_cpu = make_case(cfg)
     case = case_cpu.to(dev)

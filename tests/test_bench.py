@@ -71,3 +71,24 @@ def test_other_configs_are_timed_in_the_same_run(device, monkeypatch):
     for r in res.values():
         assert r["main_us"] > 0 and r["step_us"] >= 0.9 * r["main_us"] and 0 < r["frac"] < 1
         assert r["kernel"].startswith("pa_") and r["workers"] >= 1
+
+
+def test_shape_variants_keep_the_configs_draws():
+    # --q-len / --num-heads / --causal change the shape, keep the seed (so the
+    # context lengths and block table), and name the variant
+    sys.path.insert(0, str(ROOT))
+    import argparse
+
+    import bench
+    from simpler_amd.workloads import CONFIGS, make_case
+
+    base = CONFIGS["cfg5_verify"]
+    ns = argparse.Namespace(q_len=1, num_heads=0, causal=-1)
+    v = bench.variant_config(base, ns)
+    assert v.name == "cfg5_verify[q_len=1]" and v.q_len == 1 and v.num_heads == base.num_heads and v.causal
+    assert v.index == base.index
+    a, b = make_case(base), make_case(v)
+    assert a.seed == b.seed
+    assert a.context_lens.tolist() == b.context_lens.tolist() and a.block_table.equal(b.block_table)
+    same = bench.variant_config(base, argparse.Namespace(q_len=0, num_heads=0, causal=-1))
+    assert same is base
