@@ -343,39 +343,57 @@ __device__ __forceinline__ int list_of_tile(const KernelParams &P, int g, int b)
     return ((g - b) % P.lanes + P.lanes) % P.lanes;
 }
 
+// Work of sequence b for the scans below: (blocks + seg_cost) * tiles per
+// batch, 0 for an empty context or past the batch. The length is loaded from a
+// clamped index and selected, so the loads of several sequences carry no
+// branch between them and stay in flight together.
+__device__ __forceinline__ int work_of(const KernelParams &P, const int b, const int tpb) {
+    const int len = P.context_lens[b < P.batch ? b : 0];
+    const int ctx = min(max(len, 0), P.max_blocks * P.block_size);
+    const int nbb = b < P.batch ? (ctx + P.block_size - 1) / P.block_size : 0;
+    return nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
+}
+
 // Wave-level scan over the batch for one list. Work of batch b = (blocks_of(b)
 // + seg_cost) * lane_tiles, or 0 for an empty context. Returns the total
 // work; if `want_b` >= 0, *prefix_of_want = work before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
 // *prefix_of_pos = the batch whose work range contains pos and the work before
-// it. `pos` may be given as a fraction of the total (pos_num / pos_den of it,
-// rounded up to whole chunks) so that one pass suffices. All results are
-// wave-uniform. One context_lens load per 64 sequences.
+// it. All results are wave-uniform. The lengths of up to kScanGroup chunks of
+// 64 sequences are loaded together before they are scanned, so a batch of up
+// to 512 sequences costs one memory round trip.
+constexpr int kScanGroup = 8;
 __device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
                          int *prefix_of_pos) {
     const int lane = threadIdx.x & 63;
     const int tpb = lane_tiles(P);
     int carry = 0;
-    for (int base = 0; base < P.batch; base += 64) {
-        const int b = base + lane;
-        const int nbb = b < P.batch ? blocks_of(P, b) : 0;
-        const int cnt = nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
-        int incl = cnt;
+    for (int base0 = 0; base0 < P.batch; base0 += 64 * kScanGroup) {
+        int cnts[kScanGroup];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += y;
-        }
-        const int excl = carry + incl - cnt;
-        if (want_b >= base && want_b < base + 64) *prefix_of_want = __shfl(excl, want_b - base, 64);
-        if (pos >= 0) {
-            const unsigned long long hit = __ballot(cnt > 0 && pos >= excl && pos < excl + cnt);
-            if (hit) {
-                const int src = __ffsll((long long)hit) - 1;
-                *b_of_pos = base + src;
-                *prefix_of_pos = __shfl(excl, src, 64);
+        for (int k = 0; k < kScanGroup; ++k) cnts[k] = work_of(P, base0 + 64 * k + lane, tpb);
+#pragma unroll
+        for (int k = 0; k < kScanGroup; ++k) {
+            const int base = base0 + 64 * k;
+            if (base >= P.batch) break;  // wave-uniform
+            const int cnt = cnts[k];
+            int incl = cnt;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += y;
             }
+            const int excl = carry + incl - cnt;
+            if (want_b >= base && want_b < base + 64) *prefix_of_want = __shfl(excl, want_b - base, 64);
+            if (pos >= 0) {
+                const unsigned long long hit = __ballot(cnt > 0 && pos >= excl && pos < excl + cnt);
+                if (hit) {
+                    const int src = __ffsll((long long)hit) - 1;
+                    *b_of_pos = base + src;
+                    *prefix_of_pos = __shfl(excl, src, 64);
+                }
+            }
+            carry += __shfl(incl, 63, 64);
         }
-        carry += __shfl(incl, 63, 64);
     }
     return carry;
 }
