@@ -407,3 +407,60 @@ def test_eager_graphs_do_not_replay(device):
             g.wait()
         assert g.replay_count == 0
     assert_close(out.cpu().numpy(), oracle_numpy(case), what="eager")
+
+
+def test_user_step_with_registered_kernels_replays(device, user_code_object):
+    # A caller's own step (two registered kernels and a built-in) recorded under
+    # a key, then replayed on reset graphs: new input values at the same
+    # addresses flow through; a different key orchestrates again.
+    print("[case] tg user step record/replay", flush=True)
+    rng = np.random.default_rng(12)
+    x = torch.from_numpy(rng.standard_normal((4, 64)).astype(np.float32)).to(device)
+    b = torch.from_numpy(rng.standard_normal((4, 64)).astype(np.float32)).to(device)
+    s = torch.from_numpy(rng.standard_normal(4).astype(np.float32)).to(device)
+    out = torch.zeros((4, 64), dtype=torch.float32, device=device)
+    with TaskGraph("graph") as g:
+        g.register_kernel(10, user_code_object, "tg_axpb", block_threads=256, grid_tensor=2, elems_per_workgroup=256)
+        g.register_kernel(11, user_code_object, "tg_row_scale", block_threads=128, grid_tensor=2,
+                          elems_per_workgroup=128)
+        g.bind(12, IncoreKernel.VEC_ADD)
+
+        def step(alpha: float) -> None:
+            key = f"axpb-rowscale-add alpha={alpha}".encode()
+            g.reset()
+            if not g.replay(key):
+                a0 = CoreTaskArgs()
+                a0.add_input(ct(x), ct(b))
+                a0.add_output(TensorCreateInfo((4, 64), DataType.FLOAT32))
+                a0.add_scalar(float(alpha))
+                y0 = g.submit_task(10, a0).get_ref(0)
+                a1 = CoreTaskArgs()
+                a1.add_input(y0, ct(s))
+                a1.add_output(TensorCreateInfo((4, 64), DataType.FLOAT32))
+                y1 = g.submit_task(11, a1).get_ref(0)
+                a2 = CoreTaskArgs()
+                a2.add_input(y1, ct(x))
+                a2.add_output(ct(out))
+                g.submit_task(12, a2)
+                g.record_replay(key)
+            g.launch()
+            g.wait()
+
+        def want(alpha: float) -> np.ndarray:
+            xn, bn, sn = x.cpu().numpy(), b.cpu().numpy(), s.cpu().numpy()
+            return (np.float32(alpha) * xn + bn) * sn[:, None] + xn
+
+        step(2.0)
+        np.testing.assert_allclose(out.cpu().numpy(), want(2.0), rtol=1e-6, atol=1e-6)
+        assert g.replay_count == 0
+        x.mul_(-1.5)  # new values, same address: the recorded step still applies
+        out.fill_(float("nan"))
+        step(2.0)
+        assert g.replay_count == 1 and g.task_count == 3
+        np.testing.assert_allclose(out.cpu().numpy(), want(2.0), rtol=1e-6, atol=1e-6)
+        step(0.5)  # another key: orchestrated and recorded again
+        assert g.replay_count == 1
+        np.testing.assert_allclose(out.cpu().numpy(), want(0.5), rtol=1e-6, atol=1e-6)
+        step(0.5)
+        assert g.replay_count == 2
+        np.testing.assert_allclose(out.cpu().numpy(), want(0.5), rtol=1e-6, atol=1e-6)
