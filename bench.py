@@ -92,8 +92,12 @@ def variant_config(cfg, args):
 def time_decode(case, out, num_workers: int, dev, steps: int, warmup: int) -> dict:
     """Time one decode config on device-resident inputs: `steps` back-to-back
     calls between two events on the launch stream (the step: main + merge
-    kernels), then the main kernel alone, with events around each main launch
-    (its merge kernel still runs after it, outside the events)."""
+    kernels), then the main kernel alone: `steps` back-to-back main launches
+    between two events (each writes the same partials and outputs; one merge
+    after them leaves the output complete). Back to back is how a serving loop
+    runs it: events around every launch would add their own overhead and let
+    the clock recover between launches (the MLA kernel runs 11% faster after
+    an idle gap)."""
     import torch
 
     from simpler_amd import paged_attention as pa
@@ -119,18 +123,18 @@ def time_decode(case, out, num_workers: int, dev, steps: int, warmup: int) -> di
     wall = time.perf_counter() - t0
     step_ms = start.elapsed_time(end) / steps
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)  # one untimed split step first
     pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
     torch.cuda.synchronize(dev)
-    for e0, e1 in evs:
-        e0.record(stream)
+    m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    m0.record(stream)
+    for _ in range(steps):
         pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MAIN)
-        e1.record(stream)
-        pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
+    m1.record(stream)
+    pa.launch(pargs, dev, stream.cuda_stream, phases=pa.PHASE_MERGE)
     torch.cuda.synchronize(dev)
     pa.check_errors(dev)
-    main_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / steps
+    main_ms = m0.elapsed_time(m1) / steps
     print(f"[bench] {cfg.name}: {step_ms * 1e3:.1f} us/step, main kernel {main_ms * 1e3:.1f} us, "
           f"wall {wall:.3f} s", file=sys.stderr, flush=True)
     return {"step_ms": step_ms, "main_ms": main_ms, "wall_s": wall, "workers": pa.plan(pargs),
