@@ -312,9 +312,18 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
     const int64_t cap = (int64_t)P.max_blocks * P.block_size;
     const int lo = (P.causal || P.k_new) ? P.q_len : 0;  // an appended context holds its new tokens
     bool bad = false;
-    for (int b = lane; b < P.batch; b += 64) {
-        const int len = P.context_lens[b];
-        bad |= len < lo || (int64_t)len > cap;
+    for (int base0 = 0; base0 < P.batch; base0 += 64 * 8) {  // eight loads in flight together
+        int lens[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int b = base0 + 64 * k + lane;
+            lens[k] = P.context_lens[b < P.batch ? b : 0];
+        }
+        asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
+                     "+v"(lens[6]), "+v"(lens[7]));
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            bad |= base0 + 64 * k + lane < P.batch && (lens[k] < lo || (int64_t)lens[k] > cap);
     }
     if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
 }
@@ -343,12 +352,9 @@ __device__ __forceinline__ int list_of_tile(const KernelParams &P, int g, int b)
     return ((g - b) % P.lanes + P.lanes) % P.lanes;
 }
 
-// Work of sequence b for the scans below: (blocks + seg_cost) * tiles per
-// batch, 0 for an empty context or past the batch. The length is loaded from a
-// clamped index and selected, so the loads of several sequences carry no
-// branch between them and stay in flight together.
-__device__ __forceinline__ int work_of(const KernelParams &P, const int b, const int tpb) {
-    const int len = P.context_lens[b < P.batch ? b : 0];
+// Work of sequence b (raw length len) for the scans below: (blocks +
+// seg_cost) * tiles per batch, 0 for an empty context or past the batch.
+__device__ __forceinline__ int work_of(const KernelParams &P, const int b, const int len, const int tpb) {
     const int ctx = min(max(len, 0), P.max_blocks * P.block_size);
     const int nbb = b < P.batch ? (ctx + P.block_size - 1) / P.block_size : 0;
     return nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
@@ -367,10 +373,23 @@ __device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_o
     const int lane = threadIdx.x & 63;
     const int tpb = lane_tiles(P);
     int carry = 0;
+    static_assert(kScanGroup == 8, "the load fence below names each length");
     for (int base0 = 0; base0 < P.batch; base0 += 64 * kScanGroup) {
+        // Lengths from clamped indices, all loaded before any is used: the
+        // empty asm needs all eight, so the compiler can neither sink a load
+        // into the past-the-batch branch of work_of nor wait for each in turn
+        // (one memory round trip, not eight).
+        int lens[kScanGroup];
+#pragma unroll
+        for (int k = 0; k < kScanGroup; ++k) {
+            const int b = base0 + 64 * k + lane;
+            lens[k] = P.context_lens[b < P.batch ? b : 0];
+        }
+        asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
+                     "+v"(lens[6]), "+v"(lens[7]));
         int cnts[kScanGroup];
 #pragma unroll
-        for (int k = 0; k < kScanGroup; ++k) cnts[k] = work_of(P, base0 + 64 * k + lane, tpb);
+        for (int k = 0; k < kScanGroup; ++k) cnts[k] = work_of(P, base0 + 64 * k + lane, lens[k], tpb);
 #pragma unroll
         for (int k = 0; k < kScanGroup; ++k) {
             const int base = base0 + 64 * k;
