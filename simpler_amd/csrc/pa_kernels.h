@@ -312,7 +312,11 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
     const int64_t cap = (int64_t)P.max_blocks * P.block_size;
     const int lo = (P.causal || P.k_new) ? P.q_len : 0;  // an appended context holds its new tokens
     bool bad = false;
-    for (int base0 = 0; base0 < P.batch; base0 += 64 * 8) {  // eight loads in flight together
+    if (P.batch <= 64) {
+        const int len = lane < P.batch ? P.context_lens[lane] : 0;
+        bad = lane < P.batch && (len < lo || (int64_t)len > cap);
+    }
+    for (int base0 = 0; P.batch > 64 && base0 < P.batch; base0 += 64 * 8) {  // eight loads in flight together
         int lens[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -360,55 +364,72 @@ __device__ __forceinline__ int work_of(const KernelParams &P, const int b, const
     return nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
 }
 
+constexpr int kScanGroup = 8;
+
+// The raw lengths of sequences base0 + 64 k + lane (k < kScanGroup), from
+// clamped indices and all loaded before any is used: the empty asm needs all
+// eight, so the compiler can neither sink a load into the past-the-batch
+// branch of work_of nor wait for each in turn (one memory round trip, not
+// eight).
+__device__ __forceinline__ void load_lengths(const KernelParams &P, const int base0, int (&lens)[kScanGroup]) {
+    static_assert(kScanGroup == 8, "the load fence below names each length");
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kScanGroup; ++k) {
+        const int b = base0 + 64 * k + lane;
+        lens[k] = P.context_lens[b < P.batch ? b : 0];
+    }
+    asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
+                 "+v"(lens[6]), "+v"(lens[7]));
+}
+
+// Inclusive wave scan of x.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
 // Wave-level scan over the batch for one list. Work of batch b = (blocks_of(b)
 // + seg_cost) * lane_tiles, or 0 for an empty context. Returns the total
-// work; if `want_b` >= 0, *prefix_of_want = work before batch want_b; if `pos` >= 0 (and < total), *b_of_pos /
-// *prefix_of_pos = the batch whose work range contains pos and the work before
-// it. All results are wave-uniform. The lengths of up to kScanGroup chunks of
-// 64 sequences are loaded together before they are scanned, so a batch of up
-// to 512 sequences costs one memory round trip.
-constexpr int kScanGroup = 8;
-__device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int pos, int *b_of_pos,
-                         int *prefix_of_pos) {
+// work; if `want_b` >= 0, *prefix_of_want = work before batch want_b and
+// *ctx_of_want = its clamped length (ctx_of); if `pos` >= 0 (and < total),
+// *b_of_pos / *prefix_of_pos / *ctx_of_pos = the batch whose work range
+// contains pos, the work before it and its clamped length. All results are
+// wave-uniform. Each group of up to 64 * kScanGroup sequences costs one memory
+// round trip.
+__device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_of_want, int *ctx_of_want, int pos,
+                                int *b_of_pos, int *prefix_of_pos, int *ctx_of_pos) {
     const int lane = threadIdx.x & 63;
     const int tpb = lane_tiles(P);
+    const int cap = P.max_blocks * P.block_size;
     int carry = 0;
-    static_assert(kScanGroup == 8, "the load fence below names each length");
     for (int base0 = 0; base0 < P.batch; base0 += 64 * kScanGroup) {
-        // Lengths from clamped indices, all loaded before any is used: the
-        // empty asm needs all eight, so the compiler can neither sink a load
-        // into the past-the-batch branch of work_of nor wait for each in turn
-        // (one memory round trip, not eight).
         int lens[kScanGroup];
-#pragma unroll
-        for (int k = 0; k < kScanGroup; ++k) {
-            const int b = base0 + 64 * k + lane;
-            lens[k] = P.context_lens[b < P.batch ? b : 0];
-        }
-        asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
-                     "+v"(lens[6]), "+v"(lens[7]));
-        int cnts[kScanGroup];
-#pragma unroll
-        for (int k = 0; k < kScanGroup; ++k) cnts[k] = work_of(P, base0 + 64 * k + lane, lens[k], tpb);
+        load_lengths(P, base0, lens);
 #pragma unroll
         for (int k = 0; k < kScanGroup; ++k) {
             const int base = base0 + 64 * k;
             if (base >= P.batch) break;  // wave-uniform
-            const int cnt = cnts[k];
-            int incl = cnt;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int y = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += y;
-            }
+            const int cnt = work_of(P, base + lane, lens[k], tpb);
+            const int incl = wave_incl_scan(cnt);
             const int excl = carry + incl - cnt;
-            if (want_b >= base && want_b < base + 64) *prefix_of_want = __shfl(excl, want_b - base, 64);
+            const int ctx = min(max(lens[k], 0), cap);
+            if (want_b >= base && want_b < base + 64) {
+                *prefix_of_want = __shfl(excl, want_b - base, 64);
+                *ctx_of_want = __shfl(ctx, want_b - base, 64);
+            }
             if (pos >= 0) {
                 const unsigned long long hit = __ballot(cnt > 0 && pos >= excl && pos < excl + cnt);
                 if (hit) {
                     const int src = __ffsll((long long)hit) - 1;
                     *b_of_pos = base + src;
                     *prefix_of_pos = __shfl(excl, src, 64);
+                    *ctx_of_pos = __shfl(ctx, src, 64);
                 }
             }
             carry += __shfl(incl, 63, 64);
@@ -417,40 +438,69 @@ __device__ inline int scan_work(const KernelParams &P, int want_b, int *prefix_o
     return carry;
 }
 
-// Slice c of a list (the list's c-th worker), in one pass over the batch when
-// there are at most 64 sequences: total work, then the batch containing
-// c*chunk.
+// Slice c of a list (the list's c-th worker): [*start, *end) of its work
+// units, and the batch holding *start with the work before it and its clamped
+// length. Up to 64 * kScanGroup sequences take one memory round trip: their
+// lengths stay in registers between the total and the search for the start
+// (up to 64, one per lane).
 __device__ inline int locate_slice(const KernelParams &P, int c, int *start, int *end, int *b_of_start,
-                            int *prefix_of_start) {
+                                   int *prefix_of_start, int *ctx_of_start) {
     const int lane = threadIdx.x & 63;
     const int per_list = max(P.workers / P.lanes, 1);
-    if (P.batch > 64) {
-        const int total = scan_work(P, -1, nullptr, -1, nullptr, nullptr);
+    if (P.batch > 64 * kScanGroup) {
+        const int total = scan_work(P, -1, nullptr, nullptr, -1, nullptr, nullptr, nullptr);
         const int chunk = (total + per_list - 1) / per_list;
         *start = c * chunk;
         *end = min(*start + chunk, total);
-        if (*start < *end) scan_work(P, -1, nullptr, *start, b_of_start, prefix_of_start);
+        if (*start < *end) scan_work(P, -1, nullptr, nullptr, *start, b_of_start, prefix_of_start, ctx_of_start);
         return total;
     }
     const int tpb = lane_tiles(P);
-    const int nbl = lane < P.batch ? blocks_of(P, lane) : 0;
-    const int cnt = nbl > 0 ? (nbl + P.seg_cost) * tpb : 0;
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
+    const int cap = P.max_blocks * P.block_size;
+    if (P.batch <= 64) {  // one length per lane
+        const int ctxl = lane < P.batch ? min(max(P.context_lens[lane], 0), cap) : 0;
+        const int nbl = (ctxl + P.block_size - 1) / P.block_size;
+        const int cnt = nbl > 0 ? (nbl + P.seg_cost) * tpb : 0;
+        const int incl = wave_incl_scan(cnt);
+        const int total = __shfl(incl, 63, 64);
+        const int chunk = (total + per_list - 1) / per_list;
+        *start = c * chunk;
+        *end = min(*start + chunk, total);
+        const int excl = incl - cnt;
+        const unsigned long long hit = __ballot(cnt > 0 && *start >= excl && *start < excl + cnt);
+        if (hit) {
+            const int src = __ffsll((long long)hit) - 1;
+            *b_of_start = src;
+            *prefix_of_start = __shfl(excl, src, 64);
+            *ctx_of_start = __shfl(ctxl, src, 64);
+        }
+        return total;
     }
-    const int total = __shfl(incl, 63, 64);
+    int lens[kScanGroup], cnts[kScanGroup], excl[kScanGroup];
+    load_lengths(P, 0, lens);
+    int carry = 0;
+#pragma unroll
+    for (int k = 0; k < kScanGroup; ++k) {
+        cnts[k] = work_of(P, 64 * k + lane, lens[k], tpb);  // 0 past the batch
+        excl[k] = carry;
+        if (64 * k >= P.batch) continue;  // wave-uniform
+        const int incl = wave_incl_scan(cnts[k]);
+        excl[k] = carry + incl - cnts[k];
+        carry += __shfl(incl, 63, 64);
+    }
+    const int total = carry;
     const int chunk = (total + per_list - 1) / per_list;
     *start = c * chunk;
     *end = min(*start + chunk, total);
-    const int excl = incl - cnt;
-    const unsigned long long hit = __ballot(cnt > 0 && *start >= excl && *start < excl + cnt);
-    if (hit) {
-        const int src = __ffsll((long long)hit) - 1;
-        *b_of_start = src;
-        *prefix_of_start = __shfl(excl, src, 64);
+#pragma unroll
+    for (int k = 0; k < kScanGroup; ++k) {
+        const unsigned long long hit = __ballot(cnts[k] > 0 && *start >= excl[k] && *start < excl[k] + cnts[k]);
+        if (hit) {
+            const int src = __ffsll((long long)hit) - 1;
+            *b_of_start = 64 * k + src;
+            *prefix_of_start = __shfl(excl[k], src, 64);
+            *ctx_of_start = __shfl(min(max(lens[k], 0), cap), src, 64);
+        }
     }
     return total;
 }
@@ -1416,8 +1466,8 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     char *const klds = MAXW == 1 ? klds1 : klds_waves + wave * (BS * 256);
     const int tpb = lane_tiles(P);
     const int list = w % P.lanes;
-    int start = 0, end = 0, b = 0, prefix = 0;
-    locate_slice(P, w / P.lanes, &start, &end, &b, &prefix);
+    int start = 0, end = 0, b = 0, prefix = 0, ctx0 = 0;
+    locate_slice(P, w / P.lanes, &start, &end, &b, &prefix, &ctx0);
     // wave-uniform values (cross-lane results), kept in scalar registers so that
     // block-table and scale reads derived from them are scalar loads
     start = __builtin_amdgcn_readfirstlane(start);
@@ -1425,7 +1475,7 @@ __global__ void __launch_bounds__(64 * MAXW) pa_decode_kernel(const KernelParams
     b = __builtin_amdgcn_readfirstlane(b);
     prefix = __builtin_amdgcn_readfirstlane(prefix);
     if (start >= end) return;
-    int ctx = __builtin_amdgcn_readfirstlane(ctx_of(P, b));  // the segment's sequence, read once
+    int ctx = __builtin_amdgcn_readfirstlane(ctx0);  // the segment's sequence
     int nb = (ctx + BS - 1) / BS;
     if (nb == 0) return;  // not reached: the batch holding `start` has work
     const int rel = start - prefix;
@@ -1499,8 +1549,9 @@ __global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const Ker
     const int list = list_of_tile(P, jt / lane_tiles(P), b), j = jt - (jt / lane_tiles(P)) * lane_tiles(P);
     const int rows_here = min(16, P.rows - rt * 16);
     int prefix = 0;
-    const int total = scan_work(P, b, &prefix, -1, nullptr, nullptr);
-    const int nb = blocks_of(P, b);
+    int ctxb = 0;
+    const int total = scan_work(P, b, &prefix, &ctxb, -1, nullptr, nullptr, nullptr);
+    const int nb = (ctxb + P.block_size - 1) / P.block_size;
     if (nb == 0) {  // empty context: defined as a zero output
         for (int idx = tid; idx < rows_here * (DV / 4); idx += MT) {
             const int row = idx / (DV / 4), c4 = idx - row * (DV / 4);
@@ -2130,15 +2181,15 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     int slice = 0, rgrp = 0;
     mla_worker(blockIdx.x, P.workers, groups, &slice, &rgrp);
     const int tpb = P.kv_heads;  // work-list tiles per batch
-    int start = 0, end = 0, b = 0, prefix = 0;
-    locate_slice(P, slice, &start, &end, &b, &prefix);  // identical in every wave
+    int start = 0, end = 0, b = 0, prefix = 0, ctx0 = 0;
+    locate_slice(P, slice, &start, &end, &b, &prefix, &ctx0);  // identical in every wave
     // wave-uniform values, kept in scalar registers
     start = __builtin_amdgcn_readfirstlane(start);
     end = __builtin_amdgcn_readfirstlane(end);
     b = __builtin_amdgcn_readfirstlane(b);
     prefix = __builtin_amdgcn_readfirstlane(prefix);
     if (start >= end) return;
-    int nb = blocks_of(P, b);
+    int nb = (__builtin_amdgcn_readfirstlane(ctx0) + BS - 1) / BS;
     if (nb == 0) return;
     // Work units: each (batch, kv head) tile takes seg_cost units, then one
     // per block. The slice [start, end) runs the blocks whose units it holds.
