@@ -535,6 +535,32 @@ def test_bad_device_lengths_are_reported_then_next_run_is_good(bad, device):
     assert_close(out.cpu().numpy(), oracle_numpy(case), what=f"good run after {bad}")
 
 
+@pytest.mark.parametrize("batch, bad_at, workers", [(100, 97, 0), (300, 5, 0), (600, 590, 0), (600, 70, 333)])
+def test_bad_device_length_found_in_a_large_batch(batch, bad_at, workers, device):
+    """Batches above 64 sequences check and scan their lengths in groups of
+    512 (one load round trip per group): a bad length anywhere in the batch is
+    reported, and the next call with good lengths matches the oracle."""
+    print(f"[case] bad length at {bad_at} of {batch}, workers={workers}", flush=True)
+    lens = [(7 * i) % 50 + 1 for i in range(batch)]
+    case = make_custom_case(batch=batch, num_heads=8, kv_heads=4, head_dim=32, block_size=16, context_lens=lens,
+                            seed=952)
+    d = case.to(device)
+    bad_lens = d.context_lens.clone()
+    bad_lens[bad_at] = -3
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, bad_lens, out, case.scale,
+                              num_workers=workers)
+    torch.cuda.synchronize(device)
+    with pytest.raises(pa.PagedAttentionError) as ei:
+        pa.check_errors(device)
+    assert ei.value.rc == -7
+    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out, case.scale,
+                              num_workers=workers)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what=f"batch {batch} workers {workers}")
+
+
 def test_mla_bad_device_length_is_reported(device):
     case = _mla_case(heads=128, lens=[200, 70], seed=951)
     d = case.to(device)
