@@ -1529,11 +1529,16 @@ template <int DV> constexpr int merge_threads() { return DV * 4 < 512 ? (DV * 4 
 constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weights
 
 template <int DV, typename OutT>
-__global__ void __launch_bounds__(merge_threads<DV>()) pa_merge_kernel(const KernelParams P) {
+// MLA (DV = 512): every tile of a launch is cut, and 1024 of them (cfg4) fit
+// the chip at once only at eight waves per SIMD, i.e. 64 registers, hence one
+// piece read ahead (measured 24.9 -> 23.2 us against two waves per SIMD with
+// four read ahead).
+__global__ void __launch_bounds__(merge_threads<DV>()) __attribute__((amdgpu_waves_per_eu(DV >= 512 ? 8 : 1)))
+pa_merge_kernel(const KernelParams P) {
     constexpr int MT = merge_threads<DV>();
-    constexpr int UNITS = 16 * (DV / 4);            // 16-byte units of a full tile
-    constexpr int UPT = (UNITS + MT - 1) / MT;      // units per thread
-    constexpr int PRE = UPT == 1 ? 8 : 4;           // pieces per unit read before the weights are known
+    constexpr int UNITS = 16 * (DV / 4);        // 16-byte units of a full tile
+    constexpr int UPT = (UNITS + MT - 1) / MT;  // units per thread
+    constexpr int PRE = UPT == 1 ? 8 : (DV >= 512 ? 1 : 4);  // pieces per unit read before the weights are known
     const int tid = threadIdx.x;
     // The main kernel is done: hand its error word to the host through
     // pinned memory (a run's wait then needs no device-to-host copy).
