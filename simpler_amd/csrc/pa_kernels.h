@@ -1531,7 +1531,7 @@ constexpr int kMergeLdsPieces = 32;  // pieces per tile merged through LDS weigh
 template <int DV, typename OutT>
 // MLA (DV = 512): every tile of a launch is cut, and 1024 of them (cfg4) fit
 // the chip at once only at eight waves per SIMD, i.e. 64 registers, hence one
-// piece read ahead (measured 24.9 -> 23.2 us against two waves per SIMD with
+// piece read ahead (measured 24.9 -> 23.2 us against four waves per SIMD with
 // four read ahead).
 __global__ void __launch_bounds__(merge_threads<DV>()) __attribute__((amdgpu_waves_per_eu(DV >= 512 ? 8 : 1)))
 pa_merge_kernel(const KernelParams P) {
