@@ -301,6 +301,25 @@ __device__ __forceinline__ int blocks_of(const KernelParams &P, int b) {
 constexpr unsigned kErrBadBlock = 1u;   // a block_table entry outside the pool (that block is skipped)
 constexpr unsigned kErrBadLength = 2u;  // a context_lens entry the kernels had to clamp
 
+constexpr int kScanGroup = 8;
+
+// The raw lengths of sequences base0 + 64 k + lane (k < kScanGroup), from
+// clamped indices and all loaded before any is used: the empty asm needs all
+// eight, so the compiler can neither sink a load into the past-the-batch
+// branch that uses it nor wait for each in turn (one memory round trip, not
+// eight).
+__device__ __forceinline__ void load_lengths(const KernelParams &P, const int base0, int (&lens)[kScanGroup]) {
+    static_assert(kScanGroup == 8, "the load fence below names each length");
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kScanGroup; ++k) {
+        const int b = base0 + 64 * k + lane;
+        lens[k] = P.context_lens[b < P.batch ? b : 0];
+    }
+    asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
+                 "+v"(lens[6]), "+v"(lens[7]));
+}
+
 // One wave of the grid (wave 0 of workgroup 0) checks every raw length: below
 // 0, above what the block-table row holds, or (causal) shorter than the query.
 // With a fused append, a length below q_len cannot hold the new tokens. The
@@ -316,17 +335,11 @@ __device__ __forceinline__ void flag_bad_lengths(const KernelParams &P) {
         const int len = lane < P.batch ? P.context_lens[lane] : 0;
         bad = lane < P.batch && (len < lo || (int64_t)len > cap);
     }
-    for (int base0 = 0; P.batch > 64 && base0 < P.batch; base0 += 64 * 8) {  // eight loads in flight together
-        int lens[8];
+    for (int base0 = 0; P.batch > 64 && base0 < P.batch; base0 += 64 * kScanGroup) {
+        int lens[kScanGroup];
+        load_lengths(P, base0, lens);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int b = base0 + 64 * k + lane;
-            lens[k] = P.context_lens[b < P.batch ? b : 0];
-        }
-        asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
-                     "+v"(lens[6]), "+v"(lens[7]));
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < kScanGroup; ++k)
             bad |= base0 + 64 * k + lane < P.batch && (lens[k] < lo || (int64_t)lens[k] > cap);
     }
     if (__ballot(bad) && lane == 0) atomicOr(P.error_flag, kErrBadLength);
@@ -364,33 +377,17 @@ __device__ __forceinline__ int work_of(const KernelParams &P, const int b, const
     return nbb > 0 ? (nbb + P.seg_cost) * tpb : 0;
 }
 
-constexpr int kScanGroup = 8;
-
-// The raw lengths of sequences base0 + 64 k + lane (k < kScanGroup), from
-// clamped indices and all loaded before any is used: the empty asm needs all
-// eight, so the compiler can neither sink a load into the past-the-batch
-// branch of work_of nor wait for each in turn (one memory round trip, not
-// eight).
-__device__ __forceinline__ void load_lengths(const KernelParams &P, const int base0, int (&lens)[kScanGroup]) {
-    static_assert(kScanGroup == 8, "the load fence below names each length");
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int k = 0; k < kScanGroup; ++k) {
-        const int b = base0 + 64 * k + lane;
-        lens[k] = P.context_lens[b < P.batch ? b : 0];
-    }
-    asm volatile("" : "+v"(lens[0]), "+v"(lens[1]), "+v"(lens[2]), "+v"(lens[3]), "+v"(lens[4]), "+v"(lens[5]),
-                 "+v"(lens[6]), "+v"(lens[7]));
-}
-
-// Inclusive wave scan of x.
+// Inclusive wave scan of x by DPP lane moves (no LDS round trips, which
+// __shfl_up takes): row_shr 1, 2, 4, 8 within each 16-lane row (lanes past a
+// row's start read 0), then row_bcast:15 adds the last lane of rows 0 and 2
+// to rows 1 and 3, and row_bcast:31 lane 31 to rows 2 and 3.
 __device__ __forceinline__ int wave_incl_scan(int x) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
     return x;
 }
 
