@@ -143,10 +143,11 @@ def time_decode(case, out, num_workers: int, dev, steps: int, warmup: int) -> di
 
 def other_configs(args, dev, skip: str) -> dict:
     """Every other benchmark config, timed in this same run (fewer steps, no CPU
-    baseline): main-kernel µs and its fraction of HBM peak, and the step µs."""
+    baseline): main-kernel µs and its fraction of HBM peak (and of the dense
+    bf16 MFMA peak), and the step µs."""
     import torch
 
-    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, make_case
+    from simpler_amd.workloads import CONFIGS, algorithmic_bytes, algorithmic_flops, make_case
 
     res = {}
     steps, warmup = max(1, min(args.steps, 50)), max(1, min(args.warmup, 5))
@@ -163,7 +164,10 @@ def other_configs(args, dev, skip: str) -> dict:
                      "frac": round(nbytes / (tm["main_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "step_us": round(tm["step_ms"] * 1e3, 2),
                      "step_frac": round(nbytes / (tm["step_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": nbytes, "steps": steps}
+                     "algorithmic_bytes": nbytes, "steps": steps,
+                     # the MFMA side of the roofline (MLA sits near the ridge)
+                     "mfma_frac": round(algorithmic_flops(case_cpu) / (tm["main_ms"] * 1e-3) / 1e12
+                                        / MFMA_BF16_PEAK_TFLOPS, 4)}
         del case, out
         torch.cuda.empty_cache()
     return res
