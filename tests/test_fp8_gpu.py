@@ -151,3 +151,15 @@ def test_fp8_through_simpler_run(device):
         assert_close(out.numpy(), oracle_fp8(case), what="fp8 worker")
     finally:
         w.close()
+
+
+def test_fp8_blocks_shared_between_sequences(device):
+    """fp8 caches with block tables that share physical blocks (and their
+    per-(block, kv head) scales) between sequences match the dequantised
+    oracle on the same table."""
+    case = fp8_case(pow2=False, batch=4, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                    context_lens=[1000, 1000, 300, 2049], seed=962)
+    bt = case.block_table
+    for b in range(1, 4):
+        bt[b, :4] = bt[0, :4]
+    assert_close(run_fp8(case, device), oracle_fp8(case), what="fp8 shared blocks")

@@ -573,3 +573,40 @@ def test_mla_bad_device_length_is_reported(device):
         pa.check_errors(device)
     assert ei.value.rc == -7
     pa.check_errors(device)
+
+
+def _share_prefix_blocks(case, shared: int, repeat_in_row: bool = False):
+    """Prefix caching / beam search: sequences 1.. point their first `shared`
+    block-table entries at sequence 0's physical blocks (and, with
+    repeat_in_row, sequence 0 reads its own first block a second time in place
+    of its last full block). The cache contents are those of the blocks the
+    table names, so the oracle reads the same bytes."""
+    bt = case.block_table
+    for b in range(1, bt.shape[0]):
+        n = min(shared, (int(case.context_lens[b]) + case.config.block_size - 1) // case.config.block_size)
+        bt[b, :n] = bt[0, :n]
+    if repeat_in_row:
+        nb0 = (int(case.context_lens[0]) + case.config.block_size - 1) // case.config.block_size
+        if nb0 > 2:
+            bt[0, nb0 - 2] = bt[0, 0]
+    return case
+
+
+@pytest.mark.parametrize("kind,workers", [("gqa", 0), ("gqa", 77), ("gqa_verify", 0), ("mla", 0), ("mla", 9)])
+def test_blocks_shared_between_sequences(kind, workers, device):
+    """Sequences whose block tables name the same physical blocks (a shared
+    prompt prefix, beam-search siblings, one block twice in a row) read those
+    blocks like any other: the result matches the oracle on the same table."""
+    print(f"[case] shared blocks {kind} workers={workers}", flush=True)
+    if kind == "mla":
+        case = _mla_case(heads=128, lens=[700, 700, 450, 1000], seed=960)
+        shared = 6
+    else:
+        q_len = 4 if kind == "gqa_verify" else 1
+        case = make_custom_case(batch=5, num_heads=32, kv_heads=8, head_dim=128, block_size=64, q_len=q_len,
+                                causal=q_len > 1, context_lens=[900, 900, 700, 1500, 65], seed=961)
+        shared = 8
+    _share_prefix_blocks(case, shared, repeat_in_row=True)
+    got = run_gpu(case, device, num_workers=workers)
+    pa.check_errors(device)
+    assert_close(got, oracle_numpy(case), what=f"shared blocks {kind} w{workers}")
