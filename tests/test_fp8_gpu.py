@@ -163,3 +163,21 @@ def test_fp8_blocks_shared_between_sequences(device):
     for b in range(1, 4):
         bt[b, :4] = bt[0, :4]
     assert_close(run_fp8(case, device), oracle_fp8(case), what="fp8 shared blocks")
+
+
+def test_fp8_fused_kv_buffer(device):
+    """fp8 K and V as the two halves of one [num_blocks, 2, bs, h, d] byte
+    buffer (strided views) match the dequantised oracle."""
+    case = fp8_case(pow2=False, batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=64,
+                    context_lens=[700, 65, 1500], seed=965)
+    k8, v8 = case.key_cache.view(torch.uint8), case.value_cache.view(torch.uint8)
+    buf = torch.full((k8.shape[0], 2, *k8.shape[1:]), 0x7F, dtype=torch.uint8)  # 0x7F: E4M3FN NaN
+    buf[:, 0], buf[:, 1] = k8, v8
+    buf = buf.to(device)
+    d = case.to(device)
+    out = torch.zeros(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, buf[:, 0], buf[:, 1], d.block_table, d.context_lens, out, case.scale,
+                              k_scale=d.k_scale, v_scale=d.v_scale)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert_close(out.cpu().numpy(), oracle_fp8(case), what="fp8 fused kv")

@@ -610,3 +610,62 @@ def test_blocks_shared_between_sequences(kind, workers, device):
     got = run_gpu(case, device, num_workers=workers)
     pa.check_errors(device)
     assert_close(got, oracle_numpy(case), what=f"shared blocks {kind} w{workers}")
+
+
+def _strided_caches(k, v, layout: str, device):
+    """Device views of the dense caches k, v [nb, bs, h, d] in another memory
+    layout, with everything the views do not cover set to NaN:
+    fused_kv: one buffer [nb, 2, bs, h, d] holding K then V of each block;
+    hnd: head-major blocks [nb, h, bs, d] seen through a permute;
+    padded: rows of d + 16 elements, the caches the first d."""
+    nb, bs, h, d = k.shape
+    if layout == "fused_kv":
+        buf = torch.full((nb, 2, bs, h, d), float("nan"), dtype=k.dtype)
+        buf[:, 0], buf[:, 1] = k, v
+        buf = buf.to(device)
+        return buf[:, 0], buf[:, 1], buf
+    if layout == "hnd":
+        kb, vb = k.permute(0, 2, 1, 3).contiguous().to(device), v.permute(0, 2, 1, 3).contiguous().to(device)
+        return kb.permute(0, 2, 1, 3), vb.permute(0, 2, 1, 3), (kb, vb)
+    assert layout == "padded"
+    kb = torch.full((nb, bs, h, d + 16), float("nan"), dtype=k.dtype)
+    vb = torch.full((nb, bs, h, v.shape[-1] + 16), float("nan"), dtype=v.dtype)
+    kb[..., :d], vb[..., : v.shape[-1]] = k, v
+    kb, vb = kb.to(device), vb.to(device)
+    return kb[..., :d], vb[..., : v.shape[-1]], (kb, vb)
+
+
+@pytest.mark.parametrize("layout", ["fused_kv", "hnd", "padded"])
+@pytest.mark.parametrize("q_len", [1, 8])
+def test_cache_layouts_through_strides(layout, q_len, device):
+    """The entry takes the caches' block, token and head strides: K and V in
+    one fused buffer, head-major blocks and padded rows give the oracle's
+    result on the dense caches, and never read the NaN padding."""
+    print(f"[case] cache layout {layout} q_len={q_len}", flush=True)
+    case = make_custom_case(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=64, q_len=q_len,
+                            causal=q_len > 1, context_lens=[700, 64 + q_len, 1500], seed=963)
+    kc, vc, _keep = _strided_caches(case.key_cache, case.value_cache, layout, device)
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, kc, vc, d.block_table, d.context_lens, out, case.scale,
+                              causal=case.config.causal)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what=f"layout {layout} q{q_len}")
+
+
+def test_mla_padded_token_rows(device):
+    """MLA with the latent cache's token rows padded past 576 elements (NaN in
+    the padding): V stays the first 512 dims of the same rows."""
+    case = _mla_case(heads=128, lens=[700, 70, 1300], seed=964)
+    nb, bs, h, dk = case.key_cache.shape
+    buf = torch.full((nb, bs, h, dk + 32), float("nan"), dtype=case.key_cache.dtype)
+    buf[..., :dk] = case.key_cache
+    buf = buf.to(device)
+    kc = buf[..., :dk]
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode(d.query, kc, kc[..., :512], d.block_table, d.context_lens, out, case.scale)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    assert_close(out.cpu().numpy(), oracle_numpy(case), what="mla padded rows")
