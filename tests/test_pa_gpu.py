@@ -669,3 +669,46 @@ def test_mla_padded_token_rows(device):
     torch.cuda.synchronize(device)
     pa.check_errors(device)
     assert_close(out.cpu().numpy(), oracle_numpy(case), what="mla padded rows")
+
+
+def test_threads_on_their_own_streams(device):
+    """Host threads calling the decode at the same time, each on a stream of
+    its own (default priority), get their own workspaces and correct results:
+    GQA and MLA shapes interleaved, several calls per thread."""
+    import threading
+
+    cases = [make_custom_case(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=128,
+                              context_lens=[900, 129, 2500], seed=966),
+             _mla_case(heads=128, lens=[300, 1100], seed=967)]
+    refs = [oracle_numpy(c) for c in cases]
+    dev_cases = [c.to(device) for c in cases]
+    results, errors_seen = {}, []
+
+    def worker(tid):
+        try:
+            s = torch.cuda.Stream(device=device)
+            outs = []
+            with torch.cuda.stream(s):
+                for i in range(6):
+                    ci = (tid + i) % 2
+                    d, c = dev_cases[ci], cases[ci]
+                    out = torch.empty(c.out_shape(), dtype=torch.float32, device=device)
+                    pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens,
+                                              out, c.scale)
+                    outs.append((ci, out))
+                s.synchronize()
+                pa.check_errors(device)
+            results[tid] = [(ci, o.cpu().numpy()) for ci, o in outs]
+        except Exception as e:  # reported below, with the thread that raised it
+            errors_seen.append((tid, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(3)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "a decode thread did not finish"
+    assert not errors_seen, errors_seen
+    for tid, outs in results.items():
+        for i, (ci, got) in enumerate(outs):
+            assert_close(got, refs[ci], what=f"thread {tid} call {i}")
