@@ -5,14 +5,16 @@ One "step" = one decode-attention call over the whole batch (one layer) of the
 Qwen3-8B-shaped GQA workload (B=32, Hq=32, Hkv=8, D=128, BS=128, context
 lengths U[1024, 8192], seeded), inputs resident in HBM. Prints ONE JSON line:
 value = algorithmic KV-read GB/s (K+V of valid tokens + Q + out + tables,
-divided by the kernel time), plus µs/step, the roofline of the kernel and the
-CPU baseline (the C restatement of the reference kernels, timed on the host).
+divided by the step time: the main and merge kernels, back to back), plus
+µs/step, the roofline of the main kernel (its time over back-to-back
+launches) and the CPU baseline (the C restatement of the reference kernels,
+timed on the host).
 
     python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--no-other-configs]
 
 The default run also times every other config (cfg1, cfg3-5, cfg2_fp8 and the
 reference's unroll Case1) on the GPU, and reports their main-kernel µs, HBM
-fraction and step µs under "other_configs".
+and MFMA fractions and step µs under "other_configs".
 
 Only one GPU is used; --gpus N with N > 1 exits with a message.
 """
