@@ -636,14 +636,15 @@ def _strided_caches(k, v, layout: str, device):
 
 
 @pytest.mark.parametrize("layout", ["fused_kv", "hnd", "padded"])
-@pytest.mark.parametrize("q_len", [1, 8])
-def test_cache_layouts_through_strides(layout, q_len, device):
+@pytest.mark.parametrize("q_len,dtype", [(1, torch.bfloat16), (8, torch.bfloat16), (1, torch.float16)])
+def test_cache_layouts_through_strides(layout, q_len, dtype, device):
     """The entry takes the caches' block, token and head strides: K and V in
     one fused buffer, head-major blocks and padded rows give the oracle's
-    result on the dense caches, and never read the NaN padding."""
-    print(f"[case] cache layout {layout} q_len={q_len}", flush=True)
+    result on the dense caches, and never read the NaN padding (bf16 and fp16
+    caches)."""
+    print(f"[case] cache layout {layout} q_len={q_len} {dtype}", flush=True)
     case = make_custom_case(batch=3, num_heads=32, kv_heads=8, head_dim=128, block_size=64, q_len=q_len,
-                            causal=q_len > 1, context_lens=[700, 64 + q_len, 1500], seed=963)
+                            causal=q_len > 1, context_lens=[700, 64 + q_len, 1500], seed=963, dtype=dtype)
     kc, vc, _keep = _strided_caches(case.key_cache, case.value_cache, layout, device)
     d = case.to(device)
     out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
