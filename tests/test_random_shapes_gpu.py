@@ -6,7 +6,8 @@ bf16 or fp16, fp32 or input-dtype output), MLA (Dk 576 / Dv 512, block size 32
 or 64, 16–192 heads) or fp8 E4M3FN caches; 1–12 sequences with lengths up to
 4,000 tokens, some empty; 0 (the default), 1, 3, 17, 200 or 2,000 workers.
 Tolerance: the decode tolerance (max-abs 2e-2, rel-L2 1e-3) against the numpy
-oracle, or against the oracle on the dequantised caches for fp8.
+oracle, or against the oracle on the dequantised caches for fp8. The fused
+append entry gets its own seeded sweep.
 """
 
 from __future__ import annotations
@@ -83,3 +84,44 @@ def test_random_shapes_match_the_oracle(seed, device):
         if out_dtype != torch.float32:
             ref = torch.tensor(ref).to(out_dtype).float().numpy()
         assert_close(out.float().cpu().numpy(), np.asarray(ref), what=desc)
+
+
+@pytest.mark.parametrize("seed", [21])
+def test_random_shapes_fused_append(seed, device):
+    """Seeded random shapes through the fused append entry: the caches equal
+    the oracle's append bit for bit, the output equals the plain decode on
+    those caches bit for bit and is within the decode tolerance of the
+    oracle (GQA head dims 16–256 in bf16/fp16, MLA, q_len up to 16)."""
+    from tests.test_append_gpu import new_tokens, oracle_appended, poison_new_rows, run_decode, u16
+
+    rng = random.Random(seed)
+    for i in range(60):
+        mla = rng.random() < 0.15
+        q_len = rng.choice([1, 1, 2, 4, 8, 16])
+        causal = q_len > 1 and rng.random() < 0.8
+        batch = rng.randint(1, 8)
+        if mla:
+            d, bs, hkv, g, dtype = 576, rng.choice([32, 64]), 1, rng.choice([16, 128]), torch.bfloat16
+            q_len = min(q_len, 4)
+        else:
+            d, bs = rng.choice([16, 64, 128, 256]), rng.choice([16, 32, 64, 128])
+            hkv, g = rng.choice([1, 2, 4, 8]), rng.choice([1, 2, 4, 8])
+            dtype = rng.choice([torch.bfloat16, torch.float16])
+        lens = [rng.randint(q_len, rng.choice([q_len + 3, 200, 1500])) for _ in range(batch)]
+        workers = rng.choice([0, 0, 1, 5, 300])
+        desc = (f"#{i} {'mla' if mla else 'gqa'} d={d} bs={bs} hkv={hkv} g={g} q={q_len} causal={causal} "
+                f"lens={lens} {dtype} w={workers}")
+        print(f"[case] append seed {seed} {desc}", flush=True)
+        case = make_custom_case(batch=batch, num_heads=hkv * g, kv_heads=hkv, head_dim=d, block_size=bs,
+                                q_len=q_len, causal=causal, context_lens=lens, seed=seed * 1000 + i, dtype=dtype,
+                                head_dim_v=512 if mla else None, mla=mla)
+        k_new, v_new = new_tokens(case, seed * 1000 + i)
+        appended = oracle_appended(case, k_new, v_new)
+        poison_new_rows(case)
+        got, kc, vc = run_decode(case, device, workers, k_new, v_new)
+        np.testing.assert_array_equal(u16(kc), u16(appended.key_cache))
+        if not mla:
+            np.testing.assert_array_equal(u16(vc), u16(appended.value_cache))
+        plain, _, _ = run_decode(appended, device, workers)
+        np.testing.assert_array_equal(got, plain)
+        assert_close(got, oracle_numpy(appended), what=desc)
