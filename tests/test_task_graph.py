@@ -7,7 +7,8 @@ creator edges, TensorMap overlap lookups for INPUT/INOUT, INOUT retiring a
 covered writer, OUTPUT_EXISTING publishing without lookup, NO_DEP and
 manual_dep skipping the map, explicit dependencies, and write-after-read
 edges when a closed scope's memory is reused. The two example orchestrations
-give the DAGs their reference sources imply.
+give the DAGs their reference sources imply. Seeded random programs check the
+same rules as properties against an element-level model of every buffer.
 """
 
 from __future__ import annotations
@@ -277,3 +278,140 @@ def test_replay_is_graph_mode_only():
         g.reset()
         assert g.replay(b"key") is False
         assert g.replay_count == 0
+
+
+# ---- seeded random programs against an element-level model -----------------------------------------
+#
+# Each program mixes INPUT / INOUT / OUTPUT_EXISTING / OUTPUT arguments over
+# views of several geometries (boxes of the buffer's own layout, flat ranges,
+# strided and transposed views: the latter three are compared by byte range),
+# inside nested scopes whose memory is reused. The model tracks, per element of
+# every buffer, the last task that wrote it. Three properties must hold for
+# every task j:
+#   * every element j reads (INPUT or INOUT) was last written by an ancestor of
+#     j: the creator of a runtime tensor, or the last INOUT / OUTPUT_EXISTING
+#     writer of that element (an INOUT that covers and retires an older writer
+#     depends on it, so the order still holds transitively);
+#   * a runtime tensor placed on memory a closed scope returned has every task
+#     that used the old tensor among its ancestors (write after read on reuse);
+#   * every edge is justified: the target created a tensor j passes, wrote a
+#     byte range j reads or updates, or used the memory j's new tensor reuses.
+
+def _elements(t: ChipTensor) -> np.ndarray:
+    idx = np.array([int(t.start_offset)], dtype=np.int64)
+    for d in range(int(t.ndims)):
+        step = np.arange(int(t.shapes[d]), dtype=np.int64) * int(t.strides[d])
+        idx = (idx[:, None] + step[None, :]).ravel()
+    return idx
+
+
+def _byte_range(t: ChipTensor) -> tuple[int, int]:
+    last = sum((int(t.shapes[d]) - 1) * int(t.strides[d]) for d in range(int(t.ndims)))
+    return 4 * int(t.start_offset), 4 * (int(t.start_offset) + last + 1)
+
+
+def _random_view(rng, base: ChipTensor, external: bool) -> ChipTensor:
+    rows, cols = base.shape
+    kind = int(rng.integers(0, 5 if external else 2))
+    if kind == 0:
+        return base
+    if kind == 1:  # a box of the buffer's own layout
+        h, w = int(rng.integers(1, rows + 1)), int(rng.integers(1, cols + 1))
+        return base.view((h, w), (int(rng.integers(0, rows - h + 1)), int(rng.integers(0, cols - w + 1))))
+    addr, n = base.buffer.addr, rows * cols
+    if kind == 2:  # a flat range (dense, another geometry)
+        k = int(rng.integers(1, n + 1))
+        return ext(addr, (n,)).view((k,), (int(rng.integers(0, n - k + 1)),))
+    if kind == 3:  # every other element (not dense)
+        k = int(rng.integers(1, n // 2 + 1))
+        return ChipTensor.make(addr, (n // 2,), F32, True, strides=(2,)).view((k,), (int(rng.integers(0, n // 2 - k + 1)),))
+    w, h = int(rng.integers(1, cols + 1)), int(rng.integers(1, rows + 1))  # transposed
+    t = ChipTensor.make(addr, (cols, rows), F32, True, strides=(1, cols))
+    return t.view((w, h), (int(rng.integers(0, cols - w + 1)), int(rng.integers(0, rows - h + 1))))
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_random_programs_keep_every_read_after_its_writer(seed):
+    rng = np.random.default_rng(seed)
+    g = TaskGraph("record")
+    externals = [ext(0x1000000 * (i + 1), (8, 16)) for i in range(3)]
+    last = {t.buffer.addr: np.full(8 * 16, -1, dtype=np.int64) for t in externals}  # addr -> last writer
+    hist = {t.buffer.addr: [] for t in externals}  # addr -> [(task, byte range)] of published writes
+    live = {t.buffer.addr: t for t in externals}  # tensors a task may pass
+    users: dict[int, set[int]] = {}  # runtime tensor addr -> tasks that passed it
+    span: dict[int, tuple[int, int]] = {}  # runtime tensor addr -> absolute byte range
+    scopes: list[list[int]] = []
+    freed: list[tuple[int, int, set[int]]] = []
+    anc: list[int] = []  # ancestor bitsets
+    shapes = [(8, 16), (4, 16), (3, 16), (16, 16)]
+    for j in range(400):
+        if rng.random() < 0.08 and len(scopes) < 3:
+            g.scope_begin()
+            scopes.append([])
+        if rng.random() < 0.06 and scopes:
+            g.scope_end()
+            for addr in scopes.pop():
+                freed.append((*span.pop(addr), users.pop(addr)))
+                del live[addr], last[addr], hist[addr]
+        args, roles = CoreTaskArgs(), []
+        pool = list(live.values())
+        for _ in range(int(rng.integers(0, 3))):
+            base = pool[int(rng.integers(0, len(pool)))]
+            v = _random_view(rng, base, base.buffer.addr not in users)
+            args.add_input(v)
+            roles.append(("in", v))
+        for role in ("inout", "existing"):
+            if rng.random() < 0.4:
+                base = pool[int(rng.integers(0, len(pool)))]
+                v = _random_view(rng, base, base.buffer.addr not in users)
+                (args.add_inout if role == "inout" else args.add_output)(v)
+                roles.append((role, v))
+        if not roles or rng.random() < 0.35:
+            args.add_output(TensorCreateInfo(shapes[int(rng.integers(0, len(shapes)))], F32))
+            roles.append(("create", None))
+        made = g.rt_submit_dummy_task(args)
+        assert made.task_id() == j
+        fanin = g.fanin(j)
+        assert all(0 <= i < j for i in fanin), (j, fanin)
+        a = 0
+        for i in fanin:
+            a |= anc[i] | (1 << i)
+        anc.append(a)
+
+        justified = set()
+        for role, v in roles:
+            if role == "create":
+                continue
+            addr = v.buffer.addr
+            if v.owner_task_id != 0xFFFFFFFFFFFFFFFF:
+                justified.add(int(v.owner_task_id))
+            if role in ("in", "inout"):
+                for w in set(last[addr][_elements(v)].tolist()) - {-1}:
+                    assert a >> w & 1, f"seed {seed}: task {j} reads what task {w} wrote; fanin {fanin}"
+                b, e = _byte_range(v)
+                justified.update(w for w, (wb, we) in hist[addr] if wb < e and b < we)
+        created = iter(made.get_ref(i) for i in range(made.size()))
+        for role, v in roles:
+            if role != "create":
+                continue
+            t = next(created)
+            b, e = t.buffer.addr, t.buffer.addr + 4 * int(np.prod(t.shape))
+            for fb, fe, who in [f for f in freed if f[0] < e and b < f[1]]:
+                for u in who:
+                    assert a >> u & 1, f"seed {seed}: task {j} reuses memory task {u} used; fanin {fanin}"
+                justified.update(who)
+                freed.remove((fb, fe, who))
+            live[b], last[b], hist[b], users[b], span[b] = t, np.full(int(np.prod(t.shape)), j), [], {j}, (b, e)
+            if scopes:
+                scopes[-1].append(b)
+        assert set(fanin) <= justified, f"seed {seed}: task {j} has unjustified edges {set(fanin) - justified}"
+        for role, v in roles:
+            if role == "create":
+                continue
+            addr = v.buffer.addr
+            if addr in users:
+                users[addr].add(j)
+            if role in ("inout", "existing"):
+                last[addr][_elements(v)] = j
+                hist[addr].append((j, _byte_range(v)))
+    g.close()
