@@ -16,6 +16,11 @@ The default run also times every other config (cfg1, cfg3-5, cfg2_fp8 and the
 reference's unroll Case1) on the GPU, and reports their main-kernel µs, HBM
 and MFMA fractions and step µs under "other_configs".
 
+The synthetic K and V caches share one allocation laid out by
+kv_cache.alloc_kv_pools (V an odd multiple of 256 bytes from K), the layout
+the library recommends; --kv-layout separate allocates them apart, which
+costs the GQA main kernel 1-4%.
+
 Only one GPU is used; --gpus N with N > 1 exits with a message.
 """
 
@@ -37,6 +42,10 @@ DEFAULT_CONFIG = "cfg2_qwen3_8b"
 # The headline metric, quoted on the default workload; other --config runs
 # carry their workload name after it.
 METRIC = "decode-attn KV-read GB/s & % HBM peak; µs/step at Qwen3-8B shape bs=32"
+KV_LAYOUTS = {
+    "pool": "K and V caches in one allocation, V 256 bytes past K's end rounded to 512 (kv_cache.alloc_kv_pools)",
+    "separate": "K and V caches in two allocations",
+}
 
 
 def parse() -> argparse.Namespace:
@@ -53,6 +62,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--tokens", type=int, default=32768,
                    help="--op kv_append: tokens written per call (32 = one decode step of bs=32)")
     p.add_argument("--workers", type=int, default=0, help="worker wavefronts; 0 = one per wave slot")
+    p.add_argument("--kv-layout", default="pool", choices=["pool", "separate"],
+                   help="pool: K and V caches in one allocation from kv_cache.alloc_kv_pools (V an odd multiple "
+                        "of 256 bytes from K); separate: two allocations")
     p.add_argument("--out-dtype", default="bf16", choices=["bf16", "f32"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-other-configs", action="store_true",
@@ -158,7 +170,7 @@ def other_configs(args, dev, skip: str) -> dict:
         if name == skip:
             continue
         case_cpu = make_case(name)
-        case = case_cpu.to(dev)
+        case = case_cpu.to(dev, kv_pool=args.kv_layout == "pool")
         out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
         tm = time_decode(case, out, args.workers, dev, steps, warmup)
         nbytes = algorithmic_bytes(case_cpu, out_bytes=2 if out_dtype == torch.bfloat16 else 4)
@@ -407,7 +419,7 @@ def bench_decode_prelude(args) -> int:
         print("bench.py: --op decode_prelude times bf16 GQA configs with 128-dim heads", file=sys.stderr)
         return 2
     case_cpu = make_case(cfg)
-    case = case_cpu.to(dev)
+    case = case_cpu.to(dev, kv_pool=args.kv_layout == "pool")
     g = torch.Generator().manual_seed(20261212)
     b, ql, hq, hkv, d = cfg.batch, cfg.q_len, cfg.num_heads, cfg.kv_heads, cfg.head_dim_k
     rn = lambda *shape, std=0.5: (torch.randn(*shape, generator=g) * std).to(dev)  # noqa: E731
@@ -494,7 +506,7 @@ def bench_decode_append(args) -> int:
         print("bench.py: --op decode_append times bf16 GQA configs", file=sys.stderr)
         return 2
     case_cpu = make_case(cfg)
-    case = case_cpu.to(dev)
+    case = case_cpu.to(dev, kv_pool=args.kv_layout == "pool")
     g = torch.Generator().manual_seed(20261211)
     shape = (cfg.batch, cfg.q_len, cfg.kv_heads)
     k_new = torch.randn(*shape, cfg.head_dim_k, generator=g).to(torch.bfloat16).to(dev)
@@ -574,7 +586,7 @@ def bench_taskgraph(args) -> int:
     cfg = CONFIGS[args.config if args.config != DEFAULT_CONFIG else "cfg1_small"]
     dev = torch.device("cuda", 0)
     case_cpu = make_case(cfg)
-    case = case_cpu.to(dev)
+    case = case_cpu.to(dev, kv_pool=args.kv_layout == "pool")
     out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
     out = torch.zeros(case.out_shape(), dtype=out_dtype, device=dev)
     dt = {torch.bfloat16: DataType.BFLOAT16, torch.float32: DataType.FLOAT32, torch.int32: DataType.INT32}
@@ -666,7 +678,7 @@ def main() -> int:
     cfg = variant_config(CONFIGS[args.config], args)
     print(f"[bench] generating {cfg.name}: {cfg.description}", file=sys.stderr, flush=True)
     case_cpu = make_case(cfg)
-    case = case_cpu.to(dev)
+    case = case_cpu.to(dev, kv_pool=args.kv_layout == "pool")
     out_dtype = torch.bfloat16 if args.out_dtype == "bf16" else torch.float32
     out = torch.empty(case.out_shape(), dtype=out_dtype, device=dev)
 
@@ -732,6 +744,7 @@ def main() -> int:
             "context_tokens": int(case_cpu.context_lens.sum()),
             "out_dtype": args.out_dtype,
             "kv_format": "fp8_e4m3fn + fp32 scale per (block, kv head); bf16 MFMA" if case_cpu.fp8 else "bf16",
+            "kv_layout": KV_LAYOUTS[args.kv_layout] if not cfg.mla else "one latent cache; V is its first Dv columns",
             "workers": workers,
             "parallelism": "single GPU",
         },

@@ -92,9 +92,20 @@ class DecodeCase:
     k_scale: torch.Tensor | None = None  # fp8 caches: fp32 [num_blocks, kv_heads]
     v_scale: torch.Tensor | None = None
 
-    def to(self, device) -> "DecodeCase":
-        k = self.key_cache.to(device)
-        v = k[..., : self.config.head_dim_v] if self.config.mla else self.value_cache.to(device)
+    def to(self, device, kv_pool: bool = False) -> "DecodeCase":
+        """The case on ``device``. ``kv_pool``: separate K and V caches share one
+        allocation laid out by ``kv_cache.alloc_kv_pools`` (V an odd multiple of
+        256 bytes from K) instead of two allocations."""
+        if kv_pool and not self.config.mla:
+            from .kv_cache import alloc_kv_pools
+
+            nblk, bs, hkv, dk = self.key_cache.shape
+            k, v = alloc_kv_pools(nblk, bs, hkv, dk, self.key_cache.dtype, device, self.value_cache.shape[3])
+            k.copy_(self.key_cache)
+            v.copy_(self.value_cache)
+        else:
+            k = self.key_cache.to(device)
+            v = k[..., : self.config.head_dim_v] if self.config.mla else self.value_cache.to(device)
         mv = lambda t: None if t is None else t.to(device)  # noqa: E731
         return DecodeCase(self.config, self.seed, self.query.to(device), k, v, self.block_table.to(device),
                           self.context_lens.to(device), self.scale, dict(self.extra), mv(self.k_scale),

@@ -377,3 +377,25 @@ def test_kv_cache_entry_points_validate_on_the_host():
     assert pre() == 0
     for bad in (dict(head_dim=127), dict(q_out=0), dict(max_position=0), dict(eps=-1.0), dict(v_head_stride=0)):
         assert pre(**bad) == -1, bad
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16", "float8_e4m3fn"])
+def test_kv_pools_sit_an_odd_multiple_of_256_bytes_apart(dtype_name):
+    import torch
+
+    from simpler_amd.kv_cache import alloc_kv_pools
+    from simpler_amd.workloads import make_case
+
+    dtype = getattr(torch, dtype_name)
+    for nblk, bs, hkv, dk, dv in ((7, 16, 3, 96, 64), (10, 128, 8, 128, 128), (1, 1, 1, 8, 8)):
+        k, v = alloc_kv_pools(nblk, bs, hkv, dk, dtype, "cpu", head_dim_v=dv)
+        assert k.shape == (nblk, bs, hkv, dk) and v.shape == (nblk, bs, hkv, dv)
+        assert k.is_contiguous() and v.is_contiguous() and k.dtype == v.dtype == dtype
+        gap = v.data_ptr() - k.data_ptr()
+        assert gap >= k.numel() * k.element_size()  # no overlap
+        assert gap % 512 == 256 and gap - k.numel() * k.element_size() < 768
+        assert k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()  # one allocation
+    case = make_case("cfg1_small")
+    pooled = case.to("cpu", kv_pool=True)
+    assert torch.equal(pooled.key_cache, case.key_cache) and torch.equal(pooled.value_cache, case.value_cache)
+    assert (pooled.value_cache.data_ptr() - pooled.key_cache.data_ptr()) % 512 == 256

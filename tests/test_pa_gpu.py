@@ -655,6 +655,31 @@ def test_cache_layouts_through_strides(layout, q_len, dtype, device):
     assert_close(out.cpu().numpy(), oracle_numpy(case), what=f"layout {layout} q{q_len}")
 
 
+@pytest.mark.parametrize("name", ["cfg2_qwen3_8b", "cfg5_verify", "cfg2_fp8", "cfg1_small"])
+def test_pooled_kv_layout_is_bit_identical(name, device):
+    """The benchmark's cache layout (K and V in one allocation from
+    kv_cache.alloc_kv_pools, V an odd multiple of 256 bytes from K) gives the
+    same bits as two separate allocations, at the configs' full sizes; on the
+    small config both also match the oracle."""
+    print(f"[case] pooled kv layout {name}", flush=True)
+    case = make_case(name)
+    outs = []
+    for pool in (False, True):
+        d = case.to(device, kv_pool=pool)
+        gap = d.value_cache.data_ptr() - d.key_cache.data_ptr()
+        assert (gap % 512 == 256) == pool
+        out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+        pa.paged_attention_decode(d.query, d.key_cache, d.value_cache, d.block_table, d.context_lens, out,
+                                  case.scale, causal=case.config.causal, k_scale=d.k_scale, v_scale=d.v_scale)
+        torch.cuda.synchronize(device)
+        pa.check_errors(device)
+        outs.append(out.cpu())
+        del d
+    assert torch.equal(outs[0], outs[1])
+    if name == "cfg1_small":
+        assert_close(outs[1].numpy(), oracle_numpy(case), what="pooled layout")
+
+
 def test_mla_padded_token_rows(device):
     """MLA with the latent cache's token rows padded past 576 elements (NaN in
     the padding): V stays the first 512 dims of the same rows."""
