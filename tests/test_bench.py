@@ -45,6 +45,7 @@ def test_default_line_carries_the_contract(device, capsys, monkeypatch):
     assert line["n_gpus"] == 1 and line["steps"] == 5 and line["warmup"] == 2
     assert line["unit"] == "GB/s" and line["higher_is_better"] is True and line["dtype"] == "bf16"
     assert line["config"]["workload"].startswith("cfg2_qwen3_8b")
+    assert "one allocation" in line["config"]["kv_layout"]  # the default: alloc_kv_pools
     roof = line["roofline"]
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert 0 < roof["frac"] < 1 and abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
