@@ -156,6 +156,41 @@ def test_fused_append_worker_counts_at_qwen3_shape(workers, device):
     np.testing.assert_array_equal(got, plain)
 
 
+@pytest.mark.parametrize("name", ["gqa_d128", "verify_q8", "multi_d64_q8", "fp16_d128"])
+def test_fused_append_into_pooled_caches_stays_in_its_pools(name, device):
+    """K and V pools in one allocation (kv_cache.alloc_kv_pools, the
+    benchmark's layout): the fused append writes exactly the oracle's rows
+    into each pool and nothing into the bytes between them, and the output is
+    the plain decode's on the appended caches, bit for bit."""
+    from simpler_amd.kv_cache import alloc_kv_pools
+
+    print(f"[case] append into pooled caches {name}", flush=True)
+    seed = 900 + sorted(CASES).index(name)
+    case = make_custom_case(seed=seed, **CASES[name])
+    c = case.config
+    k_new, v_new = new_tokens(case, seed + 1)
+    want = oracle_appended(case, k_new, v_new)
+    poison_new_rows(case)
+    nblk, bs, hkv, dk = case.key_cache.shape
+    kc, vc = alloc_kv_pools(nblk, bs, hkv, dk, case.key_cache.dtype, device, case.value_cache.shape[3])
+    buf = torch.empty(0, dtype=kc.dtype, device=device).set_(kc.untyped_storage())
+    buf.fill_(-7.0)  # exact in bf16 and fp16; stays in the gap
+    kc.copy_(case.key_cache)
+    vc.copy_(case.value_cache)
+    d = case.to(device)
+    out = torch.empty(case.out_shape(), dtype=torch.float32, device=device)
+    pa.paged_attention_decode_append(d.query, kc, vc, d.block_table, d.context_lens, k_new.to(device),
+                                     v_new.to(device), out, case.scale, causal=c.causal)
+    torch.cuda.synchronize(device)
+    pa.check_errors(device)
+    np.testing.assert_array_equal(u16(kc.cpu()), u16(want.key_cache))
+    np.testing.assert_array_equal(u16(vc.cpu()), u16(want.value_cache))
+    gap = buf[kc.numel(): vc.storage_offset()]
+    assert gap.numel() > 0 and bool((gap == -7.0).all())
+    plain, _, _ = run_decode(want, device)
+    np.testing.assert_array_equal(out.cpu().numpy(), plain)
+
+
 def test_fused_append_out_of_pool_block_is_reported_and_not_written(device):
     case = make_custom_case(batch=2, num_heads=8, kv_heads=2, head_dim=128, block_size=128,
                             context_lens=[300, 50], seed=960)
