@@ -1759,11 +1759,6 @@ __device__ __forceinline__ void lds_fill16(i32x4_t rsrc, uint32_t voffset, uint3
                  "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory", "m0");
 }
-__device__ __forceinline__ void lds_fill4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc),
-                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-                 : "memory", "m0");
-}
 #pragma clang diagnostic pop
 __device__ __forceinline__ uint32_t lds_addr_of(const char *p) {
     return (uint32_t)(uintptr_t)(const LDS_AS char *)p;
@@ -1780,10 +1775,9 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t num_re
 }
 
 template <int BS, int DK, int DV, typename OutT>
-__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp,
-                                                const int groups, const int b, const int kvh, const int nblk,
-                                                const int blk_begin, const int blk_end, const int slot,
-                                                char *const smem0, char *const smem1, char *const sink) {
+__device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int slice, const int rgrp, const int b,
+                                                const int kvh, const int nblk, const int blk_begin, const int blk_end,
+                                                const int slot, char *const smem0, char *const smem1) {
     using L = MlaLayout<DK>;
     constexpr int RB = L::kRowBytes;
     constexpr int RC = L::kRowChunks;
@@ -1858,18 +1852,7 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
             if ((x * kDivRC) >> 16 != x / RC) return false;
         return true;
     }(), "multiply-shift division by RC");
-    // ---- L2 prefetch two blocks ahead: every 128-byte line of the block's
-    // valid tokens (as one byte range), each touched by one 4-byte load into a
-    // scratch LDS slot, so the block's later fill is an L2 hit. Row group g
-    // of a slice takes lines g, g + groups, ... Lines past the descriptor's
-    // record count (tokens past the context) are not fetched. ----
-    constexpr int LPB = (BS * DK * 2 + 127) / 128;  // lines of a block of dense rows
-    constexpr int NPF = (LPB + 255) / 256;
-    // Every lane issues all NPF loads, so each wave has exactly NPF prefetch
-    // loads outstanding after its block fill: see the barrier below.
-    const uint32_t pf_base = 128u * ((uint32_t)threadIdx.x * groups + rgrp);
-    const uint32_t pf_step = 128u * 256u * groups;
-    // A block's fill (or L2 prefetch) as a buffer descriptor and an LDS
+    // A block's fill as a buffer descriptor and an LDS
     // address, both wave-uniform; its loads are issued one at a time so that
     // those of the next block can be spread over this block's math (issued
     // in a burst, the four waves' loads queue behind each other at the
@@ -1886,16 +1869,15 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         const int phys = blk >= 0 ? phys_of(blk, bad) : 0;
         const int vvalid = (bad || blk < 0) ? 0 : min(BS, ctx - blk * BS);
         return {buffer_rsrc(k_head + (int64_t)phys * P.k_block_stride * 2, (uint32_t)vvalid * tok_b),
-                (uint32_t)__builtin_amdgcn_readfirstlane(dst ? lds_addr_of(dst) + 1024u * wave : lds_addr_of(sink))};
+                (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr_of(dst) + 1024u * wave)};
     };
     // Per-lane offsets: recomputed for every block from two registers. The
     // empty asm hides that they do not change, so the compiler cannot hoist
     // NII offsets out of the block loop into registers it does not have.
-    auto fill_regs = [&](uint32_t &base, uint32_t &cc, uint32_t &pf) {
+    auto fill_regs = [&](uint32_t &base, uint32_t &cc) {
         base = fill_base;
         cc = (uint32_t)c0;
-        pf = pf_base;
-        asm volatile("" : "+v"(base), "+v"(cc), "+v"(pf));
+        asm volatile("" : "+v"(base), "+v"(cc));
     };
     auto fill_one = [&](const Fill &f, int ii, uint32_t base, uint32_t cc) {
         if (NI % 4 == 0 || 4 * ii + wave < NI) {
@@ -1907,7 +1889,6 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
             lds_fill16(f.rsrc, off, f.lds + 4096u * ii);
         }
     };
-    auto prefetch_one = [&](const Fill &f, int pi, uint32_t pf) { lds_fill4(f.rsrc, pf + pi * pf_step, f.lds); };
 
     // O^T accumulators (tile mt: dims 32mt .. 32mt+31 of row j) and the row
     // sum, both in the frame of the latest used block max f.
@@ -1947,13 +1928,11 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
     constexpr int VA = 2;  // PV stages (single MFMAs) the V^T reads run ahead
     constexpr int NPV = NM * PS;  // PV stages
     static_assert(NM % 2 == 0, "PV runs over pairs of O^T tiles");
-    // next: the fill of the next block (its loads spread over the QK
-    // stages), pf: the L2 prefetch of the block after (in the first PV
-    // stages, after every fill load, for the vmcnt accounting below).
-    auto compute = [&](const char *kb, int blk, bool blk_bad, const Fill &next, const Fill &pf) {
+    // next: the fill of the next block (its loads spread over the QK stages).
+    auto compute = [&](const char *kb, int blk, bool blk_bad, const Fill &next) {
         const bool first = (blk == blk_begin);
-        uint32_t fbase, fcc, fpf;
-        fill_regs(fbase, fcc, fpf);
+        uint32_t fbase, fcc;
+        fill_regs(fbase, fcc);
         // ---- QK: stage = one 16-dim k-step over the NT token tiles ----
         f32x16_t s[NT];
 #pragma unroll
@@ -2060,7 +2039,6 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
         for (int q = 0; q < NPV; ++q) {
             const int mt = stage_tile(q), ks = stage_kstep(q);
             const int pair = q / (2 * PS), qi = q % (2 * PS);
-            if (q < NPF) prefetch_one(pf, q, fpf);
             if (q + VA < NPV) load_v(q + VA, vf[(q + VA) % (VA + 1)]);
             if (2 * pair + 2 < NM) {
 #pragma unroll
@@ -2080,55 +2058,47 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
     };
 
     // ---- block loop: wait + barrier, then the math on this block with the
-    // next block's fill and the L2 prefetch of the one after spread over it
-    // (both as loads of nothing where there is no such block) ----
+    // next block's fill spread over it (as loads of nothing where there is no
+    // such block) ----
     // Vector memory ops complete in order. Before the loop, one wait for
     // everything: the Q rows and the first block's fill. It is unconditional
     // so that the compiler knows those loads are complete and inserts no
     // waits for them inside the loop (a wait there would also wait for the
     // next block's fill, which it does not count). At the top of iteration
-    // blk > blk_begin this wave has outstanding: the prefetch of blk, the
-    // fill of blk, then the NPF prefetch loads of blk+1. Waiting for "at most
-    // NPF outstanding" completes the fill and leaves the prefetch in flight.
-    // lgkmcnt(0): this wave's LDS reads of the buffer about to be refilled
-    // are done.
+    // blk > blk_begin this wave's only outstanding loads are the fill of blk:
+    // the wait for all of them completes it. lgkmcnt(0): this wave's LDS
+    // reads of the buffer about to be refilled are done.
+    // (A second stream that touched every 128-byte line of the block two
+    // ahead, so that its fill hit L2, made cfg4 2.5% slower and the 32-token
+    // block shape 7% slower, with one shape of 32 query rows 3% faster.)
     // s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
-    constexpr unsigned kWaitFillOnly = 0x0070u | ((unsigned)NPF & 15u) | (((unsigned)NPF >> 4) << 14);
     constexpr unsigned kWaitAll = 0x0070u;  // vmcnt(0) expcnt(7) lgkmcnt(0)
-    static_assert(NPF < 64, "vmcnt range");
     bool bad_cur = false, any_bad = false;
     {
         const Fill f0 = fill_of(blk_begin, smem0, bad_cur);
-        uint32_t fbase, fcc, fpf;
-        fill_regs(fbase, fcc, fpf);
+        uint32_t fbase, fcc;
+        fill_regs(fbase, fcc);
 #pragma unroll
         for (int ii = 0; ii < NII; ++ii) fill_one(f0, ii, fbase, fcc);
         __builtin_amdgcn_s_waitcnt(kWaitAll);
-        bool unused = false;
-        const Fill f1 = fill_of(blk_begin + 1 < blk_end ? blk_begin + 1 : -1, nullptr, unused);
-#pragma unroll
-        for (int pi = 0; pi < NPF; ++pi) prefetch_one(f1, pi, fpf);
     }
     for (int blk = blk_begin; blk < blk_end; ++blk) {
         const bool even = ((blk - blk_begin) & 1) == 0;
         __builtin_amdgcn_sched_barrier(0);
-        if (blk > blk_begin) __builtin_amdgcn_s_waitcnt(kWaitFillOnly);
+        if (blk > blk_begin) __builtin_amdgcn_s_waitcnt(kWaitAll);
         __builtin_amdgcn_s_barrier();  // every wave's fill landed; the other buffer is free
         __builtin_amdgcn_sched_barrier(0);
-        bool bad_next = false, unused = false;
+        bool bad_next = false;
         // the buffer not read by this block takes the next one (or zeros)
         const Fill next = fill_of(blk + 1 < blk_end ? blk + 1 : -1, even ? smem1 : smem0, bad_next);
-        const Fill pf = fill_of(blk + 2 < blk_end ? blk + 2 : -1, nullptr, unused);
         any_bad |= bad_cur;
         if (active) {
-            compute(even ? smem0 : smem1, blk, bad_cur, next, pf);
+            compute(even ? smem0 : smem1, blk, bad_cur, next);
         } else {  // no rows: the loads only
-            uint32_t fbase, fcc, fpf;
-            fill_regs(fbase, fcc, fpf);
+            uint32_t fbase, fcc;
+            fill_regs(fbase, fcc);
 #pragma unroll
             for (int ii = 0; ii < NII; ++ii) fill_one(next, ii, fbase, fcc);
-#pragma unroll
-            for (int pi = 0; pi < NPF; ++pi) prefetch_one(pf, pi, fpf);
         }
         bad_cur = bad_next;
     }
@@ -2177,7 +2147,6 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     using L = MlaLayout<DK>;
     __shared__ __attribute__((aligned(16))) char smem0[BS * L::kRowBytes];
     __shared__ __attribute__((aligned(16))) char smem1[BS * L::kRowBytes];
-    __shared__ __attribute__((aligned(16))) char sink[256];  // target of the L2 prefetch loads
     flag_bad_lengths(P);
     const int groups = (P.rows + kMlaRowsPerGroup - 1) / kMlaRowsPerGroup;
     int slice = 0, rgrp = 0;
@@ -2202,8 +2171,7 @@ __global__ void __launch_bounds__(256) pa_mla_kernel(const KernelParams P) {
     while (nb > 0) {
         const int blk0 = max(0, start - t0 - P.seg_cost), blk1 = min(nb, end - t0 - P.seg_cost);
         if (blk1 > blk0) {
-            run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, groups, b, kvh, nb, blk0, blk1, slot, smem0, smem1,
-                                              sink);
+            run_mla_segment<BS, DK, DV, OutT>(P, slice, rgrp, b, kvh, nb, blk0, blk1, slot, smem0, smem1);
             slot = 1;
         }
         t0 += nb + P.seg_cost;
