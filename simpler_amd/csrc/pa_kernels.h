@@ -1663,10 +1663,9 @@ pa_merge_kernel(const KernelParams P) {
 // 32 rows per wave), so with 128 query heads each KV block of a work slice
 // is fetched from HBM into LDS once, by one compute unit. Blocks are copied
 // with direct global->LDS loads (double buffered: the next block is in flight
-// during the math on this one), plus an L2 prefetch two blocks ahead. Each
-// wave runs its 32 rows end to end; Q (Dk/16 operand quads) and O^T (Dv x 32
-// rows, fp32) stay in its registers, and the waves share only the block
-// buffers.
+// during the math on this one). Each wave runs its 32 rows end to end; Q
+// (Dk/16 operand quads) and O^T (Dv x 32 rows, fp32) stay in its registers,
+// and the waves share only the block buffers.
 //   QK  S^T[token][row] = K[token][:] . Q[row][:]   MFMA 32x32x16 bf16,
 //       A = K rows from LDS (16-B reads), B = Q registers. C: lane l holds
 //       row l%32 and, in register 4a+e, token 8a+4h+e of the 32-token tile
@@ -1712,14 +1711,6 @@ __device__ __forceinline__ f32x16_t mma_32x32x16(const u32x4_t a, const u32x4_t 
 // The two bf16 values of a packed word, summed in fp32.
 __device__ __forceinline__ float bf16_pair_sum(const unsigned w) {
     return __uint_as_float(w << 16) + __uint_as_float(w & 0xffff0000u);
-}
-
-// Workgroup barrier that orders LDS accesses only: the block fill and L2
-// prefetch loads in flight are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Work slice and row group of workgroup w. Row groups of a slice are
@@ -1816,7 +1807,7 @@ __device__ __forceinline__ void run_mla_segment(const KernelParams &P, const int
 
     // Block-table entries are read through the scalar cache (constant
     // address space): the load is counted by lgkmcnt, so waiting for it never
-    // waits for the vector-memory loads in flight (block fill, L2 prefetch).
+    // waits for the vector-memory loads in flight (the block fill).
     const __attribute__((address_space(4))) int32_t *bt_row =
         (const __attribute__((address_space(4))) int32_t *)(P.block_table + (int64_t)b * P.max_blocks);
     auto phys_of = [&](int blk, bool &bad) -> int {
