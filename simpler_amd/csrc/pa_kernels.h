@@ -1708,11 +1708,6 @@ __device__ __forceinline__ f32x16_t mma_32x32x16(const u32x4_t a, const u32x4_t 
                                                    c, 0, 0, 0);
 }
 
-// The two bf16 values of a packed word, summed in fp32.
-__device__ __forceinline__ float bf16_pair_sum(const unsigned w) {
-    return __uint_as_float(w << 16) + __uint_as_float(w & 0xffff0000u);
-}
-
 // Work slice and row group of workgroup w. Row groups of a slice are
 // w, w+8, w+16, ...: the same XCD under round-robin workgroup dispatch.
 __device__ __forceinline__ void mla_worker(int w, int slices, int groups, int *slice, int *group) {
