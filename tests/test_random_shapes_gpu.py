@@ -4,7 +4,8 @@ Each case draws a valid configuration: GQA (head dim 16–256, block size
 16–128, 1–8 kv heads, group 1–16, q_len 1–8 with or without the causal mask,
 bf16 or fp16, fp32 or input-dtype output), MLA (Dk 576 / Dv 512, block size 32
 or 64, 16–192 heads) or fp8 E4M3FN caches; 1–12 sequences with lengths up to
-4,000 tokens, some empty; 0 (the default), 1, 3, 17, 200 or 2,000 workers.
+4,000 tokens, some empty; 0 (the default), 1, 3, 17, 200 or 2,000 workers;
+every other case with K and V in one allocation (kv_cache.alloc_kv_pools).
 Tolerance: the decode tolerance (max-abs 2e-2, rel-L2 1e-3) against the numpy
 oracle, or against the oracle on the dequantised caches for fp8. The fused
 append entry gets its own seeded sweep.
@@ -73,7 +74,7 @@ def test_random_shapes_match_the_oracle(seed, device):
                                             case.context_lens.numpy(), case.scale, causal=causal)
         else:
             ref = oracle_numpy(case)
-        dc = case.to(device)
+        dc = case.to(device, kv_pool=i % 2 == 1)  # every other case: K and V in one allocation
         if kind == "fp8":
             kw = dict(k_scale=dc.k_scale, v_scale=dc.v_scale)
         out = torch.empty(case.out_shape(), dtype=out_dtype, device=device)
